@@ -1,0 +1,19 @@
+"""MI355X (gfx950) group-quantized linear path: host side of libdgm_amd.so.
+
+The directory name is not a Python identifier, so load it with
+    importlib.util.spec_from_file_location("dgm_amd", ".../__init__.py",
+        submodule_search_locations=[".../diffusion-gpt-metal_amd"])
+(see load_package() in tests/conftest.py and bench.py).
+"""
+from .abi import (DGM_ERR_ARG, DGM_ERR_BITS, DGM_ERR_HIP, DGM_ERR_NOT_BEGUN,
+                  DGM_ERR_SHAPE, DGM_ERR_UNSUPPORTED, DGM_MATH_BF16,
+                  DGM_MATH_FP32, DGM_OK, HEADER, LIB_PATH, PROTOTYPES,
+                  DgmError, GemmP, QuantP, load_library)
+from .gpu import GPU, Buf, RawBuf
+
+__all__ = [
+    "GPU", "Buf", "RawBuf", "GemmP", "QuantP", "DgmError", "load_library",
+    "LIB_PATH", "HEADER", "PROTOTYPES", "DGM_OK", "DGM_ERR_ARG", "DGM_ERR_SHAPE",
+    "DGM_ERR_NOT_BEGUN", "DGM_ERR_HIP", "DGM_ERR_BITS", "DGM_ERR_UNSUPPORTED",
+    "DGM_MATH_FP32", "DGM_MATH_BF16",
+]

@@ -1,0 +1,106 @@
+"""ctypes binding of include/dgm_quant.h (libdgm_amd.so).
+
+Only plumbing: prototypes, the two parameter-block structs and the status
+codes. The HIP library is required; there is no fallback of any kind, and a
+missing library raises at load time.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdgm_amd.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "dgm_quant.h")
+
+DGM_OK = 0
+DGM_ERR_ARG = 1
+DGM_ERR_SHAPE = 2
+DGM_ERR_NOT_BEGUN = 3
+DGM_ERR_HIP = 4
+DGM_ERR_BITS = 5
+DGM_ERR_UNSUPPORTED = 6
+
+DGM_MATH_FP32 = 0
+DGM_MATH_BF16 = 1
+
+
+class GemmP(ctypes.Structure):
+    """src/Params.swift:7-16 — eight u32, 32 bytes."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("M", "N", "K", "hasBias", "qGroup", "pad0", "pad1", "pad2")]
+
+
+class QuantP(ctypes.Structure):
+    """src/Params.swift:18-23 — rows, cols, qmax (f32), qGroup; 16 bytes."""
+    _fields_ = [("rows", ctypes.c_uint32), ("cols", ctypes.c_uint32),
+                ("qmax", ctypes.c_float), ("qGroup", ctypes.c_uint32)]
+
+
+assert ctypes.sizeof(GemmP) == 32 and ctypes.sizeof(QuantP) == 16
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_GP = ctypes.POINTER(GemmP)
+_QP = ctypes.POINTER(QuantP)
+
+# name -> (restype, argtypes); every function of include/dgm_quant.h.
+PROTOTYPES = {
+    "dgm_gpu_create": (_I, [ctypes.POINTER(_P)]),
+    "dgm_gpu_destroy": (None, [_P]),
+    "dgm_gpu_set_stream": (_I, [_P, _P]),
+    "dgm_gpu_stream": (_P, [_P]),
+    "dgm_set_math": (_I, [_P, _I]),
+    "dgm_get_math": (_I, [_P]),
+    "dgm_begin": (_I, [_P]),
+    "dgm_end": (_I, [_P]),
+    "dgm_last_kernel": (ctypes.c_char_p, [_P]),
+    "dgm_last_error": (ctypes.c_char_p, [_P]),
+    "dgm_quant_i8": (_I, [_P, _P, _P, _P, _QP]),
+    "dgm_quant_i4": (_I, [_P, _P, _P, _P, _QP]),
+    "dgm_gemm_nt_f32": (_I, [_P, _P, _P, _P, _P, _GP]),
+    "dgm_gemm_nt_i8": (_I, [_P, _P, _P, _P, _P, _P, _GP]),
+    "dgm_gemm_nt_i4": (_I, [_P, _P, _P, _P, _P, _P, _GP]),
+    "dgm_gemm_dx_f32": (_I, [_P, _P, _P, _P, _GP]),
+    "dgm_gemm_dx_i8": (_I, [_P, _P, _P, _P, _P, _GP]),
+    "dgm_gemm_dx_i4": (_I, [_P, _P, _P, _P, _P, _GP]),
+    "dgm_gemm_dw": (_I, [_P, _P, _P, _P, _GP]),
+    "dgm_gemm_dw_acc": (_I, [_P, _P, _P, _P, _GP]),
+    "dgm_quantize": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_gemmNT": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_gemmDX": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_gemmDW": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "dgm_gemmDWAcc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+}
+
+
+class DgmError(RuntimeError):
+    """A nonzero status from the C ABI (the reference's fatalError/exit path)."""
+
+    def __init__(self, code: int, message: str, kernel: str = ""):
+        super().__init__(f"dgm status {code} ({kernel}): {message}")
+        self.code = code
+        self.message = message
+        self.kernel = kernel
+
+
+_LIB = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads libdgm_amd.so and installs prototypes. Raises if it is not built."""
+    global _LIB
+    if _LIB is not None and path == LIB_PATH:
+        return _LIB
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is not built; run python diffusion-gpt-metal_amd/build.py "
+            "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path == LIB_PATH:
+        _LIB = lib
+    return lib

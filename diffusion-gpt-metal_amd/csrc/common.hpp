@@ -1,0 +1,61 @@
+// Internal helpers shared by the HIP translation units of libdgm_amd.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/dgm_quant.h"
+
+// Context behind the opaque dgm_gpu handle (mirrors class GPU, src/GPU.swift:91-198).
+struct dgm_gpu {
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    bool begun = false;
+    int math = DGM_MATH_FP32;
+    int first_err = DGM_OK;           // first error since begin()
+    char last_kernel[64] = {0};
+    char err_msg[320] = {0};
+    // Grow-only device workspace for staging (bf16 activations, split-K
+    // partials). Owned by the context, freed in dgm_gpu_destroy.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+namespace dgm {
+
+// Records an error on the context (keeps the first one of the region) and
+// returns the code so call sites can `return fail(...)`.
+int fail(dgm_gpu* g, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+
+// Marks `name` as the last dispatched kernel (GPU.lastKernel) and checks that
+// a begin()/end() region is open.
+int enter(dgm_gpu* g, const char* name);
+
+// Checks hipGetLastError() after a launch.
+int check_launch(dgm_gpu* g, const char* name);
+
+// Ensures the context workspace holds at least `bytes`; returns nullptr on
+// allocation failure (error recorded).
+void* workspace(dgm_gpu* g, size_t bytes);
+
+constexpr int64_t kMaxIndex = (int64_t(1) << 31) - 1;
+
+inline bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+inline unsigned ceil_div(int64_t a, int64_t b) { return unsigned((a + b - 1) / b); }
+
+}  // namespace dgm
+
+#define DGM_LAUNCH_CHECK(g, name)                         \
+    do {                                                  \
+        int _rc = ::dgm::check_launch((g), (name));       \
+        if (_rc != DGM_OK) return _rc;                    \
+    } while (0)

@@ -1,0 +1,155 @@
+// C-ABI entry points of the GEMM family and the GPU.swift-style wrappers
+// (src/GPU.swift:227-272). Validates the reference's preconditions, then picks
+// the kernel: fp32 MFMA tiles (default), the fp32 GEMV for M <= 4 quantized
+// forwards, or the bf16 MFMA kernels when the context's math mode is BF16.
+#include "common.hpp"
+
+namespace dgm {
+int gemm_check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits);
+int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
+                 const float* bias, float* Y, const dgm_GemmP* p);
+int gemm_f32_dx(dgm_gpu* g, int bits, const void* W, const float* scale, const float* dY,
+                float* dX, const dgm_GemmP* p);
+int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dgm_GemmP* p,
+                bool accumulate);
+}  // namespace dgm
+
+namespace {
+
+int gemm_nt(dgm_gpu* g, const char* name, int bits, const void* W, const float* scale,
+            const float* X, const float* bias, float* Y, const dgm_GemmP* p) {
+    int rc = dgm::enter(g, name);
+    if (rc) return rc;
+    rc = dgm::gemm_check_sizes(g, name, p, bits);
+    if (rc) return rc;
+    if (p->M == 0 || p->N == 0) return DGM_OK;
+    if (!Y || (p->K > 0 && (!W || !X)) || (bits != 32 && p->K > 0 && !scale) ||
+        (p->hasBias && !bias))
+        return dgm::fail(g, DGM_ERR_ARG, "%s: null buffer", name);
+    rc = dgm::gemm_f32_fwd(g, bits, W, scale, X, bias, Y, p);
+    if (rc) return rc;
+    DGM_LAUNCH_CHECK(g, name);
+    return DGM_OK;
+}
+
+int gemm_dx(dgm_gpu* g, const char* name, int bits, const void* W, const float* scale,
+            const float* dY, float* dX, const dgm_GemmP* p) {
+    int rc = dgm::enter(g, name);
+    if (rc) return rc;
+    rc = dgm::gemm_check_sizes(g, name, p, bits);
+    if (rc) return rc;
+    if (p->M == 0 || p->K == 0) return DGM_OK;
+    if (!dX || (p->N > 0 && (!W || !dY)) || (bits != 32 && p->N > 0 && !scale))
+        return dgm::fail(g, DGM_ERR_ARG, "%s: null buffer", name);
+    rc = dgm::gemm_f32_dx(g, bits, W, scale, dY, dX, p);
+    if (rc) return rc;
+    DGM_LAUNCH_CHECK(g, name);
+    return DGM_OK;
+}
+
+int gemm_dw(dgm_gpu* g, const char* name, const float* dY, const float* X, float* dW,
+            const dgm_GemmP* p, bool accumulate) {
+    int rc = dgm::enter(g, name);
+    if (rc) return rc;
+    rc = dgm::gemm_check_sizes(g, name, p, 32);
+    if (rc) return rc;
+    if (p->N == 0 || p->K == 0) return DGM_OK;
+    if (!dW || (p->M > 0 && (!dY || !X))) return dgm::fail(g, DGM_ERR_ARG, "%s: null buffer", name);
+    rc = dgm::gemm_f32_dw(g, dY, X, dW, p, accumulate);
+    if (rc) return rc;
+    DGM_LAUNCH_CHECK(g, name);
+    return DGM_OK;
+}
+
+int make_p(dgm_gpu* g, const char* name, int64_t M, int64_t N, int64_t K, int hasBias,
+           int64_t qGroup, dgm_GemmP* p) {
+    if (M < 0 || N < 0 || K < 0 || M > dgm::kMaxIndex || N > dgm::kMaxIndex || K > dgm::kMaxIndex ||
+        qGroup < 0 || qGroup > dgm::kMaxIndex)
+        return dgm::fail(g, DGM_ERR_ARG, "%s: bad sizes M=%lld N=%lld K=%lld group=%lld", name,
+                         (long long)M, (long long)N, (long long)K, (long long)qGroup);
+    *p = dgm_GemmP{uint32_t(M), uint32_t(N), uint32_t(K), uint32_t(hasBias), uint32_t(qGroup), 0, 0, 0};
+    return DGM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dgm_gemm_nt_f32(dgm_gpu* g, const float* W, const float* X, const float* bias, float* Y,
+                    const dgm_GemmP* p) {
+    return gemm_nt(g, "gemm_nt_f32", 32, W, nullptr, X, bias, Y, p);
+}
+int dgm_gemm_nt_i8(dgm_gpu* g, const int8_t* W, const float* scale, const float* X,
+                   const float* bias, float* Y, const dgm_GemmP* p) {
+    return gemm_nt(g, "gemm_nt_i8", 8, W, scale, X, bias, Y, p);
+}
+int dgm_gemm_nt_i4(dgm_gpu* g, const uint8_t* W, const float* scale, const float* X,
+                   const float* bias, float* Y, const dgm_GemmP* p) {
+    return gemm_nt(g, "gemm_nt_i4", 4, W, scale, X, bias, Y, p);
+}
+int dgm_gemm_dx_f32(dgm_gpu* g, const float* W, const float* dY, float* dX, const dgm_GemmP* p) {
+    return gemm_dx(g, "gemm_dx_f32", 32, W, nullptr, dY, dX, p);
+}
+int dgm_gemm_dx_i8(dgm_gpu* g, const int8_t* W, const float* scale, const float* dY, float* dX,
+                   const dgm_GemmP* p) {
+    return gemm_dx(g, "gemm_dx_i8", 8, W, scale, dY, dX, p);
+}
+int dgm_gemm_dx_i4(dgm_gpu* g, const uint8_t* W, const float* scale, const float* dY, float* dX,
+                   const dgm_GemmP* p) {
+    return gemm_dx(g, "gemm_dx_i4", 4, W, scale, dY, dX, p);
+}
+int dgm_gemm_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dgm_GemmP* p) {
+    return gemm_dw(g, "gemm_dw", dY, X, dW, p, false);
+}
+int dgm_gemm_dw_acc(dgm_gpu* g, const float* dY, const float* X, float* dW, const dgm_GemmP* p) {
+    return gemm_dw(g, "gemm_dw_acc", dY, X, dW, p, true);
+}
+
+int dgm_gemmNT(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale,
+               const float* x, const float* bias, float* y, int64_t M, int64_t N, int64_t K,
+               int64_t qGroup) {
+    if (!g) return DGM_ERR_ARG;
+    dgm_GemmP p;
+    int rc = make_p(g, "gemmNT", M, N, K, bias ? 1 : 0, qGroup, &p);
+    if (rc) return rc;
+    switch (bits) {
+        case 32: return dgm_gemm_nt_f32(g, w, x, bias, y, &p);
+        case 8: return dgm_gemm_nt_i8(g, static_cast<const int8_t*>(q), scale, x, bias, y, &p);
+        case 4: return dgm_gemm_nt_i4(g, static_cast<const uint8_t*>(q), scale, x, bias, y, &p);
+        default: return dgm::fail(g, DGM_ERR_BITS, "gemmNT: unsupported bits %lld", (long long)bits);
+    }
+}
+
+int dgm_gemmDX(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale,
+               const float* dy, float* dx, int64_t M, int64_t N, int64_t K, int64_t qGroup) {
+    if (!g) return DGM_ERR_ARG;
+    dgm_GemmP p;
+    int rc = make_p(g, "gemmDX", M, N, K, 0, qGroup, &p);
+    if (rc) return rc;
+    switch (bits) {
+        case 32: return dgm_gemm_dx_f32(g, w, dy, dx, &p);
+        case 8: return dgm_gemm_dx_i8(g, static_cast<const int8_t*>(q), scale, dy, dx, &p);
+        case 4: return dgm_gemm_dx_i4(g, static_cast<const uint8_t*>(q), scale, dy, dx, &p);
+        default: return dgm::fail(g, DGM_ERR_BITS, "gemmDX: unsupported bits %lld", (long long)bits);
+    }
+}
+
+int dgm_gemmDW(dgm_gpu* g, const float* dy, const float* x, float* dw, int64_t M, int64_t N,
+               int64_t K) {
+    if (!g) return DGM_ERR_ARG;
+    dgm_GemmP p;
+    int rc = make_p(g, "gemmDW", M, N, K, 0, 8, &p);   // defaultQGroup, unused (GPU.swift:263)
+    if (rc) return rc;
+    return dgm_gemm_dw(g, dy, x, dw, &p);
+}
+
+int dgm_gemmDWAcc(dgm_gpu* g, const float* dy, const float* x, float* dw, int64_t M, int64_t N,
+                  int64_t K) {
+    if (!g) return DGM_ERR_ARG;
+    dgm_GemmP p;
+    int rc = make_p(g, "gemmDWAcc", M, N, K, 0, 8, &p);
+    if (rc) return rc;
+    return dgm_gemm_dw_acc(g, dy, x, dw, &p);
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+"""Python mirror of the reference's GPU class (src/GPU.swift:91-272) over the C ABI.
+
+Same method names and argument meaning as the Swift wrappers (quantize,
+gemmNT, gemmDX, gemmDW, gemmDWAcc, begin, end, lastKernel) plus the
+kernel-level entries (quant_i8 ... gemm_dw_acc) in the buffer slot order of
+metal/kernels.metal. Buffers are device tensors (torch is used only to hold
+device memory) or raw device addresses. A nonzero status raises DgmError,
+where the reference calls fatalError / exit(1).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Optional
+
+from .abi import (DGM_MATH_BF16, DGM_MATH_FP32, DgmError, GemmP, QuantP,
+                  load_library)
+
+
+def _ptr(t: Any) -> Optional[int]:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        if hasattr(t, "is_cuda") and not t.is_cuda:
+            raise ValueError("buffers must live in device memory")
+        return t.data_ptr()
+    raise TypeError(f"cannot take a device address of {type(t).__name__}")
+
+
+def Buf(count: int, device: str = "cuda"):
+    """src/GPU.swift:31-55: zero-filled fp32 buffer of max(count, 1) floats."""
+    import torch
+    return torch.zeros(max(count, 1), dtype=torch.float32, device=device)
+
+
+def RawBuf(nbytes: int, device: str = "cuda"):
+    """src/GPU.swift:57-68: zero-filled byte buffer of max(bytes, 16)."""
+    import torch
+    return torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+class GPU:
+    """One context = one HIP stream, in-order dispatch (src/GPU.swift:91-198)."""
+
+    def __init__(self, stream: Any = None, lib: Optional[ctypes.CDLL] = None):
+        self.lib = lib or load_library()
+        h = ctypes.c_void_p()
+        rc = self.lib.dgm_gpu_create(ctypes.byref(h))
+        if rc != 0:
+            raise DgmError(rc, "dgm_gpu_create failed (no HIP device?)")
+        self.h = h
+        if stream is not None:
+            self.set_stream(stream)
+
+    # -- lifecycle -----------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.dgm_gpu_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream: Any) -> None:
+        """Accepts a torch.cuda.Stream, a raw hipStream_t address or None."""
+        raw = getattr(stream, "cuda_stream", stream)
+        self._check(self.lib.dgm_gpu_set_stream(self.h, raw))
+
+    @property
+    def stream(self) -> int:
+        return self.lib.dgm_gpu_stream(self.h) or 0
+
+    def set_math(self, mode: int) -> None:
+        self._check(self.lib.dgm_set_math(self.h, mode))
+
+    @property
+    def math(self) -> int:
+        return self.lib.dgm_get_math(self.h)
+
+    @property
+    def lastKernel(self) -> str:
+        return self.lib.dgm_last_kernel(self.h).decode()
+
+    @property
+    def lastError(self) -> str:
+        return self.lib.dgm_last_error(self.h).decode()
+
+    def _check(self, rc: int) -> None:
+        if rc != 0:
+            raise DgmError(rc, self.lastError, self.lastKernel)
+
+    # -- dispatch region (src/GPU.swift:158-180) ------------------------------
+    def begin(self) -> None:
+        self._check(self.lib.dgm_begin(self.h))
+
+    def end(self) -> None:
+        self._check(self.lib.dgm_end(self.h))
+
+    # -- host call surface (src/GPU.swift:220-272) ----------------------------
+    def quantize(self, w, q, scale, rows: int, cols: int, bits: int, qGroup: int) -> None:
+        self._check(self.lib.dgm_quantize(self.h, _ptr(w), _ptr(q), _ptr(scale), rows, cols, bits, qGroup))
+
+    def gemmNT(self, bits: int, w, q, scale, x, bias, y, M: int, N: int, K: int, qGroup: int) -> None:
+        self._check(self.lib.dgm_gemmNT(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(x),
+                                        _ptr(bias), _ptr(y), M, N, K, qGroup))
+
+    def gemmDX(self, bits: int, w, q, scale, dy, dx, M: int, N: int, K: int, qGroup: int) -> None:
+        self._check(self.lib.dgm_gemmDX(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(dy),
+                                        _ptr(dx), M, N, K, qGroup))
+
+    def gemmDW(self, dy, x, dw, M: int, N: int, K: int) -> None:
+        self._check(self.lib.dgm_gemmDW(self.h, _ptr(dy), _ptr(x), _ptr(dw), M, N, K))
+
+    def gemmDWAcc(self, dy, x, dw, M: int, N: int, K: int) -> None:
+        self._check(self.lib.dgm_gemmDWAcc(self.h, _ptr(dy), _ptr(x), _ptr(dw), M, N, K))
+
+    # -- kernel-level entries (metal/kernels.metal slot order) ----------------
+    def quant_i8(self, W, Q, scale, p: QuantP) -> None:
+        self._check(self.lib.dgm_quant_i8(self.h, _ptr(W), _ptr(Q), _ptr(scale), ctypes.byref(p)))
+
+    def quant_i4(self, W, Q, scale, p: QuantP) -> None:
+        self._check(self.lib.dgm_quant_i4(self.h, _ptr(W), _ptr(Q), _ptr(scale), ctypes.byref(p)))
+
+    def gemm_nt_f32(self, W, X, bias, Y, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_nt_f32(self.h, _ptr(W), _ptr(X), _ptr(bias), _ptr(Y), ctypes.byref(p)))
+
+    def gemm_nt_i8(self, W, scale, X, bias, Y, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_nt_i8(self.h, _ptr(W), _ptr(scale), _ptr(X), _ptr(bias), _ptr(Y),
+                                            ctypes.byref(p)))
+
+    def gemm_nt_i4(self, W, scale, X, bias, Y, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_nt_i4(self.h, _ptr(W), _ptr(scale), _ptr(X), _ptr(bias), _ptr(Y),
+                                            ctypes.byref(p)))
+
+    def gemm_dx_f32(self, W, dY, dX, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_dx_f32(self.h, _ptr(W), _ptr(dY), _ptr(dX), ctypes.byref(p)))
+
+    def gemm_dx_i8(self, W, scale, dY, dX, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_dx_i8(self.h, _ptr(W), _ptr(scale), _ptr(dY), _ptr(dX), ctypes.byref(p)))
+
+    def gemm_dx_i4(self, W, scale, dY, dX, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_dx_i4(self.h, _ptr(W), _ptr(scale), _ptr(dY), _ptr(dX), ctypes.byref(p)))
+
+    def gemm_dw(self, dY, X, dW, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_dw(self.h, _ptr(dY), _ptr(X), _ptr(dW), ctypes.byref(p)))
+
+    def gemm_dw_acc(self, dY, X, dW, p: GemmP) -> None:
+        self._check(self.lib.dgm_gemm_dw_acc(self.h, _ptr(dY), _ptr(X), _ptr(dW), ctypes.byref(p)))
+
+
+__all__ = ["GPU", "Buf", "RawBuf", "DGM_MATH_FP32", "DGM_MATH_BF16"]

@@ -1,0 +1,155 @@
+/*
+ * dgm_quant.h — C ABI of the MI355X (gfx950) group-quantized linear path.
+ *
+ * Drop-in for the reference's quantize / group-quant GEMM / STE backward
+ * dispatch surface (githubpradeep/diffusion-gpt-metal, paths relative to the
+ * reference root). Plain pointers and sizes only: every buffer is device
+ * memory owned by the caller, nothing here allocates caller-visible memory,
+ * and every call returns an int status (0 = DGM_OK).
+ *
+ * Layouts are the reference's, unchanged:
+ *   W   fp32 master weights [N, K] row-major (output rows x input cols)
+ *   Q8  int8 codes [N*K], one byte per weight, codes in [-127, 127]
+ *   Q4  int4 codes [N*K/2] bytes, two signed nibbles per byte, even k in the
+ *       low nibble, codes in [-7, 7]
+ *   S   fp32 scales [N, K/G] row-major, one per (row, group of G along K)
+ *   X [M,K], Y [M,N], dY [M,N], dX [M,K], dW [N,K]: fp32 row-major
+ *
+ * Ordering: one HIP stream per context. Calls are enqueued in issue order
+ * (the reference puts a full buffer barrier between dispatches,
+ * src/GPU.swift:182-198, which an in-order stream already gives).
+ */
+#ifndef DGM_QUANT_H
+#define DGM_QUANT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define DGM_OK              0
+#define DGM_ERR_ARG         1   /* null pointer / negative size / bad enum     */
+#define DGM_ERR_SHAPE       2   /* a reference precondition failed, e.g.
+                                   K % qGroup != 0 (src/GPU.swift:229,247) or
+                                   odd group for int4 (src/Params.swift:171)  */
+#define DGM_ERR_NOT_BEGUN   3   /* dispatch outside begin()/end()
+                                   (src/GPU.swift:183)                        */
+#define DGM_ERR_HIP         4   /* HIP launch or execution error              */
+#define DGM_ERR_BITS        5   /* bits not in {32, 8, 4} (src/GPU.swift:241) */
+#define DGM_ERR_UNSUPPORTED 6   /* size beyond what a kernel indexes (2^31)   */
+
+/* ---- math modes (dgm_set_math) ------------------------------------------ */
+/* FP32: every GEMM accumulates fp32 products of fp32 operands, like the
+ * reference kernels; max relative error vs float64 <= 1e-5.
+ * BF16: the quantized forward (gemm_nt_i8 / gemm_nt_i4) with M >= 2 runs on
+ * bf16 MFMA (activations rounded to bf16; int8/int4 codes are exact in bf16;
+ * fp32 accumulate, fp32 group scale); max relative error <= 1e-2. M == 1
+ * stays on the fp32 GEMV. Backward kernels are fp32 in both modes. */
+#define DGM_MATH_FP32 0
+#define DGM_MATH_BF16 1
+
+/* ---- parameter blocks: src/Params.swift:7-23, metal/kernels.metal:22-29 -- */
+typedef struct dgm_GemmP {
+    uint32_t M, N, K, hasBias, qGroup, pad0, pad1, pad2;
+} dgm_GemmP;                                   /* 32 bytes (src/GPU.swift:455) */
+
+typedef struct dgm_QuantP {
+    uint32_t rows, cols;
+    float qmax;                                /* 127 (int8) or 7 (int4)       */
+    uint32_t qGroup;
+} dgm_QuantP;                                  /* 16 bytes (src/GPU.swift:456) */
+
+/* ---- context: src/GPU.swift:91-198 (class GPU) --------------------------- */
+typedef struct dgm_gpu dgm_gpu;
+
+/* GPU.init (src/GPU.swift:118-156): binds the current HIP device and creates
+ * the context's own stream. */
+int dgm_gpu_create(dgm_gpu** out);
+void dgm_gpu_destroy(dgm_gpu* g);
+/* Use a caller-owned stream (e.g. a framework's current stream) instead of the
+ * context's own; NULL restores the context's stream. */
+int dgm_gpu_set_stream(dgm_gpu* g, void* hip_stream);
+void* dgm_gpu_stream(const dgm_gpu* g);
+int dgm_set_math(dgm_gpu* g, int mode);
+int dgm_get_math(const dgm_gpu* g);
+
+/* GPU.begin (src/GPU.swift:158-166): opens a dispatch region. */
+int dgm_begin(dgm_gpu* g);
+/* GPU.end (src/GPU.swift:168-180): waits for the region's work and returns the
+ * first error of the region (the reference prints it with lastKernel and
+ * exits; callers turn a nonzero status into their own fatal error). */
+int dgm_end(dgm_gpu* g);
+/* GPU.lastKernel (src/GPU.swift:99): name of the last dispatched kernel. */
+const char* dgm_last_kernel(const dgm_gpu* g);
+/* Human-readable text of the context's last error ("" when none). */
+const char* dgm_last_error(const dgm_gpu* g);
+
+/* ---- kernel-level entry points: buffer slot order of metal/kernels.metal -- */
+
+/* quant_i8 (metal/kernels.metal:79-98): W f32 -> Q i8 codes, S f32 scales. */
+int dgm_quant_i8(dgm_gpu* g, const float* W, int8_t* Q, float* scale,
+                 const dgm_QuantP* p);
+/* quant_i4 (metal/kernels.metal:100-124): W f32 -> packed nibbles, S. */
+int dgm_quant_i4(dgm_gpu* g, const float* W, uint8_t* Q, float* scale,
+                 const dgm_QuantP* p);
+
+/* gemm_nt_f32 (metal/kernels.metal:128-150): Y = X W^T (+bias). */
+int dgm_gemm_nt_f32(dgm_gpu* g, const float* W, const float* X,
+                    const float* bias, float* Y, const dgm_GemmP* p);
+/* gemm_nt_i8 (metal/kernels.metal:152-178): Y = X dequant(Q8,S)^T (+bias). */
+int dgm_gemm_nt_i8(dgm_gpu* g, const int8_t* W, const float* scale,
+                   const float* X, const float* bias, float* Y,
+                   const dgm_GemmP* p);
+/* gemm_nt_i4 (metal/kernels.metal:180-209): Y = X dequant(Q4,S)^T (+bias). */
+int dgm_gemm_nt_i4(dgm_gpu* g, const uint8_t* W, const float* scale,
+                   const float* X, const float* bias, float* Y,
+                   const dgm_GemmP* p);
+
+/* gemm_dx_f32 (metal/kernels.metal:211-224): dX = dY W. */
+int dgm_gemm_dx_f32(dgm_gpu* g, const float* W, const float* dY, float* dX,
+                    const dgm_GemmP* p);
+/* gemm_dx_i8 (metal/kernels.metal:226-246): STE dX = dY dequant(Q8,S). */
+int dgm_gemm_dx_i8(dgm_gpu* g, const int8_t* W, const float* scale,
+                   const float* dY, float* dX, const dgm_GemmP* p);
+/* gemm_dx_i4 (metal/kernels.metal:248-268): STE dX = dY dequant(Q4,S). */
+int dgm_gemm_dx_i4(dgm_gpu* g, const uint8_t* W, const float* scale,
+                   const float* dY, float* dX, const dgm_GemmP* p);
+
+/* gemm_dw (metal/kernels.metal:270-283): dW = dY^T X, overwrite. */
+int dgm_gemm_dw(dgm_gpu* g, const float* dY, const float* X, float* dW,
+                const dgm_GemmP* p);
+/* gemm_dw_acc (metal/kernels.metal:1014-1027): dW += dY^T X. */
+int dgm_gemm_dw_acc(dgm_gpu* g, const float* dY, const float* X, float* dW,
+                    const dgm_GemmP* p);
+
+/* ---- host call surface: src/GPU.swift:220-272 ----------------------------
+ * Same names and argument meaning as the Swift wrappers. Sizes are Swift Int
+ * (int64_t). q is int8_t* for bits 8, uint8_t* for bits 4; w is read only
+ * when bits == 32. bias may be NULL (the reference binds a dummy buffer and
+ * sets hasBias = 0). */
+
+/* GPU.quantize (src/GPU.swift:220-225): qmax = 7 for bits 4, else 127. */
+int dgm_quantize(dgm_gpu* g, const float* w, void* q, float* scale,
+                 int64_t rows, int64_t cols, int64_t bits, int64_t qGroup);
+/* GPU.gemmNT (src/GPU.swift:227-243). */
+int dgm_gemmNT(dgm_gpu* g, int64_t bits, const float* w, const void* q,
+               const float* scale, const float* x, const float* bias, float* y,
+               int64_t M, int64_t N, int64_t K, int64_t qGroup);
+/* GPU.gemmDX (src/GPU.swift:245-260). */
+int dgm_gemmDX(dgm_gpu* g, int64_t bits, const float* w, const void* q,
+               const float* scale, const float* dy, float* dx,
+               int64_t M, int64_t N, int64_t K, int64_t qGroup);
+/* GPU.gemmDW (src/GPU.swift:262-266). */
+int dgm_gemmDW(dgm_gpu* g, const float* dy, const float* x, float* dw,
+               int64_t M, int64_t N, int64_t K);
+/* GPU.gemmDWAcc (src/GPU.swift:268-272). */
+int dgm_gemmDWAcc(dgm_gpu* g, const float* dy, const float* x, float* dw,
+                  int64_t M, int64_t N, int64_t K);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DGM_QUANT_H */

@@ -1,0 +1,440 @@
+/*
+ * CPU oracle for the group-quantized linear path — TEST INFRASTRUCTURE ONLY.
+ *
+ * Used solely as the checker by tests/, by __graft_entry__.smoke() and by the
+ * cpu_baseline leg of bench.py. The product library never calls into it.
+ * Build: oracle/build.sh (gcc -O2 -ffp-contract=off -fno-fast-math), which keeps
+ * every fp32 operation separate and in source order, like the reference's
+ * scalar Swift CPU path.
+ *
+ * How each function is pinned (tests/test_oracle.py), without restating it:
+ *   orc_rng_*          SplitMix64 integer outputs against the published
+ *                      splitmix64 reference values for seed 1234567; uniform()
+ *                      against its closed form on those integers.
+ *   orc_quant_code,    hand-derived known answers (power-of-two scales so the
+ *   orc_quant          ties are exact: 2.5 -> 2, 3.5 -> 4, -2.5 -> -2; all-zero
+ *                      group -> s = 1e-8f and code 0; nibble encodings
+ *                      -7 -> 0x9, -1 -> 0xF, byte = lo | hi << 4), plus the
+ *                      invariants |q| <= lim, the group arg-max codes to +-lim,
+ *                      |q*s - w| <= s/2 (1 ulp slack), S == max(maxAbs/qmax,1e-8f),
+ *                      and a float64 numpy brute force of the same definition.
+ *   orc_dequant        q*s for hand-built codes; round trip |dequant - w| <= s/2.
+ *   orc_gemm_*         float64 numpy matmul on the same dequantised weights
+ *                      (tiny shapes: relative error <= 1e-6), and the identity
+ *                      matrix / one-hot inputs that select a single row or column.
+ *   DiT block pieces   rmsnorm: unit-RMS rows map to the weight; rope: norm
+ *                      preservation per pair and the t = 0 identity; attention:
+ *                      equal keys give the uniform average of v (the closed form
+ *                      used by Check.swift:214-241); softmax rows sum to 1;
+ *                      swiglu: silu(0) = 0 and float64 formula; block: float64
+ *                      numpy restatement on a tiny config.
+ * Nothing here is parity-unpinned.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- RNG: src/GPU.swift:4-29 ------------------------------------------- */
+
+void orc_rng_init(orc_rng* r, uint64_t seed) {
+    /* GPU.swift:6-8: seed 0 is replaced by a fixed constant. */
+    r->state = seed == 0 ? 0x123456789abcdef0ULL : seed;
+}
+
+uint64_t orc_rng_next(orc_rng* r) {
+    /* GPU.swift:9-15 */
+    r->state += 0x9E3779B97F4A7C15ULL;
+    uint64_t z = r->state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+float orc_rng_uniform(orc_rng* r) {
+    /* GPU.swift:16-19: top 24 bits, (x + 1) / 2^24, in fp32. */
+    uint64_t x = orc_rng_next(r) >> 40;
+    float xf = (float)x;
+    return (xf + 1.0f) / 16777216.0f;
+}
+
+float orc_rng_normal(orc_rng* r) {
+    /* GPU.swift:20-24. Swift's Float.pi is pi rounded toward zero (0x40490FDA).
+     * logf/cosf come from the C library here and from Darwin in the reference,
+     * so a draw may differ by an ulp; fixtures therefore store input bytes. */
+    float u1 = orc_rng_uniform(r);
+    if (u1 < 1e-7f) u1 = 1e-7f;
+    float u2 = orc_rng_uniform(r);
+    union { uint32_t u; float f; } pi = { 0x40490FDAu };
+    float a = -2.0f * logf(u1);
+    float b = 2.0f * pi.f;
+    b = b * u2;
+    return sqrtf(a) * cosf(b);
+}
+
+void orc_fill_normal(orc_rng* r, float* out, int64_t n, float std) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_rng_normal(r) * std;
+}
+
+uint64_t orc_normal_stream(uint64_t state, float* out, int64_t n, float std) {
+    orc_rng r; r.state = state;
+    orc_fill_normal(&r, out, n, std);
+    return r.state;
+}
+
+/* ---- quantize: Check.swift:399-431, kernels.metal:62-124 ----------------- */
+
+int orc_quant_code(float w, float s, int lim) {
+    float r = rintf(w / s);         /* correctly rounded divide, ties to even */
+    int q;
+    if (r > 2147483520.0f) q = lim;          /* outside int range: clamps anyway */
+    else if (r < -2147483520.0f) q = -lim;
+    else q = (int)r;
+    if (q > lim) q = lim;
+    if (q < -lim) q = -lim;
+    return q;
+}
+
+static int shape_ok(int64_t rows, int64_t cols, int group, int bits) {
+    if (rows < 0 || cols < 0 || group <= 0) return 0;
+    if (bits != 8 && bits != 4) return 0;
+    if (cols % group != 0) return 0;
+    if (bits == 4 && (group % 2) != 0) return 0;
+    return 1;
+}
+
+int orc_quant(const float* w, int64_t rows, int64_t cols, int group, int bits,
+              int8_t* q8, uint8_t* q4, float* scale) {
+    if (!shape_ok(rows, cols, group, bits)) return -1;
+    const float lim = bits == 4 ? 7.0f : 127.0f;
+    const int ilim = (int)lim;
+    const int64_t groups = cols / group;
+    for (int64_t row = 0; row < rows; ++row) {
+        for (int64_t g = 0; g < groups; ++g) {
+            const int64_t base = row * cols + g * group;
+            float maxAbs = 0.0f;
+            for (int i = 0; i < group; ++i) {
+                float a = fabsf(w[base + i]);
+                maxAbs = a >= maxAbs ? a : maxAbs;   /* Swift max(x, y): y >= x ? y : x */
+            }
+            float d = maxAbs / lim;
+            float s = 1e-8f >= d ? 1e-8f : d;
+            scale[row * groups + g] = s;
+            if (bits == 8) {
+                for (int i = 0; i < group; ++i)
+                    q8[base + i] = (int8_t)orc_quant_code(w[base + i], s, ilim);
+            } else {
+                for (int i = 0; i < group; i += 2) {
+                    int c0 = orc_quant_code(w[base + i], s, ilim);
+                    int c1 = orc_quant_code(w[base + i + 1], s, ilim);
+                    q4[(base + i) >> 1] = (uint8_t)((c0 & 0xF) | ((c1 & 0xF) << 4));
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* Signed code at (row, col) of a packed matrix: Check.swift:450-452. */
+static inline int code_at(const void* q, int64_t row, int64_t col, int64_t cols, int bits) {
+    if (bits == 8) return ((const int8_t*)q)[row * cols + col];
+    uint8_t b = ((const uint8_t*)q)[(row * cols + col) >> 1];
+    int nib = (col & 1) ? (b >> 4) : (b & 0xF);
+    return nib >= 8 ? nib - 16 : nib;
+}
+
+int orc_dequant(const void* q, const float* scale, int64_t rows, int64_t cols,
+                int group, int bits, float* out) {
+    if (!shape_ok(rows, cols, group, bits)) return -1;
+    const int64_t groups = cols / group;
+    for (int64_t n = 0; n < rows; ++n)
+        for (int64_t k = 0; k < cols; ++k)
+            out[n * cols + k] = (float)code_at(q, n, k, cols, bits) * scale[n * groups + k / group];
+    return 0;
+}
+
+/* ---- fp32 GEMMs: Check.swift:460-494 ------------------------------------ */
+
+void orc_gemm_nt(const float* x, const float* w, const float* bias, float* y,
+                 int64_t M, int64_t N, int64_t K) {
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            float acc = bias ? bias[n] : 0.0f;
+            for (int64_t k = 0; k < K; ++k) acc += x[m * K + k] * w[n * K + k];
+            y[m * N + n] = acc;
+        }
+}
+
+void orc_gemm_dx(const float* dy, const float* w, float* dx,
+                 int64_t M, int64_t N, int64_t K) {
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t k = 0; k < K; ++k) {
+            float acc = 0.0f;
+            for (int64_t n = 0; n < N; ++n) acc += dy[m * N + n] * w[n * K + k];
+            dx[m * K + k] = acc;
+        }
+}
+
+void orc_gemm_dw(const float* dy, const float* x, float* dw,
+                 int64_t M, int64_t N, int64_t K, int accumulate) {
+    /* Check.swift:484-494 (overwrite) and kernels.metal:1014-1027 (+=). */
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t k = 0; k < K; ++k) {
+            float acc = 0.0f;
+            for (int64_t m = 0; m < M; ++m) acc += dy[m * N + n] * x[m * K + k];
+            if (accumulate) dw[n * K + k] += acc;
+            else dw[n * K + k] = acc;
+        }
+}
+
+/* ---- Metal kernel orders: kernels.metal:152-209, 226-268 ----------------- */
+
+int orc_gemm_nt_q(const void* q, const float* scale, const float* x,
+                  const float* bias, float* y, int64_t M, int64_t N, int64_t K,
+                  int group, int bits) {
+    if (!shape_ok(N, K, group, bits)) return -1;
+    const int64_t groups = K / group;
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            const float* xr = x + m * K;
+            float acc = 0.0f;
+            for (int64_t g = 0; g < groups; ++g) {
+                float part = 0.0f;
+                const int64_t base = g * group;
+                if (bits == 8) {
+                    for (int i = 0; i < group; ++i)
+                        part += (float)code_at(q, n, base + i, K, 8) * xr[base + i];
+                } else {
+                    /* gemm_nt_i4 pairs two products before the add (kernels.metal:201-204). */
+                    for (int i = 0; i < group; i += 2) {
+                        float w0 = (float)code_at(q, n, base + i, K, 4);
+                        float w1 = (float)code_at(q, n, base + i + 1, K, 4);
+                        float p0 = w0 * xr[base + i];
+                        float p1 = w1 * xr[base + i + 1];
+                        part += p0 + p1;
+                    }
+                }
+                acc += part * scale[n * groups + g];
+            }
+            if (bias) acc += bias[n];
+            y[m * N + n] = acc;
+        }
+    return 0;
+}
+
+int orc_gemm_dx_q(const void* q, const float* scale, const float* dy, float* dx,
+                  int64_t M, int64_t N, int64_t K, int group, int bits) {
+    if (!shape_ok(N, K, group, bits)) return -1;
+    const int64_t groups = K / group;
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t k = 0; k < K; ++k) {
+            const int64_t g = k / group;
+            float acc = 0.0f;
+            for (int64_t n = 0; n < N; ++n) {
+                float wv = (float)code_at(q, n, k, K, bits) * scale[n * groups + g];
+                acc += dy[m * N + n] * wv;
+            }
+            dx[m * K + k] = acc;
+        }
+    return 0;
+}
+
+/* ---- DiT block pieces (kernels.metal line refs per function) ------------- */
+
+void orc_rmsnorm_fwd(const float* x, float* y, float* rstd, const float* weight,
+                     int64_t rows, int64_t cols, float eps) {
+    /* kernels.metal:807-825 */
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float ss = 0.0f;
+        for (int64_t c = 0; c < cols; ++c) ss += xr[c] * xr[c];
+        ss /= (float)cols;
+        float rs = 1.0f / sqrtf(ss + eps);
+        if (rstd) rstd[r] = rs;
+        float* yr = y + r * cols;
+        for (int64_t c = 0; c < cols; ++c) yr[c] = (xr[c] * rs) * weight[c];
+    }
+}
+
+void orc_rope_tables(int maxT, int dim, float theta, float* cosv, float* sinv) {
+    /* src/Macro.swift:509-530 */
+    int half = dim / 2;
+    float* inv = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    for (int i = 0; i < half; ++i) {
+        float e = (float)(2 * i) / (float)dim;
+        inv[i] = powf(theta, -e);
+    }
+    for (int t = 0; t < maxT; ++t)
+        for (int i = 0; i < half; ++i) {
+            float f = (float)t * inv[i];
+            float c = cosf(f), s = sinf(f);
+            cosv[t * dim + i] = c; cosv[t * dim + i + half] = c;
+            sinv[t * dim + i] = s; sinv[t * dim + i + half] = s;
+        }
+    free(inv);
+}
+
+void orc_rope_fwd(const float* x, float* y, const float* cosv, const float* sinv,
+                  int B, int T, int H, int D) {
+    /* kernels.metal:871-889: rotate-half, [B,T,H,D], tables [T,D]. */
+    int64_t total = (int64_t)B * T * H * D;
+    int mid = D >> 1;
+    for (int64_t i = 0; i < total; ++i) {
+        int d = (int)(i % D);
+        int t = (int)((i / ((int64_t)H * D)) % T);
+        float rot = d < mid ? -x[i + mid] : x[i - mid];
+        float c = cosv[t * D + d], s = sinv[t * D + d];
+        float a = x[i] * c, b = rot * s;
+        y[i] = a + b;
+    }
+}
+
+void orc_repeat_heads(const float* src, float* dst, int B, int T, int H, int D) {
+    /* kernels.metal:980-993 */
+    int64_t total = (int64_t)B * T * H * D;
+    for (int64_t i = 0; i < total; ++i) {
+        int d = (int)(i % D);
+        int t = (int)((i / ((int64_t)H * D)) % T);
+        int b = (int)(i / ((int64_t)T * H * D));
+        dst[i] = src[((int64_t)b * T + t) * D + d];
+    }
+}
+
+void orc_attn_fwd(const float* q, const float* k, const float* v, float* scores,
+                  float* probs, float* av, int B, int T, int H, int D, int causal) {
+    /* kernels.metal:443-506; scale = 1/sqrt(Float(D)) (GPU.swift attnP). */
+    float scale = 1.0f / sqrtf((float)D);
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H; ++h)
+            for (int t = 0; t < T; ++t) {
+                float* srow = scores + (((int64_t)b * H + h) * T + t) * T;
+                for (int s = 0; s < T; ++s) {
+                    float acc = 0.0f;
+                    for (int d = 0; d < D; ++d)
+                        acc += q[(((int64_t)b * T + t) * H + h) * D + d] *
+                               k[(((int64_t)b * T + s) * H + h) * D + d];
+                    acc *= scale;
+                    if (causal && s > t) acc = -1.0e30f;
+                    srow[s] = acc;
+                }
+                float* prow = probs + (((int64_t)b * H + h) * T + t) * T;
+                float mx = srow[0];
+                for (int s = 1; s < T; ++s) mx = srow[s] > mx ? srow[s] : mx;
+                float sum = 0.0f;
+                for (int s = 0; s < T; ++s) sum += expf(srow[s] - mx);
+                float inv = 1.0f / sum;
+                for (int s = 0; s < T; ++s) prow[s] = expf(srow[s] - mx) * inv;
+            }
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    float acc = 0.0f;
+                    for (int s = 0; s < T; ++s)
+                        acc += probs[(((int64_t)b * H + h) * T + t) * T + s] *
+                               v[(((int64_t)b * T + s) * H + h) * D + d];
+                    av[(((int64_t)b * T + t) * H + h) * D + d] = acc;
+                }
+}
+
+static float silu_sigmoid(float z) {
+    /* kernels.metal:911-918 */
+    if (z >= 0.0f) { float e = expf(-z); return 1.0f / (1.0f + e); }
+    float e = expf(z);
+    return e / (1.0f + e);
+}
+
+void orc_swiglu_fwd(const float* gate, const float* up, float* y, int64_t n) {
+    /* kernels.metal:920-930 */
+    for (int64_t i = 0; i < n; ++i) {
+        float z = gate[i];
+        float a = z * silu_sigmoid(z);
+        y[i] = a * up[i];
+    }
+}
+
+void orc_add(const float* a, const float* b, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = a[i] + b[i];   /* kernels.metal:419-427 */
+}
+
+void orc_mix(const float* a, const float* b, float* y, int64_t n, float ca, float cb) {
+    for (int64_t i = 0; i < n; ++i) {                      /* kernels.metal:951-959 */
+        float p = ca * a[i], r = cb * b[i];
+        y[i] = p + r;
+    }
+}
+
+/* ---- DiT loop body: src/DiT.swift:520-550 -------------------------------- */
+
+enum { W_LN1, W_QPRE, W_KPRE, W_VPRE, W_VFIRST, W_VMIX, W_Q, W_KROT, W_K, W_V,
+       W_SCORES, W_PROBS, W_AV, W_ATTN, W_T1, W_MID, W_LN2, W_GATE, W_UP, W_SW,
+       W_MLP, W_PRE, W_RSTD, W_COS, W_SIN, W_XN, W_COUNT };
+
+static void dit_sizes(const orc_dit_cfg* c, int64_t* sz) {
+    int64_t M = (int64_t)c->B * c->T, C = c->C, F = c->F, KV = c->D;
+    int64_t att = (int64_t)c->B * c->H * c->T * c->T;
+    int64_t s[W_COUNT] = { M * C, M * C, M * KV, M * KV, M * KV, M * KV, M * C, M * KV,
+                           M * C, M * C, att, att, M * C, M * C, M * C, M * C, M * C,
+                           M * F, M * F, M * F, M * C, M * C, M,
+                           (int64_t)c->T * c->D, (int64_t)c->T * c->D, M * C };
+    memcpy(sz, s, sizeof(s));
+}
+
+int64_t orc_dit_workspace_floats(const orc_dit_cfg* c) {
+    int64_t sz[W_COUNT], total = 0;
+    dit_sizes(c, sz);
+    for (int i = 0; i < W_COUNT; ++i) total += sz[i];
+    return total;
+}
+
+int orc_dit_forward(const orc_dit_cfg* c,
+                    const void* qq, const float* sq, const void* qk, const float* sk,
+                    const void* qv, const float* sv, const void* qo, const float* so,
+                    const void* qg, const float* sg, const void* qu, const float* su,
+                    const void* qd, const float* sd,
+                    const float* n1, const float* n1b, const float* n2,
+                    const float* n2b, const float* nf,
+                    float* x_io, float* ws) {
+    if (c->H * c->D != c->C || (c->D % 2) != 0) return -1;
+    int64_t sz[W_COUNT];
+    float* p[W_COUNT];
+    dit_sizes(c, sz);
+    float* cur = ws;
+    for (int i = 0; i < W_COUNT; ++i) { p[i] = cur; cur += sz[i]; }
+    const int B = c->B, T = c->T, H = c->H, D = c->D, G = c->group, bits = c->bits;
+    const int64_t M = (int64_t)B * T, C = c->C, F = c->F, KV = D;
+    orc_rope_tables(T, D, c->theta, p[W_COS], p[W_SIN]);
+    float* x = x_io;
+    float* xn = p[W_XN];
+    for (int loop = 0; loop < c->loops; ++loop) {
+        orc_rmsnorm_fwd(x, p[W_LN1], p[W_RSTD], n1, M, C, c->eps);
+        if (orc_gemm_nt_q(qq, sq, p[W_LN1], NULL, p[W_QPRE], M, C, C, G, bits)) return -1;
+        if (orc_gemm_nt_q(qk, sk, p[W_LN1], NULL, p[W_KPRE], M, KV, C, G, bits)) return -1;
+        if (orc_gemm_nt_q(qv, sv, p[W_LN1], NULL, p[W_VPRE], M, KV, C, G, bits)) return -1;
+        if (loop == 0) {
+            memcpy(p[W_VFIRST], p[W_VPRE], sizeof(float) * (size_t)(M * KV));
+            orc_repeat_heads(p[W_VPRE], p[W_V], B, T, H, D);
+        } else {
+            orc_mix(p[W_VPRE], p[W_VFIRST], p[W_VMIX], M * KV, 1.0f - c->mix, c->mix);
+            orc_repeat_heads(p[W_VMIX], p[W_V], B, T, H, D);
+        }
+        orc_rope_fwd(p[W_QPRE], p[W_Q], p[W_COS], p[W_SIN], B, T, H, D);
+        orc_rope_fwd(p[W_KPRE], p[W_KROT], p[W_COS], p[W_SIN], B, T, 1, D);
+        orc_repeat_heads(p[W_KROT], p[W_K], B, T, H, D);
+        orc_attn_fwd(p[W_Q], p[W_K], p[W_V], p[W_SCORES], p[W_PROBS], p[W_AV], B, T, H, D, 0);
+        if (orc_gemm_nt_q(qo, so, p[W_AV], NULL, p[W_ATTN], M, C, C, G, bits)) return -1;
+        orc_rmsnorm_fwd(p[W_ATTN], p[W_T1], p[W_RSTD], n1b, M, C, c->eps);
+        orc_add(x, p[W_T1], p[W_MID], M * C);
+        orc_rmsnorm_fwd(p[W_MID], p[W_LN2], p[W_RSTD], n2, M, C, c->eps);
+        if (orc_gemm_nt_q(qg, sg, p[W_LN2], NULL, p[W_GATE], M, F, C, G, bits)) return -1;
+        if (orc_gemm_nt_q(qu, su, p[W_LN2], NULL, p[W_UP], M, F, C, G, bits)) return -1;
+        orc_swiglu_fwd(p[W_GATE], p[W_UP], p[W_SW], M * F);
+        if (orc_gemm_nt_q(qd, sd, p[W_SW], NULL, p[W_MLP], M, C, F, G, bits)) return -1;
+        orc_rmsnorm_fwd(p[W_MLP], p[W_T1], p[W_RSTD], n2b, M, C, c->eps);
+        orc_add(p[W_MID], p[W_T1], p[W_PRE], M * C);
+        orc_rmsnorm_fwd(p[W_PRE], xn, p[W_RSTD], nf, M, C, c->eps);
+        memcpy(x, xn, sizeof(float) * (size_t)(M * C));
+    }
+    return 0;
+}

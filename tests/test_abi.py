@@ -1,0 +1,61 @@
+"""CPU checks of the C ABI: header <-> library exports, struct layouts."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "dgm_quant.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:int|void\s*\*?|const char\s*\*)\s*(dgm_\w+)\s*\(", text, re.M))
+
+
+def test_header_declares_the_reference_surface():
+    names = header_functions()
+    # Kernel-level entries (metal/kernels.metal) and GPU.swift wrappers.
+    for n in ["dgm_quant_i8", "dgm_quant_i4", "dgm_gemm_nt_f32", "dgm_gemm_nt_i8", "dgm_gemm_nt_i4",
+              "dgm_gemm_dx_f32", "dgm_gemm_dx_i8", "dgm_gemm_dx_i4", "dgm_gemm_dw", "dgm_gemm_dw_acc",
+              "dgm_quantize", "dgm_gemmNT", "dgm_gemmDX", "dgm_gemmDW", "dgm_gemmDWAcc",
+              "dgm_begin", "dgm_end", "dgm_last_kernel"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(dgm):
+    lib = dgm.load_library()
+    names = header_functions()
+    assert names == set(dgm.PROTOTYPES), "binding prototypes drifted from the header"
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_param_block_layouts_compile(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include "dgm_quant.h"\n#include <stddef.h>\n'
+        "_Static_assert(sizeof(dgm_GemmP) == 32, \"GemmP\");\n"
+        "_Static_assert(sizeof(dgm_QuantP) == 16, \"QuantP\");\n"
+        "_Static_assert(offsetof(dgm_GemmP, qGroup) == 16, \"qGroup\");\n"
+        "_Static_assert(offsetof(dgm_QuantP, qmax) == 8, \"qmax\");\n"
+        "int main(void) { return 0; }\n")
+    subprocess.run(["gcc", "-std=c11", "-fsyntax-only", "-I", os.path.join(REPO, "include"), str(src)],
+                   check=True)
+    from dgm_amd import GemmP, QuantP
+    assert ctypes.sizeof(GemmP) == 32 and ctypes.sizeof(QuantP) == 16
+    assert QuantP.qmax.offset == 8 and GemmP.qGroup.offset == 16
+
+
+def test_product_does_not_touch_the_oracle():
+    """The shipped package never imports, links or calls the CPU oracle."""
+    pkg = os.path.join(REPO, "diffusion-gpt-metal_amd")
+    banned = re.compile(r"import\s+oracle|from\s+oracle|liboracle|\borc_\w+\(")
+    for root, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
+                text = open(os.path.join(root, f), errors="ignore").read()
+                assert not banned.search(text), f

@@ -1,0 +1,220 @@
+"""GPU parity of the fp32 GEMM family through the C ABI:
+gemm_nt_{f32,i8,i4} (metal/kernels.metal:128-209), STE gemm_dx_{f32,i8,i4}
+(211-268), gemm_dw / gemm_dw_acc (270-283, 1014-1027).
+
+Bars (stated per assert):
+  * the reference's own check (Check.swift:97-136): same shapes, seeds and
+    distributions, max abs error < 2e-3 against dequant + cpuGemm*;
+  * max relative error max|got - ref| / max|ref| <= 1e-5 against float64
+    products of the same dequantized weights (the fp32 path's tolerance).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import from_dev, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def quantize_dev(gpu, w_dev, N, K, G, bits):
+    import torch
+    q = torch.zeros(max(N * K // (2 if bits == 4 else 1), 1), dtype=torch.uint8 if bits == 4 else torch.int8,
+                    device="cuda")
+    s = torch.zeros(max(N * (K // G), 1), dtype=torch.float32, device="cuda")
+    gpu.begin()
+    gpu.quantize(w_dev, q, s, N, K, bits, G)
+    gpu.end()
+    return q, s
+
+
+def host_codes(q):
+    a = from_dev(q)
+    return a
+
+
+def run_step(gpu, bits, x, w, bias, dy, M, N, K, G, dw_init=None):
+    """quantize -> gemmNT -> gemmDX -> gemmDW (+ gemmDWAcc) through the wrappers."""
+    import torch
+    xd, wd, dyd = to_dev(x), to_dev(w), to_dev(dy)
+    bd = None if bias is None else to_dev(bias)
+    q = s = None
+    if bits != 32:
+        q, s = quantize_dev(gpu, wd, N, K, G, bits)
+    y = torch.zeros(max(M * N, 1), device="cuda")
+    dx = torch.zeros(max(M * K, 1), device="cuda")
+    dw = torch.zeros(max(N * K, 1), device="cuda")
+    dwa = to_dev(dw_init) if dw_init is not None else None
+    gpu.begin()
+    gpu.gemmNT(bits, wd, q, s, xd, bd, y, M, N, K, G)
+    gpu.gemmDX(bits, wd, q, s, dyd, dx, M, N, K, G)
+    gpu.gemmDW(dyd, xd, dw, M, N, K)
+    if dwa is not None:
+        gpu.gemmDWAcc(dyd, xd, dwa, M, N, K)
+    gpu.end()
+    out = dict(y=from_dev(y)[: M * N], dx=from_dev(dx)[: M * K], dw=from_dev(dw)[: N * K])
+    if dwa is not None:
+        out["dwa"] = from_dev(dwa)
+    if q is not None:
+        out["q"], out["s"] = from_dev(q), from_dev(s)
+    return out
+
+
+def dequant_host(orc, out, w, N, K, G, bits):
+    if bits == 32:
+        return np.asarray(w, np.float32)
+    q = out["q"][: (N * K if bits == 8 else N * K // 2)]
+    if bits == 8:
+        q = q.view(np.int8)
+    return orc.dequant(q, out["s"][: N * (K // G)], N, K, G, bits)
+
+
+@pytest.mark.parametrize("bits", [32, 8, 4])
+def test_reference_check_gemm(gpu, orc, bits):
+    """Check.swift:97-136 verbatim in shapes, seeds and draw order (G = 8)."""
+    cases = [(3, 5, 7), (17, 13, 16), (8, 24, 32)] if bits == 32 else [(3, 5, 8), (15, 13, 16), (8, 24, 32)]
+    rng = orc.RNG(1000 + bits)
+    worst_abs, worst_rel = 0.0, 0.0
+    for M, N, K in cases:
+        x = rng.randn(M * K, 0.5)
+        w = rng.randn(N * K, 0.5)
+        bias = rng.randn(N, 0.1)
+        dy = rng.randn(M * N, 0.2)
+        out = run_step(gpu, bits, x, w, bias, dy, M, N, K, 8)
+        if bits != 32:
+            qr, sr = orc.quant(w, N, K, 8, bits)
+            assert np.array_equal(out["q"][: qr.size].view(qr.dtype), qr)
+        wd = dequant_host(orc, out, w, N, K, 8, bits)
+        y_ref = orc.gemm_nt(x, wd, bias, M, N, K)
+        dx_ref = orc.gemm_dx(dy, wd, M, N, K)
+        dw_ref = orc.gemm_dw(dy, x, M, N, K)
+        for got, ref in ((out["y"], y_ref), (out["dx"], dx_ref), (out["dw"], dw_ref)):
+            worst_abs = max(worst_abs, float(np.max(np.abs(got - ref))))
+        w64, x64, dy64 = (a.astype(np.float64) for a in (wd.reshape(N, K), x.reshape(M, K), dy.reshape(M, N)))
+        worst_rel = max(worst_rel, rel_err(out["y"], (x64 @ w64.T + bias).ravel()),
+                        rel_err(out["dx"], (dy64 @ w64).ravel()), rel_err(out["dw"], (dy64.T @ x64).ravel()))
+    assert worst_abs < 2e-3, f"reference bar: max abs {worst_abs:.3e}"
+    assert worst_rel <= TOL, f"fp32 bar: max rel {worst_rel:.3e}"
+
+
+def _check_all(orc, out, x, w, bias, dy, M, N, K, G, bits, dw_init=None):
+    wd = dequant_host(orc, out, w, N, K, G, bits).reshape(N, K).astype(np.float64)
+    x64 = np.asarray(x, np.float64).reshape(M, K)
+    dy64 = np.asarray(dy, np.float64).reshape(M, N)
+    y_ref = x64 @ wd.T + (0 if bias is None else np.asarray(bias, np.float64))
+    errs = {
+        "y": rel_err(out["y"], y_ref.ravel()),
+        "dx": rel_err(out["dx"], (dy64 @ wd).ravel()),
+        "dw": rel_err(out["dw"], (dy64.T @ x64).ravel()),
+    }
+    if dw_init is not None:
+        errs["dwa"] = rel_err(out["dwa"], (dy64.T @ x64).ravel() + dw_init)
+    return errs
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_config1_and_config2_shapes(gpu, orc, bits):
+    """c1: X[512,192], W[768,192] int8 G32. c2: X[512,768], W[192,768] int4 G32,
+    dY ~ N(0, 1e-3). Inputs drawn X, W, dY from RNG(1000 + config)."""
+    M, N, K = (512, 768, 192) if bits == 8 else (512, 192, 768)
+    rng = orc.RNG(1001 if bits == 8 else 1002)
+    x = rng.randn(M * K, 1.0)
+    w = rng.randn(N * K, 0.02)
+    dy = rng.randn(M * N, 1e-3)
+    dw0 = rng.randn(N * K, 1e-2)
+    out = run_step(gpu, bits, x, w, None, dy, M, N, K, 32, dw_init=dw0)
+    errs = _check_all(orc, out, x, w, None, dy, M, N, K, 32, bits, dw_init=dw0)
+    assert max(errs.values()) <= TOL, errs
+    # Agreement with the Metal kernel order restated on the CPU.
+    q = out["q"][: (N * K if bits == 8 else N * K // 2)]
+    y_k = orc.gemm_nt_q(q.view(np.int8) if bits == 8 else q, out["s"], x, None, M, N, K, 32, bits)
+    assert rel_err(out["y"], y_k.astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("bits,G", [(32, 1), (8, 2), (4, 2), (8, 10), (4, 14), (8, 32), (4, 128)])
+@pytest.mark.parametrize("M,N,K_groups", [(1, 1, 1), (1, 37, 3), (33, 47, 5), (70, 3, 2), (129, 65, 7)])
+def test_ragged_shapes(gpu, orc, bits, G, M, N, K_groups):
+    K = G * K_groups if bits != 32 else 5 * K_groups + 3
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dy = rng.standard_normal(M * N).astype(np.float32)
+    dw0 = rng.standard_normal(N * K).astype(np.float32)
+    out = run_step(gpu, bits, x, w, bias, dy, M, N, K, max(G, 1), dw_init=dw0)
+    errs = _check_all(orc, out, x, w, bias, dy, M, N, K, max(G, 1), bits, dw_init=dw0)
+    assert max(errs.values()) <= TOL, errs
+
+
+def test_unaligned_operands(gpu, orc):
+    import torch
+    M, N, K, G = 20, 24, 64, 16
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = rng.standard_normal(N * K).astype(np.float32)
+    xs = torch.zeros(M * K + 1, device="cuda")
+    xs[1:] = to_dev(x)
+    wd = to_dev(w)
+    q, s = quantize_dev(gpu, wd, N, K, G, 8)
+    qs = torch.zeros(N * K + 1, dtype=torch.int8, device="cuda")
+    qs[1:] = q
+    y = torch.zeros(M * N, device="cuda")
+    gpu.begin()
+    gpu.gemmNT(8, None, qs[1:], s, xs[1:], None, y, M, N, K, G)
+    gpu.end()
+    wdq = orc.dequant(from_dev(q), from_dev(s), N, K, G, 8).reshape(N, K).astype(np.float64)
+    assert rel_err(from_dev(y), (x.reshape(M, K).astype(np.float64) @ wdq.T).ravel()) <= TOL
+
+
+def test_kernel_level_entries_and_bias_flag(gpu, dgm, orc):
+    import torch
+    M, N, K, G = 16, 32, 64, 32
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = rng.standard_normal(N * K).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    wd, xd, bd = to_dev(w), to_dev(x), to_dev(b)
+    q, s = quantize_dev(gpu, wd, N, K, G, 4)
+    y1 = torch.zeros(M * N, device="cuda")
+    y0 = torch.zeros(M * N, device="cuda")
+    gpu.begin()
+    gpu.gemm_nt_i4(q, s, xd, bd, y1, dgm.GemmP(M, N, K, 1, G, 0, 0, 0))
+    gpu.gemm_nt_i4(q, s, xd, bd, y0, dgm.GemmP(M, N, K, 0, G, 0, 0, 0))   # hasBias = 0 ignores bias
+    gpu.end()
+    assert gpu.lastKernel == "gemm_nt_i4"
+    wdq = orc.dequant(from_dev(q), from_dev(s), N, K, G, 4).reshape(N, K).astype(np.float64)
+    ref0 = x.reshape(M, K).astype(np.float64) @ wdq.T
+    assert rel_err(from_dev(y0), ref0.ravel()) <= TOL
+    assert rel_err(from_dev(y1), (ref0 + b).ravel()) <= TOL
+
+
+def test_gemm_error_paths(gpu, dgm):
+    import torch
+    t = torch.zeros(4096, device="cuda")
+    q = torch.zeros(4096, dtype=torch.int8, device="cuda")
+    with pytest.raises(dgm.DgmError) as e:
+        gpu.gemmNT(8, None, q, t, t, None, t, 4, 4, 16, 8)
+    assert e.value.code == dgm.DGM_ERR_NOT_BEGUN
+    gpu.begin()
+    with pytest.raises(dgm.DgmError) as e:       # K % qGroup != 0 (GPU.swift:229)
+        gpu.gemmNT(8, None, q, t, t, None, t, 4, 4, 12, 8)
+    assert e.value.code == dgm.DGM_ERR_SHAPE
+    gpu.begin()
+    with pytest.raises(dgm.DgmError) as e:       # GPU.swift:247
+        gpu.gemmDX(4, None, q, t, t, t, 4, 4, 12, 8)
+    assert e.value.code == dgm.DGM_ERR_SHAPE
+    gpu.begin()
+    with pytest.raises(dgm.DgmError) as e:
+        gpu.gemmNT(16, t, q, t, t, None, t, 4, 4, 16, 8)
+    assert e.value.code == dgm.DGM_ERR_BITS
+    gpu.begin()
+    with pytest.raises(dgm.DgmError) as e:
+        gpu.gemmNT(8, None, None, t, t, None, t, 4, 4, 16, 8)
+    assert e.value.code == dgm.DGM_ERR_ARG
+    gpu.begin()
+    gpu.gemmNT(8, None, q, t, t, None, t, 0, 4, 16, 8)     # M = 0: nothing to do
+    gpu.gemmDW(t, t, t, 0, 4, 16)                           # M = 0: dW = 0
+    gpu.end()
+    assert float(t[:64].abs().sum()) == 0.0
