@@ -67,7 +67,10 @@ int dgm_gpu_create(dgm_gpu** out) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, g->device) == hipSuccess && prop.multiProcessorCount > 0)
         g->num_cus = prop.multiProcessorCount;
-    if (hipStreamCreateWithFlags(&g->own_stream, hipStreamNonBlocking) != hipSuccess) {
+    // A blocking stream: it orders itself after work on the null stream, where
+    // callers that allocate with torch or hipMemset may still be filling the
+    // buffers they hand over.
+    if (hipStreamCreateWithFlags(&g->own_stream, hipStreamDefault) != hipSuccess) {
         delete g;
         return DGM_ERR_HIP;
     }

@@ -53,7 +53,8 @@ def torch_cuda():
 
 @pytest.fixture(scope="session")
 def gpu(dgm, torch_cuda):
-    g = dgm.GPU()
+    # Launch on torch's current stream: the buffers are torch tensors filled on it.
+    g = dgm.GPU(stream=torch_cuda.cuda.current_stream())
     yield g
     g.close()
 
