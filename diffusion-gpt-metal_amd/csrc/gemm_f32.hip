@@ -272,9 +272,15 @@ int check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits) {
 
 namespace dgm {
 
+bool skinny_ok(int bits, const void* W, const float* X, const dgm_GemmP* p);
+int skinny_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
+               const float* bias, float* Y, const dgm_GemmP* p);
+
 // Entry used by the dispatcher in gemm_entry.hip; declared there.
 int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
                  const float* bias, float* Y, const dgm_GemmP* p) {
+    // Decode-shaped quantized forwards stream W once through int8 MFMA.
+    if (skinny_ok(bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
     GemmArgs a{};
     a.A = X; a.B = W; a.scale = scale; a.bias = bias; a.out = Y;
     a.M = p->M; a.N = p->N; a.K = p->K;
