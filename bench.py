@@ -3,24 +3,33 @@
 Headline ("c2"): one step = the int4 group-quant
 linear forward plus its STE backward on the DiT down-projection shape,
 X[512,768] ~ N(0,1), W[192,768] ~ N(0,0.02) int4 G=32, dY ~ N(0,1e-3):
-    Y = X deq(W)^T   (gemm_nt_i4)
-    dX = dY deq(W)   (gemm_dx_i4)
-    dW = dY^T X      (gemm_dw)
+    Y  = X deq(W)^T   (gemm_nt_i4)
+    dX = dY deq(W)    (gemm_dx_i4)
+    dW = dY^T X       (gemm_dw)
 Inputs are resident in HBM before timing; the weights are quantized once
 before the timed region. value = algorithmic flop of the step / step time.
 
-The same JSON line carries `roofline` (dominant kernel of the step, timed with
-HIP events on the stream it runs on), `cpu_baseline` (the reference's scalar
-CPU path restated in C, single thread, on a bounded sample), and `workloads`:
-the other configs measured the same way (c1 int8 forward, c4 decode-shaped
-int4 with weight copies rotated past the 256 MB Infinity Cache, c5 prefill,
-quantization at the c4/c5 weight shape).
+Every GPU timing replays a captured HIP graph of the launches (through
+torch.cuda.CUDAGraph), so host-side call overhead never leaks into kernel
+times; HIP events on the launch stream bracket the replay.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extra] [--skip-cpu]
+The JSON line also carries `roofline` (dominant kernel of the step),
+`cpu_baseline` (the reference's scalar CPU path restated in C, one thread,
+bounded sample) and `workloads` (the other configs, each with its own
+roofline: c1 int8 forward, quantization at the c4/c5 weight shape, c4
+decode-shaped int4 with weight copies rotated past the 256 MB Infinity
+Cache, c5 prefill, c3 DiT block forward).
+
+Usage:
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extra] [--skip-cpu]
+                  [--only name,name] [--calib-copy]
+  python bench.py --summarize DIR [--title TEXT]      rocprofv3 csv -> markdown
+  python bench.py --traffic NAME FETCH_DIR WRITE_DIR  PMC runs -> profiles/traffic.json
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import importlib.util
 import json
 import os
@@ -29,9 +38,12 @@ import time
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(REPO, "diffusion-gpt-metal_amd")
+TRAFFIC_JSON = os.path.join(REPO, "profiles", "traffic.json")
 
 METRIC = "group-quant GEMM GB/s & TFLOP/s (% of MI355X roofline); DiT block fwd tokens/s"
-PEAK = {"hbm_GBps": 8000.0, "fp32_TFLOPs": 157.3, "bf16_TFLOPs": 2500.0}
+# MI355X published peaks (dense).
+PEAK = {"hbm_GBps": 8000.0, "fp32_TFLOPs": 157.3, "bf16_TFLOPs": 2500.0, "int8_TOPs": 5000.0}
+CALIB_BYTES = 256 * 2 ** 20   # plain copy kernel used to scale FETCH_SIZE / WRITE_SIZE
 
 
 def load_package():
@@ -52,11 +64,10 @@ def log(msg: str) -> None:
 class Bench:
     def __init__(self, dgm, torch):
         self.dgm, self.torch = dgm, torch
-        self.gpu = dgm.GPU()
-        # Launch on torch's current stream so torch.cuda.Event brackets the
-        # very stream the kernels run on.
-        self.stream = torch.cuda.current_stream()
-        self.gpu.set_stream(self.stream)
+        # A dedicated stream: graph capture needs a non-default stream, and the
+        # library launches on it, so events recorded on it bracket the kernels.
+        self.stream = torch.cuda.Stream()
+        self.gpu = dgm.GPU(stream=self.stream)
         self.gen = torch.Generator(device="cpu").manual_seed(1234)
 
     def randn(self, n: int, std: float):
@@ -66,32 +77,59 @@ class Bench:
     def zeros(self, n: int, dtype=None):
         return self.torch.zeros(max(n, 1), dtype=dtype or self.torch.float32, device="cuda")
 
+    def sync(self):
+        self.torch.cuda.synchronize()
+
     def quantized(self, w, N: int, K: int, G: int, bits: int):
         t = self.torch
         q = self.zeros(N * K // (2 if bits == 4 else 1), t.uint8 if bits == 4 else t.int8)
         s = self.zeros(N * (K // G))
+        self.sync()
         self.gpu.begin()
         self.gpu.quantize(w, q, s, N, K, bits, G)
         self.gpu.end()
         return q, s
 
-    def time_launches(self, fn, reps: int, warmup: int = 3) -> float:
-        """Average ms per call of fn (which enqueues work) between HIP events
-        recorded on the launch stream."""
+    def capture(self, fn, calls: int):
+        """A CUDA graph of `calls` invocations fn(0..calls-1). fn runs eagerly
+        first, so workspaces exist before capture (no allocation in a graph)."""
         t = self.torch
+        self.sync()
+        with t.cuda.stream(self.stream):
+            self.gpu.begin()
+            for i in range(min(calls, 3)):
+                fn(i)
+            self.gpu.end()
+        g = t.cuda.CUDAGraph()
+        with t.cuda.graph(g, stream=self.stream):
+            self.gpu.begin()
+            for i in range(calls):
+                fn(i)
+        # dgm end() synchronizes, which a capture forbids; status is checked
+        # at launch and by the synchronizing replay below.
         self.gpu.begin()
-        for i in range(warmup):
-            fn(i)
-        self.gpu.end()
+        return g
+
+    def graph_ms(self, g, replays: int = 1) -> float:
+        t = self.torch
+        with t.cuda.stream(self.stream):
+            g.replay()
+        self.stream.synchronize()
         e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        self.gpu.begin()
         e0.record(self.stream)
-        for i in range(reps):
-            fn(i)
+        with t.cuda.stream(self.stream):
+            for _ in range(replays):
+                g.replay()
         e1.record(self.stream)
-        self.gpu.end()
         e1.synchronize()
-        return e0.elapsed_time(e1) / reps
+        return e0.elapsed_time(e1)
+
+    def time_launches(self, fn, reps: int) -> float:
+        """Average ms per call of fn, from a graph replay of reps calls."""
+        g = self.capture(fn, reps)
+        ms = self.graph_ms(g) / reps
+        del g
+        return ms
 
 
 def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
@@ -100,14 +138,21 @@ def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) 
 
 
 def load_traffic() -> dict:
-    """Per-kernel HBM bytes per launch measured with rocprofv3 --pmc
-    (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel calibration) and
-    committed under profiles/; absent entries report null."""
-    path = os.path.join(REPO, "profiles", "traffic.json")
-    if os.path.exists(path):
-        with open(path) as f:
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE runs, scaled by a copy-kernel calibration (bench.py --traffic);
+    absent entries report null."""
+    if os.path.exists(TRAFFIC_JSON):
+        with open(TRAFFIC_JSON) as f:
             return json.load(f)
     return {}
+
+
+def traffic_for(workload: str, kernel_key: str):
+    ent = load_traffic().get(workload, {})
+    for name, rec in ent.items():
+        if kernel_key in name:
+            return rec.get("total_bytes")
+    return None
 
 
 # ---- headline: c2 step -------------------------------------------------------
@@ -121,12 +166,11 @@ def c2_setup(b: Bench):
     q, s = b.quantized(w, N, K, G, 4)
     y, dx, dw = b.zeros(M * N), b.zeros(M * K), b.zeros(N * K)
     g = b.gpu
-    kern = {
+    return {
         "gemm_nt_i4": lambda i: g.gemmNT(4, None, q, s, x, None, y, M, N, K, G),
         "gemm_dx_i4": lambda i: g.gemmDX(4, None, q, s, dy, dx, M, N, K, G),
         "gemm_dw": lambda i: g.gemmDW(dy, x, dw, M, N, K),
     }
-    return kern
 
 
 def c2_flops() -> int:
@@ -217,8 +261,8 @@ def bench_c4(b: Bench, reps: int, M: int, math_mode: int) -> dict:
     wq_bytes = N * K // 2 + N * (K // G) * 4
     copies = max(2, -(-512 * 2 ** 20 // wq_bytes))
     w = b.randn(N * K, 0.02)
-    qs = [b.quantized(w, N, K, G, 4) for _ in range(1)]
-    q0, s0 = qs[0]
+    q0, s0 = b.quantized(w, N, K, G, 4)
+    del w
     Q = [q0] + [q0.clone() for _ in range(copies - 1)]
     S = [s0] + [s0.clone() for _ in range(copies - 1)]
     x = b.randn(M * K, 1.0)
@@ -236,6 +280,7 @@ def bench_c4(b: Bench, reps: int, M: int, math_mode: int) -> dict:
     return {"kernel": "gemm_nt_i4", "math": mode, "shape": f"M={M} K=4096 N=14336 int4 G=128",
             "us": round(ms * 1e3, 3), "GBps": round(nbytes / ms / 1e6, 2),
             "TFLOPs": round(flops / ms / 1e9, 3), "weight_copies_rotated": copies,
+            "algorithmic_bytes": nbytes,
             "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
 
 
@@ -248,7 +293,7 @@ def bench_c5(b: Bench, reps: int, bits: int, math_mode: int) -> dict:
     y = b.zeros(M * N)
     b.gpu.set_math(math_mode)
     try:
-        ms = b.time_launches(lambda i: b.gpu.gemmNT(bits, None, q, s, x, None, y, M, N, K, G), reps, warmup=1)
+        ms = b.time_launches(lambda i: b.gpu.gemmNT(bits, None, q, s, x, None, y, M, N, K, G), reps)
     finally:
         b.gpu.set_math(b.dgm.DGM_MATH_FP32)
     flops = 2 * M * N * K
@@ -257,6 +302,103 @@ def bench_c5(b: Bench, reps: int, bits: int, math_mode: int) -> dict:
     return {"kernel": f"gemm_nt_i{bits}", "math": mode, "shape": f"M=8192 K=4096 N=14336 int{bits} G=128",
             "us": round(ms * 1e3, 3), "TFLOPs": round(flops / ms / 1e9, 3),
             "roofline": roofline(flops / ms / 1e9, peak, "TFLOP/s", "mfma")}
+
+
+def calib_copy(b: Bench) -> dict:
+    """A plain device copy of CALIB_BYTES, for scaling the --pmc traffic
+    counters (its algorithmic traffic is CALIB_BYTES read + CALIB_BYTES written)."""
+    t = b.torch
+    n = CALIB_BYTES // 4
+    src = t.ones(n, device="cuda")
+    dst = t.zeros(n, device="cuda")
+    b.sync()
+    for _ in range(10):
+        dst.copy_(src)
+    b.sync()
+    return {"bytes": CALIB_BYTES}
+
+
+# ---- rocprofv3 output helpers (run on the CPU) ---------------------------------
+
+
+def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "")
+    return name.split("(")[0] if "(" in name else name
+
+
+def _find(d: str, suffix: str):
+    for root, _, files in os.walk(d):
+        for f in files:
+            if f.endswith(suffix):
+                return os.path.join(root, f)
+    return None
+
+
+def summarize(d: str, title: str) -> str:
+    out = [f"# {title}", ""]
+    ks = _find(d, "kernel_stats.csv")
+    if ks:
+        rows = list(csv.DictReader(open(ks)))
+        out += ["| kernel | calls | avg us | min us | max us | total % |", "|---|---|---|---|---|---|"]
+        for r in rows:
+            out.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                       f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} | "
+                       f"{float(r['Percentage']):.2f} |")
+        out.append("")
+    cc = _find(d, "counter_collection.csv")
+    if cc:
+        agg: dict = {}
+        for r in csv.DictReader(open(cc)):
+            k = _short(r["Kernel_Name"])
+            agg.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        names = sorted({c for v in agg.values() for c in v})
+        out += ["| kernel | dispatches | " + " | ".join(names) + " |", "|---" * (len(names) + 2) + "|"]
+        for k, v in agg.items():
+            n = max(len(x) for x in v.values())
+            out.append(f"| `{k}` | {n} | " + " | ".join(
+                f"{sum(v[c]) / len(v[c]):.1f}" if c in v else "" for c in names) + " |")
+        out.append("")
+    return "\n".join(out)
+
+
+def _counter_means(d: str, counter: str) -> dict:
+    cc = _find(d, "counter_collection.csv")
+    if not cc:
+        raise FileNotFoundError(f"no counter_collection.csv under {d}")
+    agg: dict = {}
+    for r in csv.DictReader(open(cc)):
+        if r["Counter_Name"] == counter:
+            agg.setdefault(_short(r["Kernel_Name"]), []).append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in agg.items()}
+
+
+def traffic(name: str, fetch_dir: str, write_dir: str) -> dict:
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) -> bytes per launch, scaled so
+    that the calibration copy reads and writes exactly CALIB_BYTES."""
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    copy = [k for k in fetch if "copy" in k.lower() or "elementwise" in k.lower()]
+    if not copy:
+        raise RuntimeError("calibration copy kernel not found (run the PMC passes with --calib-copy)")
+    ck = max(copy, key=lambda k: fetch[k])
+    f_scale = CALIB_BYTES / (fetch[ck] * 1024.0)
+    w_scale = CALIB_BYTES / (write.get(ck, 0.0) * 1024.0) if write.get(ck) else 1.0
+    rec = {"_calibration": {"kernel": ck, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}}
+    for k in fetch:
+        if k == ck:
+            continue
+        fb = fetch[k] * 1024.0 * f_scale
+        wb = write.get(k, 0.0) * 1024.0 * w_scale
+        rec[k] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "total_bytes": round(fb + wb)}
+    allt = load_traffic()
+    allt[name] = rec
+    os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(allt, f, indent=1, sort_keys=True)
+    return rec
+
+
+# ---- main -------------------------------------------------------------------------
 
 
 def main() -> int:
@@ -268,7 +410,19 @@ def main() -> int:
     ap.add_argument("--skip-extra", action="store_true", help="headline only")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra workloads to run")
+    ap.add_argument("--calib-copy", action="store_true", help="run the traffic calibration copy at the end")
+    ap.add_argument("--summarize", metavar="DIR")
+    ap.add_argument("--title", default="rocprofv3 summary")
+    ap.add_argument("--traffic", nargs=3, metavar=("NAME", "FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+
+    if args.summarize:
+        print(summarize(args.summarize, args.title))
+        return 0
+    if args.traffic:
+        print(json.dumps(traffic(*args.traffic), indent=1))
+        return 0
+
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -282,7 +436,7 @@ def main() -> int:
     dgm = load_package()
     b = Bench(dgm, torch)
 
-    # -- headline step --------------------------------------------------------
+    # -- headline step ----------------------------------------------------------
     log("[bench] c2 step setup")
     kern = c2_setup(b)
     order = ["gemm_nt_i4", "gemm_dx_i4", "gemm_dw"]
@@ -291,26 +445,26 @@ def main() -> int:
         for k in order:
             kern[k](i)
 
-    b.gpu.begin()
-    for i in range(args.warmup):
-        step(i)
-    b.gpu.end()
-    torch.cuda.synchronize()
+    steps = b.capture(step, args.steps)
+    warm = b.capture(step, max(args.warmup, 1))
+    b.graph_ms(warm)
+    b.sync()
     t0 = time.perf_counter()
-    b.gpu.begin()
-    for i in range(args.steps):
-        step(i)
-    b.gpu.end()
-    torch.cuda.synchronize()
+    with torch.cuda.stream(b.stream):
+        steps.replay()
+    b.sync()
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
-    log(f"[bench] c2 step {ms_step * 1e3:.2f} us")
+    gpu_ms_step = b.graph_ms(steps) / args.steps
+    del steps, warm
+    log(f"[bench] c2 step {ms_step * 1e3:.2f} us wall, {gpu_ms_step * 1e3:.2f} us on the stream")
 
     per_kernel = {k: b.time_launches(kern[k], args.reps) for k in order}
     dom = max(per_kernel, key=per_kernel.get)
     flops_k = 2 * C2["M"] * C2["N"] * C2["K"]
-    traffic = load_traffic().get(f"c2:{dom}")
-    roof = roofline(flops_k / per_kernel[dom] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma", traffic)
+    roof = roofline(flops_k / per_kernel[dom] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
+                    traffic_for("c2", {"gemm_nt_i4": "gemm_f32_kernel<0", "gemm_dx_i4": "gemm_f32_kernel<1",
+                                       "gemm_dw": "gemm_f32_kernel<2"}[dom]))
     roof["kernel"] = dom
     roof["avg_launch_us"] = round(per_kernel[dom] * 1e3, 3)
     roof["algorithmic_bytes"] = c2_bytes()[dom]
@@ -333,7 +487,7 @@ def main() -> int:
         "data": "synthetic (torch CPU generator, seed 1234: X~N(0,1), W~N(0,0.02), dY~N(0,1e-3))",
         "config": {"workload": "c2: int4 group-quant linear fwd + STE bwd (gemm_nt_i4, gemm_dx_i4, gemm_dw)",
                    "M": C2["M"], "K": C2["K"], "N": C2["N"], "group": C2["G"], "bits": 4,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU", "timing": "one HIP graph of the timed steps"},
         "GBps": round(sum(c2_bytes().values()) / (ms_step * 1e-3) / 1e9, 2),
         "per_kernel_us": {k: round(v * 1e3, 3) for k, v in per_kernel.items()},
         "roofline": roof,
@@ -346,10 +500,11 @@ def main() -> int:
             ("c1_int8_fwd", lambda: bench_c1(b, args.reps)),
             ("quant_i4_14336x4096", lambda: bench_quant(b, 20, 4)),
             ("quant_i8_14336x4096", lambda: bench_quant(b, 20, 8)),
-            ("c4_int4_m1_fp32", lambda: bench_c4(b, 50, 1, dgm.DGM_MATH_FP32)),
-            ("c4_int4_m16_fp32", lambda: bench_c4(b, 50, 16, dgm.DGM_MATH_FP32)),
-            ("c4_int4_m16_bf16", lambda: bench_c4(b, 50, 16, dgm.DGM_MATH_BF16)),
-            ("c4_int4_m64_bf16", lambda: bench_c4(b, 50, 64, dgm.DGM_MATH_BF16)),
+            ("c4_int4_m1_fp32", lambda: bench_c4(b, 72, 1, dgm.DGM_MATH_FP32)),
+            ("c4_int4_m16_fp32", lambda: bench_c4(b, 72, 16, dgm.DGM_MATH_FP32)),
+            ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, dgm.DGM_MATH_BF16)),
+            ("c4_int4_m64_fp32", lambda: bench_c4(b, 72, 64, dgm.DGM_MATH_FP32)),
+            ("c4_int4_m64_bf16", lambda: bench_c4(b, 72, 64, dgm.DGM_MATH_BF16)),
             ("c5_int4_bf16", lambda: bench_c5(b, 5, 4, dgm.DGM_MATH_BF16)),
             ("c5_int8_bf16", lambda: bench_c5(b, 5, 8, dgm.DGM_MATH_BF16)),
         ]
@@ -363,6 +518,10 @@ def main() -> int:
                 W[name] = {"error": str(e)}
             torch.cuda.empty_cache()
         out["workloads"] = W
+
+    if args.calib_copy:
+        log("[bench] calibration copy")
+        out["calibration_copy"] = calib_copy(b)
 
     if not args.skip_cpu:
         log("[bench] cpu baseline (oracle, 1 thread)")

@@ -11,8 +11,9 @@
 // straddle rows): each lane owns 8 consecutive weights (two 128-bit loads),
 // the G/8 lanes of a group reduce maxAbs with cross-lane xor shuffles, and
 // each lane writes its 8 codes with one 64-bit (int8) or 32-bit (int4) store.
-// Groups that are not a power of two multiple of 8 (or G > 512) take a
-// one-thread-per-group kernel with the same arithmetic.
+// Groups that are not a power of two multiple of 8 (or G > 512), and rows
+// that are not a whole number of groups, take a one-thread-per-group kernel
+// with the same arithmetic.
 #include "common.hpp"
 
 namespace {
@@ -78,14 +79,18 @@ __global__ __launch_bounds__(kThreads) void quant_vec_kernel(
     }
 }
 
-// One thread per (row, group) for any even G (int4) or any G (int8).
+// One thread per (row, group) for any even G (int4) or any G (int8). Rows
+// need not hold a whole number of groups: like the reference, only
+// floor(cols/G) groups per row are quantized, the tail columns' codes are
+// left untouched and scales are strided by floor(cols/G).
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void quant_generic_kernel(
     const float* __restrict__ W, void* __restrict__ Q, float* __restrict__ S,
-    int64_t ngroups, int G, float qmax, int lim) {
+    int64_t ngroups, int64_t cols, int64_t gpr, int G, float qmax, int lim) {
     const int64_t gi = int64_t(blockIdx.x) * kThreads + threadIdx.x;
     if (gi >= ngroups) return;
-    const int64_t base = gi * G;
+    const int64_t row = gi / gpr;
+    const int64_t base = row * cols + (gi - row * gpr) * G;
     float m = 0.0f;
     for (int i = 0; i < G; ++i) {
         float x = fabsf(W[base + i]);
@@ -114,22 +119,22 @@ int launch_quant(dgm_gpu* g, const char* name, const float* W, void* Q, float* S
     if (!p) return dgm::fail(g, DGM_ERR_ARG, "%s: null QuantP", name);
     const int64_t rows = p->rows, cols = p->cols, G = p->qGroup;
     if (G <= 0) return dgm::fail(g, DGM_ERR_SHAPE, "%s: qGroup must be positive", name);
-    if (cols % G != 0)
-        return dgm::fail(g, DGM_ERR_SHAPE, "%s: cols=%lld not divisible by group %lld", name,
-                         (long long)cols, (long long)G);
+    // An odd int4 group would pack across groups (the reference rejects it in
+    // GPTConfig.validate, src/Params.swift:171).
     if (BITS == 4 && (G % 2) != 0)
         return dgm::fail(g, DGM_ERR_SHAPE, "%s: quant group must be even for int4 packing", name);
     const int64_t total = rows * cols;
-    if (total == 0) return DGM_OK;
+    const int64_t gpr = cols / G;   // groups per row (quant_i8: p.cols / G)
+    if (total == 0 || gpr == 0) return DGM_OK;
     if (!W || !Q || !S) return dgm::fail(g, DGM_ERR_ARG, "%s: null buffer", name);
     if (!(p->qmax >= 1.0f) || p->qmax > 127.0f)
         return dgm::fail(g, DGM_ERR_ARG, "%s: qmax %g outside [1, 127]", name, double(p->qmax));
     const float qmax = p->qmax;
     const int lim = static_cast<int>(qmax);
-    const int64_t ngroups = total / G;
+    const int64_t ngroups = rows * gpr;
 
     const bool pow2 = (G & (G - 1)) == 0;
-    const bool vec_ok = G >= 8 && G <= 512 && pow2 && dgm::aligned(W, 16) &&
+    const bool vec_ok = cols % G == 0 && G >= 8 && G <= 512 && pow2 && dgm::aligned(W, 16) &&
                         dgm::aligned(Q, BITS == 8 ? 8 : 4);
     hipStream_t st = g->stream;
     if (vec_ok) {
@@ -149,7 +154,7 @@ int launch_quant(dgm_gpu* g, const char* name, const float* W, void* Q, float* S
     } else {
         const unsigned blocks = dgm::ceil_div(ngroups, kThreads);
         hipLaunchKernelGGL((quant_generic_kernel<BITS>), dim3(blocks), dim3(kThreads), 0, st, W, Q,
-                           S, ngroups, static_cast<int>(G), qmax, lim);
+                           S, ngroups, cols, gpr, static_cast<int>(G), qmax, lim);
     }
     DGM_LAUNCH_CHECK(g, name);
     return DGM_OK;

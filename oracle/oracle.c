@@ -96,6 +96,7 @@ int orc_quant_code(float w, float s, int lim) {
     return q;
 }
 
+/* Shapes the GEMM/dequant side accepts: K % G == 0 (src/GPU.swift:229,247). */
 static int shape_ok(int64_t rows, int64_t cols, int group, int bits) {
     if (rows < 0 || cols < 0 || group <= 0) return 0;
     if (bits != 8 && bits != 4) return 0;
@@ -104,9 +105,22 @@ static int shape_ok(int64_t rows, int64_t cols, int group, int bits) {
     return 1;
 }
 
+/* Shapes the quantizer accepts. cpuQuant / quant_i8 / quant_i4 do not require
+ * cols % G == 0: they quantize floor(cols/G) groups per row, leave the codes
+ * of the tail columns untouched and stride the scales by floor(cols/G)
+ * (Check.swift:399-424, kernels.metal:86-98). An odd int4 group would read
+ * past the group (the reference's GPTConfig.validate rejects it,
+ * Params.swift:171), so it is rejected here. */
+static int quant_shape_ok(int64_t rows, int64_t cols, int group, int bits) {
+    if (rows < 0 || cols < 0 || group <= 0) return 0;
+    if (bits != 8 && bits != 4) return 0;
+    if (bits == 4 && (group % 2) != 0) return 0;
+    return 1;
+}
+
 int orc_quant(const float* w, int64_t rows, int64_t cols, int group, int bits,
               int8_t* q8, uint8_t* q4, float* scale) {
-    if (!shape_ok(rows, cols, group, bits)) return -1;
+    if (!quant_shape_ok(rows, cols, group, bits)) return -1;
     const float lim = bits == 4 ? 7.0f : 127.0f;
     const int ilim = (int)lim;
     const int64_t groups = cols / group;

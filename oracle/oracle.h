@@ -40,9 +40,11 @@ uint64_t orc_normal_stream(uint64_t state, float* out, int64_t n, float std);
 /* quant_code (kernels.metal:62-67, Check.swift:426-431). */
 int  orc_quant_code(float w, float s, int lim);
 
-/* cpuQuant (Check.swift:399-424 == kernels.metal:79-124), any even G with
- * cols % G == 0. bits = 8 writes q8[rows*cols]; bits = 4 writes
- * q4[rows*cols/2]. Returns 0, or -1 on a shape the reference rejects. */
+/* cpuQuant (Check.swift:399-424 == kernels.metal:79-124). Quantizes
+ * floor(cols/G) groups per row; codes of tail columns are left untouched and
+ * scales are strided by floor(cols/G), as in the reference. bits = 8 writes
+ * q8[rows*cols]; bits = 4 writes q4[rows*cols/2] (int4 needs an even G).
+ * Returns 0, or -1 on a rejected shape. */
 int  orc_quant(const float* w, int64_t rows, int64_t cols, int group, int bits,
                int8_t* q8, uint8_t* q4, float* scale);
 

@@ -110,17 +110,19 @@ class RNG:
 
 # ---- quantize / dequant: Check.swift:399-458 -------------------------------
 
-def quant(w: np.ndarray, rows: int, cols: int, group: int, bits: int):
+def quant(w: np.ndarray, rows: int, cols: int, group: int, bits: int, init=None):
     """cpuQuant (Check.swift:399-424). Returns (codes, scales); codes are
-    int8 [rows*cols] for bits 8 and packed uint8 [rows*cols/2] for bits 4."""
+    int8 [rows*cols] for bits 8 and packed uint8 [rows*cols/2] for bits 4.
+    `init` gives the codes' prior contents (tail columns of a row that is not
+    a whole number of groups keep them; zeros by default)."""
     w = _f32(w).reshape(-1)
     assert w.size == rows * cols
     scale = np.zeros(rows * (cols // group), dtype=np.float32)
     if bits == 8:
-        q = np.zeros(rows * cols, dtype=np.int8)
+        q = np.zeros(rows * cols, dtype=np.int8) if init is None else np.array(init, dtype=np.int8)
         rc = lib().orc_quant(_p(w), rows, cols, group, 8, _p(q), None, _p(scale))
     else:
-        q = np.zeros(rows * cols // 2, dtype=np.uint8)
+        q = np.zeros(rows * cols // 2, dtype=np.uint8) if init is None else np.array(init, dtype=np.uint8)
         rc = lib().orc_quant(_p(w), rows, cols, group, 4, None, _p(q), _p(scale))
     if rc != 0:
         raise ValueError("oracle rejected the quantization shape")

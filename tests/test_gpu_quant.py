@@ -137,10 +137,6 @@ def test_error_paths(gpu, dgm):
         gpu.quantize(w, q, s, 2, 32, 8, 8)
     assert e.value.code == dgm.DGM_ERR_NOT_BEGUN
     gpu.begin()
-    with pytest.raises(dgm.DgmError) as e:       # cols % G != 0
-        gpu.quantize(w, q, s, 2, 30, 8, 8)
-    assert e.value.code == dgm.DGM_ERR_SHAPE
-    gpu.begin()
     with pytest.raises(dgm.DgmError) as e:       # odd group for int4 (Params.swift:171)
         gpu.quantize(w, q, s, 2, 30, 4, 3)
     assert e.value.code == dgm.DGM_ERR_SHAPE
@@ -151,3 +147,22 @@ def test_error_paths(gpu, dgm):
     gpu.begin()
     gpu.quantize(w, q, s, 0, 32, 8, 8)           # empty: no work, no error
     gpu.end()
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_partial_last_group_left_alone(gpu, dgm, orc, bits):
+    """cols % G != 0: floor(cols/G) groups per row, tail codes untouched,
+    scales strided by floor(cols/G) (Check.swift:399-424, kernels.metal:86-98)."""
+    import torch
+    rows, cols, group = 5, 52, 8          # 6 groups + 4 tail columns per row
+    w = orc.RNG(77).randn(rows * cols, 0.4)
+    nq = rows * cols if bits == 8 else rows * cols // 2
+    prior = (np.arange(nq) % 251).astype(np.uint8)
+    q = torch.from_numpy(prior.copy()).to("cuda")
+    s = torch.zeros(rows * (cols // group), device="cuda")
+    gpu.begin()
+    gpu.quantize(to_dev(w), q, s, rows, cols, bits, group)
+    gpu.end()
+    qr, sr = orc.quant(w, rows, cols, group, bits, init=prior.view(np.int8) if bits == 8 else prior)
+    assert np.array_equal(from_dev(s), sr)
+    assert np.array_equal(from_dev(q), qr.view(np.uint8))

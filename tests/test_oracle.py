@@ -135,11 +135,23 @@ def test_quant_code_clamps(orc):
     assert orc.quant_code(-7.5, 1.0, 7) == -7   # rint -8, clamped
 
 
-def test_quant_rejects_bad_shapes(orc):
-    with pytest.raises(ValueError):
-        orc.quant(np.zeros(10, np.float32), 1, 10, 4, 8)   # cols % G != 0
+def test_quant_rejects_odd_int4_group(orc):
     with pytest.raises(ValueError):
         orc.quant(np.zeros(9, np.float32), 1, 9, 3, 4)     # odd group for int4
+
+
+def test_quant_partial_last_group_is_left_alone(orc):
+    # cols = 10, G = 4: floor(10/4) = 2 groups per row are quantized, the two
+    # tail columns keep their prior codes, scales are strided by 2
+    # (Check.swift:401-405 loops g in 0..<cols/group).
+    u = 2.0 ** -5
+    w = np.array([[127, 1, 2, 3, 64, -127, 0, 5, 9, 9],
+                  [0, 0, 0, 0, 1, 2, 3, -127, 7, 7]], dtype=np.float64) * u
+    prior = np.full(20, 99, np.int8)
+    q, s = orc.quant(w.astype(np.float32).ravel(), 2, 10, 4, 8, init=prior)
+    assert s.tolist() == [np.float32(u), np.float32(u), np.float32(1e-8), np.float32(u)]
+    assert q.reshape(2, 10).tolist() == [[127, 1, 2, 3, 64, -127, 0, 5, 99, 99],
+                                         [0, 0, 0, 0, 1, 2, 3, -127, 99, 99]]
 
 
 def _unpack4(q, n):
