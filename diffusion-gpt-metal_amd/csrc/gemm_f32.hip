@@ -275,12 +275,18 @@ namespace dgm {
 bool skinny_ok(int bits, const void* W, const float* X, const dgm_GemmP* p);
 int skinny_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
                const float* bias, float* Y, const dgm_GemmP* p);
+bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
+int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
+             const float* bias, float* Y, const dgm_GemmP* p);
 
 // Entry used by the dispatcher in gemm_entry.hip; declared there.
 int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
                  const float* bias, float* Y, const dgm_GemmP* p) {
     // Decode-shaped quantized forwards stream W once through int8 MFMA.
     if (skinny_ok(bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
+    // Larger M in the reduced-precision mode: bf16 MFMA with W dequantized in LDS.
+    if (g->math == DGM_MATH_BF16 && bf16_ok(bits, W, X, scale, p))
+        return bf16_fwd(g, bits, W, scale, X, bias, Y, p);
     GemmArgs a{};
     a.A = X; a.B = W; a.scale = scale; a.bias = bias; a.out = Y;
     a.M = p->M; a.N = p->N; a.K = p->K;

@@ -138,3 +138,37 @@ def test_skinny_repeatable_and_kernel_entry(gpu, dgm, orc):
     gpu.end()
     assert np.array_equal(from_dev(y1), from_dev(y2))
     assert rel_err(from_dev(y1), _ref(orc, q, s, x, None, M, N, K, G, 4)) <= 1e-5
+
+
+# ---- large-M reduced-precision path (bf16 MFMA, W dequantized in LDS) -------
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K,G", [(65, 33, 64, 32), (256, 256, 256, 128), (300, 500, 192, 64),
+                                     (512, 768, 192, 32), (1000, 260, 1024, 128)])
+def test_bf16_large_m(gpu, dgm, orc, bits, M, N, K, G):
+    rng = np.random.default_rng(M + N + K + bits)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if M % 2 == 0 else None
+    q, s = _quantize(gpu, to_dev(w), N, K, G, bits)
+    ref = _ref(orc, q, s, x, bias, M, N, K, G, bits)
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16)
+    assert rel_err(y, ref) <= 1e-2
+
+
+def test_config5_prefill_bf16(gpu, dgm, orc):
+    """c5: X[8192,4096] ~ N(0,1), W[14336,4096] ~ N(0,0.02) int4 G=128, bf16
+    path. The float64 reference is checked on a sample of 96 rows (full-size
+    outputs are compared through the same dequantized weights)."""
+    import torch
+    M, N, K, G = 8192, 14336, 4096, 128
+    gen = torch.Generator(device="cpu").manual_seed(1005)
+    x = torch.randn(M * K, generator=gen)
+    w = torch.randn(N * K, generator=gen) * 0.02
+    q, s = _quantize(gpu, w.to("cuda"), N, K, G, 4)
+    y = _forward(gpu, dgm, 4, q, s, x.numpy(), None, M, N, K, G, dgm.DGM_MATH_BF16).reshape(M, N)
+    wd = orc.dequant(from_dev(q), from_dev(s), N, K, G, 4).reshape(N, K).astype(np.float64)
+    rows = np.random.default_rng(0).choice(M, 96, replace=False)
+    ref = x.numpy().reshape(M, K)[rows].astype(np.float64) @ wd.T
+    assert rel_err(y[rows], ref) <= 1e-2
+    assert np.all(np.isfinite(y))
