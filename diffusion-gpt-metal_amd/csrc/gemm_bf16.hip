@@ -11,16 +11,25 @@
 //  * X is converted to bf16 once by a pre-pass (it is re-read by every tile
 //    column, so converting it inside the GEMM would repeat the work N/256
 //    times).
-//  * A workgroup of 8 waves computes a 256 x 256 tile of Y; each wave owns a
-//    128 x 64 block = 8 x 4 v_mfma_f32_16x16x32_bf16 tiles (128 fp32
-//    accumulators, so two waves fit per SIMD with their staging registers).
-//    K advances 64 per step.
-//  * Both operand tiles live in LDS as bf16 rows of 64 k with a 16-byte pad
-//    (row stride 144 B), which spreads the 16 rows read by one ds_read_b128
-//    over distinct banks. Two stages: the global loads of step k+1 are issued
-//    before the MFMAs of step k; the weight tile of step k+1 is dequantized
-//    in registers and stored to the other stage afterwards; one barrier per
-//    step.
+//  * A workgroup of 4 waves computes a 256 x 256 tile of Y; each wave owns a
+//    128 x 128 quadrant = 8 x 8 v_mfma_f32_16x16x32_bf16 tiles (256 fp32
+//    accumulators in AGPRs). K advances 64 per step. LDS traffic per step
+//    depends only on the wave tile (rows + cols), so the largest quadrant
+//    that fits the register file keeps LDS reads (128 KB per step) below the
+//    MFMA time.
+//  * The X tile goes global -> LDS with global_load_lds_dwordx4 (no VGPR
+//    staging: the 256 accumulators leave no room for it). A wave instruction
+//    fills 1 KB of LDS in lane order, so rows are unpadded (128 B) and the
+//    16-byte chunks of row r sit at slot c ^ (r & 7): each lane fetches the
+//    global chunk that belongs in its slot. Fragment reads (16 rows, one
+//    chunk) then hit 8 distinct slots per 8-lane group, free of bank
+//    conflicts. The weight tile uses the same swizzle.
+//  * Each weight row is dequantized once per workgroup, by one thread, into
+//    the bf16 weight tile in LDS.
+//  * Two stages: the loads of step k+1 are issued before the MFMAs of step k;
+//    the weight codes of step k+1 are dequantized and stored to the other
+//    stage after the MFMAs; one barrier per step. The loop is unrolled by two
+//    so every stage index is a compile-time constant.
 //  * Dequant: int4 bytes are flipped to offset binary and masked into the
 //    high nibble, so each byte is 16*(code+8) as an unsigned value and
 //    converts with one v_cvt_f32_ubyte; fma(f, s/16, -8s) then yields
@@ -40,8 +49,8 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int NT = 512;
-constexpr int RS = BK * 2 + 16;   // LDS row stride in bytes
+constexpr int NT = 256;
+constexpr int RS = BK * 2;        // LDS row stride in bytes (chunks swizzled, no pad)
 constexpr int TILE = BM * RS;     // one operand tile (BM == BN)
 constexpr int STAGE = 2 * TILE;
 constexpr size_t LDS_BYTES = 2 * STAGE;
@@ -73,14 +82,20 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
         make_uint4(pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y), pack_bf16(b.z, b.w));
 }
 
+typedef __attribute__((address_space(1))) const void global_cvoid;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Byte offset of 16-byte chunk c of row r in a swizzled operand tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * RS + ((c ^ (r & 7)) << 4); }
+
 template <int BITS>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(Bf16Args a) {
-    constexpr int WB = BITS == 4 ? 1 : 2;   // 16-byte code loads per thread per step
+    constexpr int WB = BITS == 4 ? 2 : 4;   // 16-byte code loads per weight row per step
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int l16 = lane & 15, q = lane >> 4;
-    const int wm = wave >> 2, wn = wave & 3;   // wave block: rows wm*128, cols wn*64
+    const int wm = wave >> 1, wn = wave & 1;   // quadrant: rows wm*128, cols wn*128
     const int M = a.M, N = a.N, K = a.K;
 
     // -- tile of this workgroup (XCD-aware order).
@@ -94,128 +109,142 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(Bf16Args a) {
     const int m0 = (first_m + within % gm) * BM;
     const int n0 = (within / gm) * BN;
 
-    // -- per-thread global addresses. A: 4 passes of 64 rows x 8 16-byte
-    // chunks (128 contiguous bytes per row per step). B: two threads per
-    // weight row, one 32-k half (one scale) each. Rows past the matrix are
-    // clamped (never stored).
-    const int arow = t >> 3, achunk = t & 7;
-    uint32_t aoff[4];   // element offsets (the host bounds M*K below 2^32)
+    // -- X tile: wave w loads rows w*64 .. w*64+63, 8 rows per instruction;
+    // lane l lands in slot l%8 of row l/8 and fetches the chunk that belongs
+    // there (rows past M are clamped, never stored).
+    const int arl = lane >> 3, aslot = lane & 7;
+    uint32_t aoff[8];   // element offsets (the host bounds M*K below 2^32)
 #pragma unroll
-    for (int p = 0; p < 4; ++p) aoff[p] = uint32_t(min(m0 + p * 64 + arow, M - 1)) * uint32_t(K) + achunk * 8;
-    const int brow_i = t >> 1, bh = t & 1;
-    const int bn = min(n0 + brow_i, N - 1);
-    const uint8_t* bptr = a.W + size_t(bn) * (BITS == 4 ? K / 2 : K) + bh * (BITS == 4 ? 16 : 32);
+    for (int p = 0; p < 8; ++p) {
+        const int r = wave * 64 + p * 8 + arl;
+        aoff[p] = uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8);
+    }
+    // -- weight tile: one row per thread.
+    const int bn = min(n0 + t, N - 1);
+    const uint8_t* bptr = a.W + size_t(bn) * (BITS == 4 ? K / 2 : K);
     const float* sptr = a.S + size_t(bn) * a.groups;
 
-    uint4 areg[4];
     uint4 breg[WB];
-    float sreg;
-    auto gload = [&](int ks) {
+    float sreg[2];
+    auto gload = [&](int ks, int st) {
         const int k0 = ks * BK;
+        uint8_t* As = smem + st * STAGE + wave * 64 * RS;
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+            __builtin_amdgcn_global_load_lds((global_cvoid*)(a.Xb + aoff[p] + k0),
+                                             (lds_void*)(As + p * 8 * RS), 16, 0, 0);
 #pragma unroll
         for (int j = 0; j < WB; ++j)
             breg[j] = *reinterpret_cast<const uint4*>(bptr + (BITS == 4 ? k0 / 2 : k0) + 16 * j);
-        sreg = sptr[(k0 + 32 * bh) / a.G];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) areg[p] = *reinterpret_cast<const uint4*>(a.Xb + aoff[p] + k0);
+        sreg[0] = sptr[k0 / a.G];
+        sreg[1] = sptr[(k0 + 32) / a.G];
     };
 
-    auto lstore = [&](int st) {
-        uint8_t* As = smem + st * STAGE;
-        uint8_t* Bs = As + TILE;
+    auto dequant_store = [&](int st) {
+        uint8_t* Bs = smem + st * STAGE + TILE;
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-            *reinterpret_cast<uint4*>(As + (p * 64 + arow) * RS + achunk * 16) = areg[p];
-        uint8_t* bdst = Bs + brow_i * RS + bh * 64;   // this thread's 32 k
-        const float s = sreg;
-        if constexpr (BITS == 4) {
-            const float s16 = s * 0.0625f, off = -8.0f * s;
-            const uint32_t w4[4] = {breg[0].x, breg[0].y, breg[0].z, breg[0].w};
+        for (int h = 0; h < 2; ++h) {   // 32-k halves (one scale each)
+            const float s = sreg[h];
+            if constexpr (BITS == 4) {
+                const float s16 = s * 0.0625f, off = -8.0f * s;
+                const uint32_t w4[4] = {breg[h].x, breg[h].y, breg[h].z, breg[h].w};
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {   // 8 nibbles = k 8d..8d+7 of the half
-                const uint32_t x = w4[d] ^ 0x88888888u;            // offset binary
-                const uint32_t lo = (x << 4) & 0xF0F0F0F0u;        // even k: 16*(code+8)
-                const uint32_t hi = x & 0xF0F0F0F0u;               // odd k
-                uint32_t o[4];
+                for (int d = 0; d < 4; ++d) {   // 8 nibbles = k 8d..8d+7 of the half
+                    const uint32_t x = w4[d] ^ 0x88888888u;            // offset binary
+                    const uint32_t lo = (x << 4) & 0xF0F0F0F0u;        // even k: 16*(code+8)
+                    const uint32_t hi = x & 0xF0F0F0F0u;               // odd k
+                    uint32_t o[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float fe = float((lo >> (8 * i)) & 0xFFu);
-                    const float fo = float((hi >> (8 * i)) & 0xFFu);
-                    o[i] = pack_bf16(__builtin_fmaf(fe, s16, off), __builtin_fmaf(fo, s16, off));
+                    for (int i = 0; i < 4; ++i) {
+                        const float fe = float((lo >> (8 * i)) & 0xFFu);
+                        const float fo = float((hi >> (8 * i)) & 0xFFu);
+                        o[i] = pack_bf16(__builtin_fmaf(fe, s16, off), __builtin_fmaf(fo, s16, off));
+                    }
+                    *reinterpret_cast<uint4*>(Bs + swz(t, h * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
                 }
-                *reinterpret_cast<uint4*>(bdst + 16 * d) = make_uint4(o[0], o[1], o[2], o[3]);
-            }
-        } else {
-            const float off = -128.0f * s;
-            const uint32_t w8[8] = {breg[0].x, breg[0].y, breg[0].z, breg[0].w,
-                                    breg[1].x, breg[1].y, breg[1].z, breg[1].w};
+            } else {
+                const float off = -128.0f * s;
+                const uint32_t w8[8] = {breg[2 * h].x, breg[2 * h].y, breg[2 * h].z, breg[2 * h].w,
+                                        breg[2 * h + 1].x, breg[2 * h + 1].y, breg[2 * h + 1].z, breg[2 * h + 1].w};
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {   // 8 codes = k 8d..8d+7 of the half
-                uint32_t o[4];
+                for (int d = 0; d < 4; ++d) {   // 8 codes = k 8d..8d+7 of the half
+                    uint32_t o[4];
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t x = w8[2 * d + e] ^ 0x80808080u;   // code + 128
-                    const float f0 = float(x & 0xFFu), f1 = float((x >> 8) & 0xFFu);
-                    const float f2 = float((x >> 16) & 0xFFu), f3 = float(x >> 24);
-                    o[2 * e] = pack_bf16(__builtin_fmaf(f0, s, off), __builtin_fmaf(f1, s, off));
-                    o[2 * e + 1] = pack_bf16(__builtin_fmaf(f2, s, off), __builtin_fmaf(f3, s, off));
+                    for (int e = 0; e < 2; ++e) {
+                        const uint32_t x = w8[2 * d + e] ^ 0x80808080u;   // code + 128
+                        const float f0 = float(x & 0xFFu), f1 = float((x >> 8) & 0xFFu);
+                        const float f2 = float((x >> 16) & 0xFFu), f3 = float(x >> 24);
+                        o[2 * e] = pack_bf16(__builtin_fmaf(f0, s, off), __builtin_fmaf(f1, s, off));
+                        o[2 * e + 1] = pack_bf16(__builtin_fmaf(f2, s, off), __builtin_fmaf(f3, s, off));
+                    }
+                    *reinterpret_cast<uint4*>(Bs + swz(t, h * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
                 }
-                *reinterpret_cast<uint4*>(bdst + 16 * d) = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
     };
 
-    f32x4 acc[8][4];
+    f32x4 acc[8][8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Fragment addresses: row R = base + l16 has R & 7 == l16 & 7.
+    const int cw0 = ((0 * 4 + q) ^ (l16 & 7)) << 4, cw1 = ((1 * 4 + q) ^ (l16 & 7)) << 4;
     auto compute = [&](int st) {
-        const uint8_t* As = smem + st * STAGE + (wm * 128 + l16) * RS + q * 16;
-        const uint8_t* Bs = smem + st * STAGE + TILE + (wn * 64 + l16) * RS + q * 16;
+        const uint8_t* As = smem + st * STAGE + (wm * 128 + l16) * RS;
+        const uint8_t* Bs = smem + st * STAGE + TILE + (wn * 128 + l16) * RS;
         // B fragments stay in registers for the sub-step; A fragments stream
-        // through a two-deep ping-pong (the next one loads under the 4 MFMAs
+        // through a two-deep ping-pong (the next one loads under the 8 MFMAs
         // of the current one).
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            bf16x8 bf[4], af[2];
+            const int cw = kk ? cw1 : cw0;
+            bf16x8 bf[8], af[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(Bs + j * 16 * RS + kk * 64);
-            af[0] = *reinterpret_cast<const bf16x8*>(As + kk * 64);
+            for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(Bs + j * 16 * RS + cw);
+            af[0] = *reinterpret_cast<const bf16x8*>(As + cw);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (i + 1 < 8) af[(i + 1) & 1] = *reinterpret_cast<const bf16x8*>(As + (i + 1) * 16 * RS + kk * 64);
+                if (i + 1 < 8) af[(i + 1) & 1] = *reinterpret_cast<const bf16x8*>(As + (i + 1) * 16 * RS + cw);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 8; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i & 1], bf[j], acc[i][j], 0, 0, 0);
             }
         }
     };
 
-    const int nk = K / BK;
-    gload(0);
-    lstore(0);
+    const int nk = K / BK;   // even (host)
+    gload(0, 0);
+    dequant_store(0);
     __syncthreads();
-    for (int ks = 0; ks < nk; ++ks) {
-        // The next step's loads are unconditional (the last step re-reads its
-        // own tile): a conditional load would make its consumers wait for all
-        // loads in flight.
-        gload(ks + 1 < nk ? ks + 1 : ks);
-        // Phases stay apart: mixing the dequant of step k+1 into the MFMAs of
-        // step k raises register pressure until it spills; the two waves on
-        // each SIMD overlap one's MFMAs with the other's dequant instead.
+    // Step s lives in stage s & 1. The loop is unrolled by two so every stage
+    // index is a constant: with a runtime stage, or a guarded second half, the
+    // register allocator rotates the 256 accumulators through temporaries and
+    // spills. Phases stay apart (sched_barrier): mixing the dequant of step
+    // k+1 into the MFMAs of step k raises register pressure until it spills.
+    // The next step's loads are unconditional (the last step re-reads its own
+    // tile into the idle stage): a conditional load would make its consumers
+    // wait for all loads in flight.
+    for (int ks = 0; ks < nk; ks += 2) {
+        gload(ks + 1, 1);
         __builtin_amdgcn_sched_barrier(0);
-        compute(ks & 1);
+        compute(0);
         __builtin_amdgcn_sched_barrier(0);
-        lstore((ks + 1) & 1);
+        dequant_store(1);
+        __syncthreads();   // also waits for the direct X loads of step ks+1
+        gload(ks + 2 < nk ? ks + 2 : ks + 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1);
+        __builtin_amdgcn_sched_barrier(0);
+        dequant_store(0);
         __syncthreads();
     }
 
     // D layout of 16x16 f32: lane holds rows 4*(lane/16) + r, column lane%16.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = n0 + wn * 64 + j * 16 + l16;
+    for (int j = 0; j < 8; ++j) {
+        const int col = n0 + wn * 128 + j * 16 + l16;
         const float bv = (a.has_bias && col < N) ? a.bias[col] : 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -232,11 +261,11 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(Bf16Args a) {
 namespace dgm {
 
 // The bf16 path takes quantized forwards with M > 64 in the reduced-precision
-// mode: K a multiple of 64, every 32-k half inside one group, aligned operands.
+// mode: K a multiple of 128, every 32-k half inside one group, aligned operands.
 bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p) {
     if (bits != 4 && bits != 8) return false;
-    if (p->M <= 64 || p->K == 0 || (p->K % BK) != 0) return false;
-    if (p->qGroup == 0 || (p->qGroup % 32) != 0) return false;
+    if (p->M <= 64 || p->K == 0 || (p->K % (2 * BK)) != 0) return false;   // even step count
+    if (p->qGroup == 0 || (p->qGroup % 32) != 0) return false;   // a thread's 32 k share a group
     if (int64_t(p->M) * p->K >= (int64_t(1) << 32)) return false;   // 32-bit element offsets
     (void)S;
     return aligned(W, 16) && aligned(X, 16);

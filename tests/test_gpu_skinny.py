@@ -143,8 +143,9 @@ def test_skinny_repeatable_and_kernel_entry(gpu, dgm, orc):
 # ---- large-M reduced-precision path (bf16 MFMA, W dequantized in LDS) -------
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M,N,K,G", [(65, 33, 64, 32), (256, 256, 256, 128), (300, 500, 192, 64),
-                                     (512, 768, 192, 32), (1000, 260, 1024, 128)])
+@pytest.mark.parametrize("M,N,K,G", [(65, 33, 128, 32), (256, 256, 256, 128), (300, 500, 384, 64),
+                                     (512, 768, 768, 32), (1000, 260, 1024, 128),
+                                     (129, 40, 192, 64)])   # K % 128 != 0: fp32 tile path
 def test_bf16_large_m(gpu, dgm, orc, bits, M, N, K, G):
     rng = np.random.default_rng(M + N + K + bits)
     x = rng.standard_normal(M * K).astype(np.float32)
