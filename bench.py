@@ -284,6 +284,37 @@ def bench_c4(b: Bench, reps: int, M: int, math_mode: int) -> dict:
             "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
 
 
+def c3_flops(cfg) -> int:
+    """Linear + attention flop of the looped block forward (src/DiT.swift:520-550)."""
+    M, C, F, KV, T, H, D = cfg.B * cfg.T, cfg.C, cfg.F, cfg.D, cfg.T, cfg.H, cfg.D
+    lin = 2 * M * C * (C + 2 * KV + C + 2 * F) + 2 * M * F * C
+    att = 2 * 2 * cfg.B * H * T * T * D
+    return cfg.loops * (lin + att)
+
+
+def bench_c3(b: Bench, reps: int) -> dict:
+    """c3: the photos-dit looped block forward, 8x64 tokens, 4 loops, int8 G=32
+    linears; weights ~N(0,0.02), norms 1, xs[0] ~N(0,1), all resident. The
+    timed call is the whole 4-loop forward (dgm_dit_forward), in place on x."""
+    dgm = b.dgm
+    cfg = dgm.DiTConfig()
+    w = {n: b.randn(N * K, 0.02) for n, (N, K) in cfg.linear_shapes().items()}
+    for n in dgm.DIT_NORMS:
+        w[n] = b.torch.ones(cfg.C, dtype=b.torch.float32, device="cuda")
+    b.sync()
+    with b.torch.cuda.stream(b.stream):
+        blk = dgm.DiTBlock(b.gpu, cfg, w)
+    x = b.randn(cfg.B * cfg.T * cfg.C, 1.0)
+    ms = b.time_launches(lambda i: blk.forward(x), reps)
+    tokens = cfg.B * cfg.T
+    flops = c3_flops(cfg)
+    return {"kernel": "dit_forward (4 loops)", "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
+            "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
+            "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
+            "note": "launch/latency-bound: ~2.3 GFLOP and ~0.6 MB of weights per forward"}
+
+
 def bench_c5(b: Bench, reps: int, bits: int, math_mode: int) -> dict:
     M, N, K, G = 8192, 14336, 4096, 128
     w = b.randn(N * K, 0.02)
@@ -498,6 +529,7 @@ def main() -> int:
         W = {}
         jobs = [
             ("c1_int8_fwd", lambda: bench_c1(b, args.reps)),
+            ("c3_dit_fwd", lambda: bench_c3(b, 50)),
             ("quant_i4_14336x4096", lambda: bench_quant(b, 20, 4)),
             ("quant_i8_14336x4096", lambda: bench_quant(b, 20, 8)),
             ("c4_int4_m1_fp32", lambda: bench_c4(b, 72, 1, dgm.DGM_MATH_FP32)),

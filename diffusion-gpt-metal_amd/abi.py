@@ -38,9 +38,30 @@ class QuantP(ctypes.Structure):
 
 assert ctypes.sizeof(GemmP) == 32 and ctypes.sizeof(QuantP) == 16
 
+
+class DiTCfg(ctypes.Structure):
+    """dgm_dit_cfg: the DiTConfig fields the loop body reads (src/DiT.swift:9-41)."""
+    _fields_ = ([(n, ctypes.c_int32) for n in ("B", "T", "C", "F", "H", "D", "loops", "group", "bits")]
+                + [("eps", ctypes.c_float), ("mix", ctypes.c_float), ("pad", ctypes.c_int32)])
+
+
+class DiTLinear(ctypes.Structure):
+    """dgm_dit_linear: fp32 weight (bits 32) or codes + scales (bits 8 / 4)."""
+    _fields_ = [("w", ctypes.c_void_p), ("q", ctypes.c_void_p), ("scale", ctypes.c_void_p)]
+
+
+DIT_LINEARS = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+DIT_NORMS = ("n1", "n1b", "n2", "n2b", "nf")
+
+
+class DiTWeights(ctypes.Structure):
+    """dgm_dit_weights: the block's parameters (src/DiT.swift:242-253)."""
+    _fields_ = [(n, DiTLinear) for n in DIT_LINEARS] + [(n, ctypes.c_void_p) for n in DIT_NORMS]
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
+_F = ctypes.c_float
 _GP = ctypes.POINTER(GemmP)
 _QP = ctypes.POINTER(QuantP)
 
@@ -71,6 +92,17 @@ PROTOTYPES = {
     "dgm_gemmDX": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmDW": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
     "dgm_gemmDWAcc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "dgm_rmsFwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _F]),
+    "dgm_ropeFwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_repeatHeads": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_attnFwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I]),
+    "dgm_swigluFwd": (_I, [_P, _P, _P, _P, _I64]),
+    "dgm_add": (_I, [_P, _P, _P, _P, _I64]),
+    "dgm_mix": (_I, [_P, _P, _P, _P, _I64, _F, _F]),
+    "dgm_copy": (_I, [_P, _P, _P, _I64]),
+    "dgm_ropeTables": (_I, [_I64, _I64, _F, _P, _P]),
+    "dgm_dit_workspace_floats": (_I64, [ctypes.POINTER(DiTCfg)]),
+    "dgm_dit_forward": (_I, [_P, ctypes.POINTER(DiTCfg), ctypes.POINTER(DiTWeights), _P, _P, _P, _P, _I64]),
 }
 
 

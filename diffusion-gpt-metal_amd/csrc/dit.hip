@@ -1,0 +1,492 @@
+// Looped DiT block forward (src/DiT.swift:520-550) on gfx950: the block's
+// non-GEMM kernels, their GPU.swift-style C entry points, and the block
+// orchestrator that runs the loops with every linear on the quantized GEMMs.
+//
+// Kernels (semantics of metal/kernels.metal, cited per kernel):
+//  * rmsnorm_fwd: one wave per row, wave-reduced sum of squares.
+//  * rope_fwd, repeat_heads, add_f, mix_f, copy_f, swiglu_fwd: elementwise,
+//    with fp contraction off so each product and sum rounds as in the
+//    reference's separate operations.
+//  * attn_fwd: scores, row softmax and P.V fused in one kernel. A workgroup
+//    owns (batch, head, 16 query rows); the head's K and V rows (of the one
+//    KV head when the caller repeats it, or of any head) stay in LDS, scores
+//    and probabilities of the 16 rows in LDS too. It also writes the scores
+//    and probabilities the reference's API returns.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace dgm {
+int gemm_check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits);
+int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
+                 const float* bias, float* Y, const dgm_GemmP* p);
+}  // namespace dgm
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---- rmsnorm_fwd (metal/kernels.metal:807-825) --------------------------------
+// y = x * rsqrt(mean(x^2) + eps) * w; rstd = rsqrt(mean(x^2) + eps).
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                           float* __restrict__ rstd, const float* __restrict__ w,
+                                                           int rows, int cols, float eps) {
+#pragma clang fp contract(off)
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + size_t(row) * cols;
+    float ss = 0.0f;
+    for (int c = lane; c < cols; c += 64) ss += xr[c] * xr[c];
+    ss = wave_sum(ss);
+    const float mean = ss / float(cols);
+    const float rs = 1.0f / sqrtf(mean + eps);   // correctly rounded divide and sqrt
+    if (lane == 0 && rstd) rstd[row] = rs;
+    float* yr = y + size_t(row) * cols;
+    for (int c = lane; c < cols; c += 64) yr[c] = (xr[c] * rs) * w[c];
+}
+
+// ---- rope_fwd (metal/kernels.metal:871-889): rotate-half, tables [T, D] ----------
+__global__ __launch_bounds__(kThreads) void rope_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                        const float* __restrict__ cosv,
+                                                        const float* __restrict__ sinv, int B, int T, int H,
+                                                        int D) {
+#pragma clang fp contract(off)
+    const int64_t total = int64_t(B) * T * H * D;
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= total) return;
+    const int d = int(i % D);
+    const int mid = D >> 1;
+    const int t = int((i / (int64_t(H) * D)) % T);
+    const float rot = d < mid ? -x[i + mid] : x[i - mid];
+    const float a = x[i] * cosv[t * D + d];
+    const float b = rot * sinv[t * D + d];
+    y[i] = a + b;
+}
+
+// ---- repeat_heads (metal/kernels.metal:980-993): [B,T,D] -> [B,T,H,D] ----------
+__global__ __launch_bounds__(kThreads) void repeat_heads_kernel(const float* __restrict__ src,
+                                                                float* __restrict__ dst, int B, int T, int H,
+                                                                int D) {
+    const int64_t total = int64_t(B) * T * H * D;
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= total) return;
+    const int d = int(i % D);
+    const int64_t bt = i / (int64_t(H) * D);   // b * T + t
+    dst[i] = src[bt * D + d];
+}
+
+// ---- swiglu_fwd (metal/kernels.metal:911-930) ----------------------------------
+__device__ __forceinline__ float silu_sigmoid(float z) {
+#pragma clang fp contract(off)
+    if (z >= 0.0f) {
+        const float e = expf(-z);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(z);
+    return e / (1.0f + e);
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                          float* __restrict__ y, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float z = gate[i];
+    const float a = z * silu_sigmoid(z);
+    y[i] = a * up[i];
+}
+
+// ---- add_f / mix_f / copy_f (metal/kernels.metal:419-427, 951-968) --------------
+__global__ __launch_bounds__(kThreads) void add_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                       float* __restrict__ y, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) y[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(kThreads) void mix_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                       float* __restrict__ y, int64_t n, float ca, float cb) {
+#pragma clang fp contract(off)
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float p = ca * a[i];
+    const float r = cb * b[i];
+    y[i] = p + r;
+}
+
+__global__ __launch_bounds__(kThreads) void copy_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) y[i] = x[i];
+}
+
+// ---- attention (metal/kernels.metal:443-506), fused ------------------------------
+// q, k, v, av: [B, T, H, D]; scores, probs: [B, H, T, T]. scale = 1/sqrt(D).
+// Workgroup = (b, h, 16 query rows). K/V rows of head h in LDS.
+constexpr int kQRows = 16;
+
+__global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                        const float* __restrict__ v, float* __restrict__ scores,
+                                                        float* __restrict__ probs, float* __restrict__ av, int B,
+                                                        int T, int H, int D, float scale, int causal) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float sm[];
+    float* ks = sm;                    // [T][D]
+    float* vs = ks + T * D;            // [T][D]
+    float* qs = vs + T * D;            // [16][D]
+    float* ps = qs + kQRows * D;       // [16][T]
+    const int tblocks = (T + kQRows - 1) / kQRows;
+    const int tb = blockIdx.x % tblocks;
+    const int h = (blockIdx.x / tblocks) % H;
+    const int b = blockIdx.x / (tblocks * H);
+    const int t0 = tb * kQRows;
+    const int nq = min(kQRows, T - t0);
+    const int64_t rowstride = int64_t(H) * D;
+    const float* qb = q + (int64_t(b) * T) * rowstride + int64_t(h) * D;
+    const float* kb = k + (int64_t(b) * T) * rowstride + int64_t(h) * D;
+    const float* vb = v + (int64_t(b) * T) * rowstride + int64_t(h) * D;
+    for (int e = threadIdx.x; e < T * D; e += kThreads) {
+        const int s = e / D, d = e - s * D;
+        ks[e] = kb[int64_t(s) * rowstride + d];
+        vs[e] = vb[int64_t(s) * rowstride + d];
+    }
+    for (int e = threadIdx.x; e < nq * D; e += kThreads) {
+        const int t = e / D, d = e - t * D;
+        qs[e] = qb[int64_t(t0 + t) * rowstride + d];
+    }
+    __syncthreads();
+    // scores: sequential d, then * scale (attn_scores order).
+    for (int e = threadIdx.x; e < nq * T; e += kThreads) {
+        const int t = e / T, s = e - t * T;
+        float acc = 0.0f;
+        for (int d = 0; d < D; ++d) acc += qs[t * D + d] * ks[s * D + d];
+        acc *= scale;
+        if (causal && s > t0 + t) acc = -1.0e30f;
+        ps[e] = acc;
+        scores[((int64_t(b) * H + h) * T + t0 + t) * T + s] = acc;
+    }
+    __syncthreads();
+    // softmax: one wave per row (attn_softmax's max / sum / normalize).
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int t = wave; t < nq; t += kThreads / 64) {
+        float* row = ps + t * T;
+        float mx = -INFINITY;
+        for (int s = lane; s < T; s += 64) mx = fmaxf(mx, row[s]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float sum = 0.0f;
+        for (int s = lane; s < T; s += 64) sum += expf(row[s] - mx);
+        sum = wave_sum(sum);
+        const float inv = 1.0f / sum;
+        for (int s = lane; s < T; s += 64) {
+            const float pv = expf(row[s] - mx) * inv;
+            row[s] = pv;
+            probs[((int64_t(b) * H + h) * T + t0 + t) * T + s] = pv;
+        }
+    }
+    __syncthreads();
+    // av = probs . v, sequential s (attn_av order).
+    for (int e = threadIdx.x; e < nq * D; e += kThreads) {
+        const int t = e / D, d = e - t * D;
+        float acc = 0.0f;
+        for (int s = 0; s < T; ++s) acc += ps[t * T + s] * vs[s * D + d];
+        av[(int64_t(b) * T + t0 + t) * rowstride + int64_t(h) * D + d] = acc;
+    }
+}
+
+inline unsigned blocks_for(int64_t n) { return unsigned((n + kThreads - 1) / kThreads); }
+
+size_t attn_lds_bytes(int T, int D) {
+    return sizeof(float) * (size_t(2) * T * D + size_t(kQRows) * D + size_t(kQRows) * T);
+}
+
+// Launchers shared by the C entry points and the block orchestrator. They
+// validate only what the kernels index; the entry points add the reference's
+// argument checks.
+int launch_rms(dgm_gpu* g, const float* x, float* y, float* rstd, const float* w, int64_t rows, int64_t cols,
+               float eps) {
+    if (rows == 0 || cols == 0) return DGM_OK;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(unsigned((rows + 3) / 4)), dim3(kThreads), 0, g->stream, x, y, rstd,
+                       w, int(rows), int(cols), eps);
+    return dgm::check_launch(g, "rmsnorm_fwd");
+}
+
+int launch_rope(dgm_gpu* g, const float* x, float* y, const float* c, const float* s, int B, int T, int H, int D) {
+    const int64_t n = int64_t(B) * T * H * D;
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, x, y, c, s, B, T, H, D);
+    return dgm::check_launch(g, "rope_fwd");
+}
+
+int launch_repeat(dgm_gpu* g, const float* src, float* dst, int B, int T, int H, int D) {
+    const int64_t n = int64_t(B) * T * H * D;
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(repeat_heads_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, src, dst, B, T, H,
+                       D);
+    return dgm::check_launch(g, "repeat_heads");
+}
+
+int launch_attn(dgm_gpu* g, const float* q, const float* k, const float* v, float* scores, float* probs,
+                float* av, int B, int T, int H, int D, int causal) {
+    if (int64_t(B) * T * H * D == 0) return DGM_OK;
+    const size_t lds = attn_lds_bytes(T, D);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "attn_fwd: cannot reserve %zu bytes of LDS: %s", lds,
+                             hipGetErrorString(e));
+    }
+    const int tblocks = (T + kQRows - 1) / kQRows;
+    const float scale = 1.0f / sqrtf(float(D));
+    hipLaunchKernelGGL(attn_kernel, dim3(unsigned(B * H * tblocks)), dim3(kThreads), lds, g->stream, q, k, v,
+                       scores, probs, av, B, T, H, D, scale, causal);
+    return dgm::check_launch(g, "attn_fwd");
+}
+
+int launch_swiglu(dgm_gpu* g, const float* gate, const float* up, float* y, int64_t n) {
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, gate, up, y, n);
+    return dgm::check_launch(g, "swiglu_fwd");
+}
+
+int launch_add(dgm_gpu* g, const float* a, const float* b, float* y, int64_t n) {
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a, b, y, n);
+    return dgm::check_launch(g, "add_f");
+}
+
+int launch_mix(dgm_gpu* g, const float* a, const float* b, float* y, int64_t n, float ca, float cb) {
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(mix_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a, b, y, n, ca, cb);
+    return dgm::check_launch(g, "mix_f");
+}
+
+int launch_copy(dgm_gpu* g, const float* x, float* y, int64_t n) {
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, x, y, n);
+    return dgm::check_launch(g, "copy_f");
+}
+
+bool bad_count(int64_t n) { return n < 0 || n > (int64_t(1) << 40); }
+
+int check_bthd(dgm_gpu* g, const char* name, int64_t B, int64_t T, int64_t H, int64_t D) {
+    if (B < 0 || T < 0 || H < 0 || D < 0 || B > dgm::kMaxIndex || T > dgm::kMaxIndex || H > dgm::kMaxIndex ||
+        D > dgm::kMaxIndex || B * T * H * D > (int64_t(1) << 40))
+        return dgm::fail(g, DGM_ERR_ARG, "%s: bad sizes B=%lld T=%lld H=%lld D=%lld", name, (long long)B,
+                         (long long)T, (long long)H, (long long)D);
+    return DGM_OK;
+}
+
+// ---- the block orchestrator (src/DiT.swift:520-550) ---------------------------------
+
+enum Buf { LN1, QPRE, KPRE, VPRE, VFIRST, VMIX, Q, KROT, KH, VH, SCORES, PROBS, AV, ATTN, T1, MID, LN2, GATE,
+           UP, SW, MLP, PRE, RSTD, NBUF };
+
+void dit_sizes(const dgm_dit_cfg* c, int64_t* sz) {
+    const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
+    const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
+    const int64_t s[NBUF] = {M * C, M * C, M * KV, M * KV, M * KV, M * KV, M * C, M * KV, M * C, M * C,
+                             att,   att,   M * C,  M * C,  M * C,  M * C,  M * C, M * F,  M * F, M * F,
+                             M * C, M * C, M};
+    for (int i = 0; i < NBUF; ++i) sz[i] = s[i];
+}
+
+int64_t dit_workspace_floats(const dgm_dit_cfg* c) {
+    int64_t sz[NBUF], total = 0;
+    dit_sizes(c, sz);
+    for (int i = 0; i < NBUF; ++i) total += (sz[i] + 63) & ~int64_t(63);   // 256-byte aligned pieces
+    return total;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- GPU.swift-style entry points (src/GPU.swift:212-410) -------------------------
+
+int dgm_rmsFwd(dgm_gpu* g, const float* x, float* y, float* rstd, const float* weight, int64_t rows,
+               int64_t cols, float eps) {
+    int rc = dgm::enter(g, "rmsnorm_fwd");
+    if (rc) return rc;
+    if (rows < 0 || cols < 0 || rows > dgm::kMaxIndex || cols > dgm::kMaxIndex || bad_count(rows * cols))
+        return dgm::fail(g, DGM_ERR_ARG, "rmsFwd: bad sizes rows=%lld cols=%lld", (long long)rows, (long long)cols);
+    if (rows && cols && (!x || !y || !weight)) return dgm::fail(g, DGM_ERR_ARG, "rmsFwd: null buffer");
+    return launch_rms(g, x, y, rstd, weight, rows, cols, eps);
+}
+
+int dgm_ropeFwd(dgm_gpu* g, const float* x, float* y, const float* cosv, const float* sinv, int64_t B,
+                int64_t T, int64_t H, int64_t D) {
+    int rc = dgm::enter(g, "rope_fwd");
+    if (rc) return rc;
+    rc = check_bthd(g, "ropeFwd", B, T, H, D);
+    if (rc) return rc;
+    if (D % 2 != 0) return dgm::fail(g, DGM_ERR_SHAPE, "ropeFwd: head dim %lld must be even", (long long)D);
+    if (B * T * H * D && (!x || !y || !cosv || !sinv)) return dgm::fail(g, DGM_ERR_ARG, "ropeFwd: null buffer");
+    return launch_rope(g, x, y, cosv, sinv, int(B), int(T), int(H), int(D));
+}
+
+int dgm_repeatHeads(dgm_gpu* g, const float* src, float* dst, int64_t B, int64_t T, int64_t H, int64_t D) {
+    int rc = dgm::enter(g, "repeat_heads");
+    if (rc) return rc;
+    rc = check_bthd(g, "repeatHeads", B, T, H, D);
+    if (rc) return rc;
+    if (B * T * H * D && (!src || !dst)) return dgm::fail(g, DGM_ERR_ARG, "repeatHeads: null buffer");
+    return launch_repeat(g, src, dst, int(B), int(T), int(H), int(D));
+}
+
+int dgm_attnFwd(dgm_gpu* g, const float* q, const float* k, const float* v, float* scores, float* probs,
+                float* av, int64_t B, int64_t T, int64_t H, int64_t D, int causal) {
+    int rc = dgm::enter(g, "attn_fwd");
+    if (rc) return rc;
+    rc = check_bthd(g, "attnFwd", B, T, H, D);
+    if (rc) return rc;
+    if (B * T * H * D && (!q || !k || !v || !scores || !probs || !av))
+        return dgm::fail(g, DGM_ERR_ARG, "attnFwd: null buffer");
+    if (attn_lds_bytes(int(T), int(D)) > 160 * 1024)
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "attnFwd: T*D = %lld exceeds the LDS-resident kernel",
+                         (long long)(T * D));
+    return launch_attn(g, q, k, v, scores, probs, av, int(B), int(T), int(H), int(D), causal ? 1 : 0);
+}
+
+int dgm_swigluFwd(dgm_gpu* g, const float* gate, const float* up, float* y, int64_t n) {
+    int rc = dgm::enter(g, "swiglu_fwd");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "swigluFwd: bad count");
+    if (n && (!gate || !up || !y)) return dgm::fail(g, DGM_ERR_ARG, "swigluFwd: null buffer");
+    return launch_swiglu(g, gate, up, y, n);
+}
+
+int dgm_add(dgm_gpu* g, const float* a, const float* b, float* y, int64_t n) {
+    int rc = dgm::enter(g, "add_f");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "add: bad count");
+    if (n && (!a || !b || !y)) return dgm::fail(g, DGM_ERR_ARG, "add: null buffer");
+    return launch_add(g, a, b, y, n);
+}
+
+int dgm_mix(dgm_gpu* g, const float* a, const float* b, float* y, int64_t n, float ca, float cb) {
+    int rc = dgm::enter(g, "mix_f");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "mix: bad count");
+    if (n && (!a || !b || !y)) return dgm::fail(g, DGM_ERR_ARG, "mix: null buffer");
+    return launch_mix(g, a, b, y, n, ca, cb);
+}
+
+int dgm_copy(dgm_gpu* g, const float* x, float* y, int64_t n) {
+    int rc = dgm::enter(g, "copy_f");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "copy: bad count");
+    if (n && (!x || !y)) return dgm::fail(g, DGM_ERR_ARG, "copy: null buffer");
+    return launch_copy(g, x, y, n);
+}
+
+// ---- ropeTables (src/Macro.swift:509-530), host side --------------------------------
+
+int dgm_ropeTables(int64_t maxT, int64_t dim, float theta, float* cos_t, float* sin_t) {
+    if (maxT < 0 || dim < 0 || dim % 2 != 0 || maxT > dgm::kMaxIndex || dim > dgm::kMaxIndex ||
+        maxT * dim > (int64_t(1) << 40))
+        return DGM_ERR_ARG;
+    if (maxT * dim == 0) return DGM_OK;
+    if (!cos_t || !sin_t) return DGM_ERR_ARG;
+    const int64_t half = dim / 2;
+    for (int64_t t = 0; t < maxT; ++t) {
+        for (int64_t i = 0; i < half; ++i) {
+            const float e = float(2 * i) / float(dim);
+            const float inv = ::powf(theta, -e);
+            const float f = float(t) * inv;
+            const float c = ::cosf(f), s = ::sinf(f);
+            cos_t[t * dim + i] = c;
+            cos_t[t * dim + i + half] = c;
+            sin_t[t * dim + i] = s;
+            sin_t[t * dim + i + half] = s;
+        }
+    }
+    return DGM_OK;
+}
+
+// ---- block forward ------------------------------------------------------------------
+
+int64_t dgm_dit_workspace_floats(const dgm_dit_cfg* c) { return c ? dit_workspace_floats(c) : -1; }
+
+int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
+                    const float* sinv, float* x, float* ws, int64_t ws_floats) {
+    int rc = dgm::enter(g, "dit_forward");
+    if (rc) return rc;
+    if (!c || !w || !x || !ws || !cosv || !sinv) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: null argument");
+    if (c->bits != 4 && c->bits != 8 && c->bits != 32)
+        return dgm::fail(g, DGM_ERR_BITS, "dit_forward: unsupported bits %d", c->bits);
+    if (c->B <= 0 || c->T <= 0 || c->C <= 0 || c->F <= 0 || c->H <= 0 || c->D <= 0 || c->loops < 0 ||
+        c->H * c->D != c->C || c->D % 2 != 0)
+        return dgm::fail(g, DGM_ERR_SHAPE, "dit_forward: bad config (C must be H*D, D even)");
+    if (c->bits != 32 && (c->group <= 0 || c->C % c->group != 0 || c->F % c->group != 0 ||
+                          (c->bits == 4 && c->group % 2 != 0)))
+        return dgm::fail(g, DGM_ERR_SHAPE, "dit_forward: C and F must be multiples of an (even for int4) group");
+    if (attn_lds_bytes(c->T, c->D) > 160 * 1024)
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: T*D too large for the attention kernel");
+    if (ws_floats < dit_workspace_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: workspace too small");
+
+    int64_t sz[NBUF];
+    float* p[NBUF];
+    dit_sizes(c, sz);
+    float* cur = ws;
+    for (int i = 0; i < NBUF; ++i) {
+        p[i] = cur;
+        cur += (sz[i] + 63) & ~int64_t(63);
+    }
+    const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
+    const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D;
+
+    auto gemm = [&](const dgm_dit_linear& L, const float* in, float* out, int64_t N, int64_t K) -> int {
+        dgm_GemmP gp{uint32_t(M), uint32_t(N), uint32_t(K), 0u, uint32_t(bits == 32 ? 0 : G), 0, 0, 0};
+        int r = dgm::gemm_check_sizes(g, "dit_forward", &gp, bits);
+        if (r) return r;
+        const void* wt = bits == 32 ? static_cast<const void*>(L.w) : L.q;
+        if (!wt || (bits != 32 && !L.scale)) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: null weight");
+        r = dgm::gemm_f32_fwd(g, bits, wt, L.scale, in, nullptr, out, &gp);
+        if (r) return r;
+        return dgm::check_launch(g, "dit_forward gemm");
+    };
+#define DGM_TRY(expr)              \
+    do {                           \
+        int _r = (expr);           \
+        if (_r != DGM_OK) return _r; \
+    } while (0)
+    for (int loop = 0; loop < c->loops; ++loop) {
+        DGM_TRY(launch_rms(g, x, p[LN1], p[RSTD], w->n1, M, C, c->eps));
+        DGM_TRY(gemm(w->wq, p[LN1], p[QPRE], C, C));
+        DGM_TRY(gemm(w->wk, p[LN1], p[KPRE], KV, C));
+        DGM_TRY(gemm(w->wv, p[LN1], p[VPRE], KV, C));
+        if (loop == 0) {
+            DGM_TRY(launch_copy(g, p[VPRE], p[VFIRST], M * KV));
+            DGM_TRY(launch_repeat(g, p[VPRE], p[VH], B, T, H, D));
+        } else {
+            DGM_TRY(launch_mix(g, p[VPRE], p[VFIRST], p[VMIX], M * KV, 1.0f - c->mix, c->mix));
+            DGM_TRY(launch_repeat(g, p[VMIX], p[VH], B, T, H, D));
+        }
+        DGM_TRY(launch_rope(g, p[QPRE], p[Q], cosv, sinv, B, T, H, D));
+        DGM_TRY(launch_rope(g, p[KPRE], p[KROT], cosv, sinv, B, T, 1, D));
+        DGM_TRY(launch_repeat(g, p[KROT], p[KH], B, T, H, D));
+        DGM_TRY(launch_attn(g, p[Q], p[KH], p[VH], p[SCORES], p[PROBS], p[AV], B, T, H, D, 0));
+        DGM_TRY(gemm(w->wo, p[AV], p[ATTN], C, C));
+        DGM_TRY(launch_rms(g, p[ATTN], p[T1], p[RSTD], w->n1b, M, C, c->eps));
+        DGM_TRY(launch_add(g, x, p[T1], p[MID], M * C));
+        DGM_TRY(launch_rms(g, p[MID], p[LN2], p[RSTD], w->n2, M, C, c->eps));
+        DGM_TRY(gemm(w->wgate, p[LN2], p[GATE], F, C));
+        DGM_TRY(gemm(w->wup, p[LN2], p[UP], F, C));
+        DGM_TRY(launch_swiglu(g, p[GATE], p[UP], p[SW], M * F));
+        DGM_TRY(gemm(w->wdown, p[SW], p[MLP], C, F));
+        DGM_TRY(launch_rms(g, p[MLP], p[T1], p[RSTD], w->n2b, M, C, c->eps));
+        DGM_TRY(launch_add(g, p[MID], p[T1], p[PRE], M * C));
+        DGM_TRY(launch_rms(g, p[PRE], x, p[RSTD], w->nf, M, C, c->eps));
+    }
+#undef DGM_TRY
+    return DGM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,146 @@
+"""Host side of the looped DiT block forward (src/DiT.swift:505-550) over the C ABI.
+
+DiTBlock holds the block's linears quantized once on the device
+(GPU.quantize, src/GPU.swift:220-225), device copies of the RoPE tables
+(ropeTables, src/Macro.swift:509-530, computed on the host as the reference
+does) and the forward's workspace. forward() enqueues the whole loop body
+(dgm_dit_forward) on the context's stream: nothing is allocated and nothing
+waits on the host, so the call can be captured into a HIP graph.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict
+
+import numpy as np
+
+from .abi import DIT_LINEARS, DIT_NORMS, DgmError, DiTCfg, DiTLinear, DiTWeights, load_library
+from .gpu import GPU, _ptr
+
+
+@dataclass
+class DiTConfig:
+    """The DiTConfig fields the block forward reads (src/DiT.swift:9-41).
+    Defaults are the photos-dit block: 8 x 64 tokens, embd 192, 4 heads of 48
+    with one KV head, SwiGLU 768, eps 1e-6, theta 1e4, mix 0.5, 4 loops."""
+    B: int = 8
+    T: int = 64
+    C: int = 192
+    F: int = 768
+    H: int = 4
+    D: int = 48
+    loops: int = 4
+    group: int = 32
+    bits: int = 8
+    eps: float = 1e-6
+    theta: float = 1e4
+    mix: float = 0.5
+
+    def linear_shapes(self) -> Dict[str, tuple]:
+        """[N, K] of each linear (src/DiT.swift:242-248); KV width = D."""
+        C, F, KV = self.C, self.F, self.D
+        return {"wq": (C, C), "wk": (KV, C), "wv": (KV, C), "wo": (C, C),
+                "wgate": (F, C), "wup": (F, C), "wdown": (C, F)}
+
+    def c_cfg(self) -> DiTCfg:
+        return DiTCfg(self.B, self.T, self.C, self.F, self.H, self.D, self.loops, self.group, self.bits,
+                      self.eps, self.mix, 0)
+
+
+def rope_tables(maxT: int, dim: int, theta: float):
+    """ropeTables (src/Macro.swift:509-530) on the host: (cos, sin), each a
+    float32 array of maxT * dim."""
+    lib = load_library()
+    cos = np.zeros(max(maxT * dim, 1), dtype=np.float32)
+    sin = np.zeros(max(maxT * dim, 1), dtype=np.float32)
+    rc = lib.dgm_ropeTables(maxT, dim, theta, cos.ctypes.data, sin.ctypes.data)
+    if rc != 0:
+        raise DgmError(rc, f"ropeTables: bad sizes maxT={maxT} dim={dim}")
+    return cos[: maxT * dim], sin[: maxT * dim]
+
+
+class DiTBlock:
+    """The shared block of a looped DiT with quantized linears.
+
+    weights: fp32 device tensors keyed by DIT_LINEARS ([N, K] row-major) and
+    DIT_NORMS ([C]). With bits 8 / 4 each linear is quantized once on the
+    device; with bits 32 the fp32 weights are used as they are.
+    """
+
+    def __init__(self, gpu: GPU, cfg: DiTConfig, weights: Dict[str, object]):
+        import torch
+        self.gpu, self.cfg = gpu, cfg
+        if cfg.bits not in (4, 8, 32):
+            raise DgmError(5, f"unsupported bits {cfg.bits}")
+        self.keep = []
+        self.codes: Dict[str, object] = {}
+        self.scales: Dict[str, object] = {}
+        lin = {}
+        gpu.begin()
+        for name in DIT_LINEARS:
+            N, K = cfg.linear_shapes()[name]
+            w = weights[name]
+            if w.numel() != N * K or w.dtype != torch.float32 or not w.is_cuda:
+                raise ValueError(f"{name}: expected {N}x{K} fp32 device tensor")
+            w = w.contiguous()
+            self.keep.append(w)
+            if cfg.bits == 32:
+                lin[name] = DiTLinear(_ptr(w), None, None)
+                continue
+            nbytes = N * K // 2 if cfg.bits == 4 else N * K
+            q = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=w.device)
+            s = torch.zeros(max(N * (K // cfg.group), 1), dtype=torch.float32, device=w.device)
+            gpu.quantize(w, q, s, N, K, cfg.bits, cfg.group)
+            self.codes[name], self.scales[name] = q, s
+            lin[name] = DiTLinear(None, _ptr(q), _ptr(s))
+        gpu.end()
+        norms = {}
+        for name in DIT_NORMS:
+            w = weights[name].contiguous()
+            if w.numel() != cfg.C or w.dtype != torch.float32 or not w.is_cuda:
+                raise ValueError(f"{name}: expected {cfg.C} fp32 device tensor")
+            self.keep.append(w)
+            norms[name] = _ptr(w)
+        self.c = cfg.c_cfg()
+        self.w = DiTWeights(*[lin[n] for n in DIT_LINEARS], *[norms[n] for n in DIT_NORMS])
+        cos, sin = rope_tables(cfg.T, cfg.D, cfg.theta)
+        dev = self.keep[0].device
+        self.cos = torch.from_numpy(cos).to(dev)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.ws_floats = gpu.dit_workspace_floats(self.c)
+        if self.ws_floats < 0:
+            raise DgmError(1, "dit workspace size")
+        self.ws = torch.zeros(self.ws_floats, dtype=torch.float32, device=dev)
+
+    def forward(self, x) -> None:
+        """xs[0] -> xs[loops] in place; x is a [B*T*C] fp32 device tensor.
+        Must be called inside begin()/end() of the block's GPU."""
+        cfg = self.cfg
+        if x.numel() != cfg.B * cfg.T * cfg.C or not x.is_contiguous():
+            raise ValueError("x must be a contiguous [B*T, C] tensor")
+        self.gpu.dit_forward(self.c, self.w, self.cos, self.sin, x, self.ws, self.ws_floats)
+
+    def workspace_view(self, name: str):
+        """The last loop's intermediate `name` (scores, probs, ...) as a view of
+        the workspace, in the order dgm_dit_forward lays them out."""
+        sizes = _ws_sizes(self.cfg)
+        off = 0
+        for n, sz in sizes:
+            if n == name:
+                return self.ws[off:off + sz]
+            off += (sz + 63) & ~63
+        raise KeyError(name)
+
+
+def _ws_sizes(cfg: DiTConfig):
+    M, C, F, KV = cfg.B * cfg.T, cfg.C, cfg.F, cfg.D
+    att = cfg.B * cfg.H * cfg.T * cfg.T
+    names = ["ln1", "qpre", "kpre", "vpre", "vfirst", "vmix", "q", "krot", "k", "v", "scores", "probs", "av",
+             "attn", "t1", "mid", "ln2", "gate", "up", "sw", "mlp", "pre", "rstd"]
+    sizes = [M * C, M * C, M * KV, M * KV, M * KV, M * KV, M * C, M * KV, M * C, M * C, att, att, M * C,
+             M * C, M * C, M * C, M * C, M * F, M * F, M * F, M * C, M * C, M]
+    return list(zip(names, sizes))
+
+
+__all__ = ["DiTConfig", "DiTBlock", "rope_tables", "DIT_LINEARS", "DIT_NORMS"]

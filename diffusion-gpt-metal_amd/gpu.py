@@ -12,8 +12,8 @@ from __future__ import annotations
 import ctypes
 from typing import Any, Optional
 
-from .abi import (DGM_MATH_BF16, DGM_MATH_FP32, DgmError, GemmP, QuantP,
-                  load_library)
+from .abi import (DGM_MATH_BF16, DGM_MATH_FP32, DgmError, DiTCfg, DiTWeights,
+                  GemmP, QuantP, load_library)
 
 
 def _ptr(t: Any) -> Optional[int]:
@@ -117,6 +117,40 @@ class GPU:
 
     def gemmDWAcc(self, dy, x, dw, M: int, N: int, K: int) -> None:
         self._check(self.lib.dgm_gemmDWAcc(self.h, _ptr(dy), _ptr(x), _ptr(dw), M, N, K))
+
+    # -- DiT block wrappers (src/GPU.swift:211-410) ---------------------------
+    def rmsFwd(self, x, y, rstd, weight, rows: int, cols: int, eps: float) -> None:
+        self._check(self.lib.dgm_rmsFwd(self.h, _ptr(x), _ptr(y), _ptr(rstd), _ptr(weight), rows, cols, eps))
+
+    def ropeFwd(self, x, y, cos, sin, B: int, T: int, H: int, D: int) -> None:
+        self._check(self.lib.dgm_ropeFwd(self.h, _ptr(x), _ptr(y), _ptr(cos), _ptr(sin), B, T, H, D))
+
+    def repeatHeads(self, src, dst, B: int, T: int, H: int, D: int) -> None:
+        self._check(self.lib.dgm_repeatHeads(self.h, _ptr(src), _ptr(dst), B, T, H, D))
+
+    def attnFwd(self, q, k, v, scores, probs, av, B: int, T: int, H: int, D: int, causal: bool = True) -> None:
+        """GPU.attnFwd; causal defaults to true as in src/GPU.swift:302-303."""
+        self._check(self.lib.dgm_attnFwd(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(scores), _ptr(probs),
+                                         _ptr(av), B, T, H, D, 1 if causal else 0))
+
+    def swigluFwd(self, gate, up, y, n: int) -> None:
+        self._check(self.lib.dgm_swigluFwd(self.h, _ptr(gate), _ptr(up), _ptr(y), n))
+
+    def add(self, a, b, y, n: int) -> None:
+        self._check(self.lib.dgm_add(self.h, _ptr(a), _ptr(b), _ptr(y), n))
+
+    def mix(self, a, b, y, n: int, ca: float, cb: float) -> None:
+        self._check(self.lib.dgm_mix(self.h, _ptr(a), _ptr(b), _ptr(y), n, ca, cb))
+
+    def copy(self, x, y, n: int) -> None:
+        self._check(self.lib.dgm_copy(self.h, _ptr(x), _ptr(y), n))
+
+    def dit_workspace_floats(self, cfg: DiTCfg) -> int:
+        return int(self.lib.dgm_dit_workspace_floats(ctypes.byref(cfg)))
+
+    def dit_forward(self, cfg: DiTCfg, w: DiTWeights, cos, sin, x, ws, ws_floats: int) -> None:
+        self._check(self.lib.dgm_dit_forward(self.h, ctypes.byref(cfg), ctypes.byref(w), _ptr(cos), _ptr(sin),
+                                             _ptr(x), _ptr(ws), ws_floats))
 
     # -- kernel-level entries (metal/kernels.metal slot order) ----------------
     def quant_i8(self, W, Q, scale, p: QuantP) -> None:

@@ -41,12 +41,14 @@ extern "C" {
 #define DGM_ERR_UNSUPPORTED 6   /* size beyond what a kernel indexes (2^31)   */
 
 /* ---- math modes (dgm_set_math) ------------------------------------------ */
-/* FP32: every GEMM accumulates fp32 products of fp32 operands, like the
- * reference kernels; max relative error vs float64 <= 1e-5.
- * BF16: the quantized forward (gemm_nt_i8 / gemm_nt_i4) with M >= 2 runs on
- * bf16 MFMA (activations rounded to bf16; int8/int4 codes are exact in bf16;
- * fp32 accumulate, fp32 group scale); max relative error <= 1e-2. M == 1
- * stays on the fp32 GEMV. Backward kernels are fp32 in both modes. */
+/* FP32 (default): every result is within max relative error 1e-5 of the
+ * float64 product. Quantized forwards with M <= 64 run on int8 MFMA over an
+ * exact three-piece int8 split of each activation row; the rest accumulate
+ * fp32 products of fp32 operands.
+ * BF16: quantized forwards with M <= 64 use a two-piece split; larger M (with
+ * K % 128 == 0 and qGroup % 32 == 0) runs on bf16 MFMA with activations
+ * rounded to bf16 and weights dequantized to bf16 in LDS, fp32 accumulate.
+ * Max relative error <= 1e-2. Backward kernels are fp32 in both modes. */
 #define DGM_MATH_FP32 0
 #define DGM_MATH_BF16 1
 
@@ -147,6 +149,81 @@ int dgm_gemmDW(dgm_gpu* g, const float* dy, const float* x, float* dw,
 /* GPU.gemmDWAcc (src/GPU.swift:268-272). */
 int dgm_gemmDWAcc(dgm_gpu* g, const float* dy, const float* x, float* dw,
                   int64_t M, int64_t N, int64_t K);
+
+/* ---- looped DiT block forward: the non-GEMM wrappers it calls -------------
+ * Same names, buffer order and sizes as the Swift wrappers; fp32 buffers in
+ * device memory. Layouts: activations [B,T,H,D] (rows of H*D), scores/probs
+ * [B,H,T,T], RoPE tables [T,D]. */
+
+/* GPU.rmsFwd (src/GPU.swift:364-367; rmsnorm_fwd, metal/kernels.metal:807-825):
+ * y = x * rsqrt(mean(x^2) + eps) * weight per row; rstd[row] = that rsqrt
+ * (rstd may be NULL). */
+int dgm_rmsFwd(dgm_gpu* g, const float* x, float* y, float* rstd, const float* weight,
+               int64_t rows, int64_t cols, float eps);
+/* GPU.ropeFwd (src/GPU.swift:375-378; rope_fwd, metal/kernels.metal:871-889):
+ * rotate-half RoPE; D must be even. */
+int dgm_ropeFwd(dgm_gpu* g, const float* x, float* y, const float* cos_t, const float* sin_t,
+                int64_t B, int64_t T, int64_t H, int64_t D);
+/* GPU.repeatHeads (src/GPU.swift:407-410; repeat_heads, metal/kernels.metal:980-993):
+ * dst[b,t,h,:] = src[b,t,:]. */
+int dgm_repeatHeads(dgm_gpu* g, const float* src, float* dst, int64_t B, int64_t T, int64_t H,
+                    int64_t D);
+/* GPU.attnFwd (src/GPU.swift:302-310; attn_scores/attn_softmax/attn_av,
+ * metal/kernels.metal:443-506), one fused kernel: scores = q.k / sqrt(D)
+ * (masked to -1e30 above the diagonal when causal), probs = row softmax,
+ * av = probs.v. Needs (2*T*D + 16*D + 16*T)*4 bytes <= 160 KiB of LDS. */
+int dgm_attnFwd(dgm_gpu* g, const float* q, const float* k, const float* v, float* scores,
+                float* probs, float* av, int64_t B, int64_t T, int64_t H, int64_t D, int causal);
+/* GPU.swigluFwd (src/GPU.swift:385-387; swiglu_fwd, metal/kernels.metal:911-930):
+ * y = gate * sigmoid(gate) * up. */
+int dgm_swigluFwd(dgm_gpu* g, const float* gate, const float* up, float* y, int64_t n);
+/* GPU.add (src/GPU.swift:211-213; add_f, metal/kernels.metal:419-427): y = a + b. */
+int dgm_add(dgm_gpu* g, const float* a, const float* b, float* y, int64_t n);
+/* GPU.mix (src/GPU.swift:393-396; mix_f, metal/kernels.metal:951-959): y = ca*a + cb*b. */
+int dgm_mix(dgm_gpu* g, const float* a, const float* b, float* y, int64_t n, float ca, float cb);
+/* GPU.copy (src/GPU.swift:398-400; copy_f, metal/kernels.metal:961-968): y = x. */
+int dgm_copy(dgm_gpu* g, const float* x, float* y, int64_t n);
+
+/* ropeTables (src/Macro.swift:509-530), host side: fills cos_t/sin_t, each
+ * maxT*dim floats of HOST memory, with cos/sin(t * theta^(-2i/dim)) for
+ * i < dim/2, repeated in both halves of each row. dim must be even. */
+int dgm_ropeTables(int64_t maxT, int64_t dim, float theta, float* cos_t, float* sin_t);
+
+/* The DiT block configuration the loop body reads (src/DiT.swift:9-41):
+ * B sequences of T tokens, embd C = H*D, SwiGLU width F, one KV head of
+ * width D repeated to H heads. bits 8 / 4 route every linear through the
+ * group-quantized forward (group `group`); bits 32 uses the fp32 weights. */
+typedef struct dgm_dit_cfg {
+    int32_t B, T, C, F, H, D, loops, group, bits;
+    float eps, mix;
+    int32_t pad;
+} dgm_dit_cfg;
+
+/* One linear: fp32 weight w [N,K] (bits 32) or codes q + scales (bits 8/4). */
+typedef struct dgm_dit_linear {
+    const float* w;
+    const void* q;
+    const float* scale;
+} dgm_dit_linear;
+
+/* The block's parameters (src/DiT.swift:242-253): wq [C,C], wk/wv [D,C],
+ * wo [C,C], wgate/wup [F,C], wdown [C,F]; RMSNorm weights of C floats. */
+typedef struct dgm_dit_weights {
+    dgm_dit_linear wq, wk, wv, wo, wgate, wup, wdown;
+    const float *n1, *n1b, *n2, *n2b, *nf;
+} dgm_dit_weights;
+
+/* Floats of device workspace dgm_dit_forward needs for cfg (-1 for NULL). */
+int64_t dgm_dit_workspace_floats(const dgm_dit_cfg* cfg);
+/* The looped block forward (src/DiT.swift:520-550): x holds xs[0] [B*T, C] on
+ * entry and xs[loops] on exit. cos_t/sin_t are device copies of
+ * ropeTables(T, D, theta). ws: device workspace of at least
+ * dgm_dit_workspace_floats(cfg) floats; on exit it holds the last loop's
+ * intermediates (scores and probs included). Enqueued on the context's
+ * stream; graph-capturable (no allocation, no host sync). */
+int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w,
+                    const float* cos_t, const float* sin_t, float* x, float* ws,
+                    int64_t ws_floats);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ HEADER = os.path.join(REPO, "include", "dgm_quant.h")
 
 def header_functions():
     text = open(HEADER).read()
-    return set(re.findall(r"^\s*(?:int|void\s*\*?|const char\s*\*)\s*(dgm_\w+)\s*\(", text, re.M))
+    return set(re.findall(r"^\s*(?:int64_t|int|void\s*\*?|const char\s*\*)\s*(dgm_\w+)\s*\(", text, re.M))
 
 
 def test_header_declares_the_reference_surface():
@@ -22,7 +22,10 @@ def test_header_declares_the_reference_surface():
     for n in ["dgm_quant_i8", "dgm_quant_i4", "dgm_gemm_nt_f32", "dgm_gemm_nt_i8", "dgm_gemm_nt_i4",
               "dgm_gemm_dx_f32", "dgm_gemm_dx_i8", "dgm_gemm_dx_i4", "dgm_gemm_dw", "dgm_gemm_dw_acc",
               "dgm_quantize", "dgm_gemmNT", "dgm_gemmDX", "dgm_gemmDW", "dgm_gemmDWAcc",
-              "dgm_begin", "dgm_end", "dgm_last_kernel"]:
+              "dgm_begin", "dgm_end", "dgm_last_kernel",
+              # the DiT loop body's wrappers (src/GPU.swift:211-410) and the block forward
+              "dgm_rmsFwd", "dgm_ropeFwd", "dgm_repeatHeads", "dgm_attnFwd", "dgm_swigluFwd", "dgm_add",
+              "dgm_mix", "dgm_copy", "dgm_ropeTables", "dgm_dit_forward", "dgm_dit_workspace_floats"]:
         assert n in names
 
 
