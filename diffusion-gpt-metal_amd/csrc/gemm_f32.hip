@@ -22,6 +22,8 @@
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const void global_cvoid;
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kThreads = 256;
 constexpr int MODE_FWD = 0, MODE_DX = 1, MODE_DW = 2;
@@ -228,6 +230,401 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs a) {
     }
 }
 
+// ---- deep-prefetch variant ---------------------------------------------------
+// Same products and the same per-wave split into partial tiles, but each wave
+// owns a CONTIGUOUS run of 16-wide contraction chunks and issues the raw loads
+// of up to PF chunks (activations, codes, scales) before converting any of
+// them, so a wave waits for one memory latency per PF chunks instead of one
+// per chunk. Loads are never predicated: row/column indices past the matrix
+// are clamped (their results land in rows/columns that are not stored) and the
+// contraction length is a multiple of 16. Workgroups are numbered XCD-aware:
+// consecutive tiles sharing an operand strip (rows of X or dY for the
+// forward/dX, columns of X for dW) run on one XCD, so that strip is fetched
+// into one L2 instead of eight.
+template <int MODE, int BITS, int TM, int TN, int PF>
+__global__ __launch_bounds__(kThreads) void gemm_deep_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    constexpr int RT = TM / 16, CT = TN / 16;
+    __shared__ float part[4][TM * TN];
+
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_i * tiles_j) return;
+    int ti, tj;
+    if constexpr (MODE == MODE_DW) {
+        tj = t / tiles_i;
+        ti = t - tj * tiles_i;
+    } else {
+        ti = t / tiles_j;
+        tj = t - ti * tiles_j;
+    }
+    const int i0 = ti * TM, j0 = tj * TN;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r16 = lane & 15;
+    const int q4 = lane >> 4;
+
+    int irow[RT], jcol[CT];
+#pragma unroll
+    for (int x = 0; x < RT; ++x) irow[x] = min(i0 + x * 16 + r16, a.rows - 1);
+#pragma unroll
+    for (int y = 0; y < CT; ++y) jcol[y] = min(j0 + y * 16 + r16, a.cols - 1);
+
+    f32x4 acc[RT][CT];
+#pragma unroll
+    for (int x = 0; x < RT; ++x)
+#pragma unroll
+        for (int y = 0; y < CT; ++y) acc[x][y] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nchunks = a.red >> 4;
+    const int cpw = (nchunks + 3) >> 2;
+    const int begin = wave * cpw;
+    const int end = min(nchunks, begin + cpw);
+    const int last = max(0, min(end, nchunks) - 1);
+
+    float ra[PF][RT][4];
+    float rb[PF][CT][4];   // fp32 operand, or codes (as int bits) for quantized W
+    float rs[PF][CT][4];   // per-element scales (DX) / rs[..][0] per-lane scale (FWD)
+
+    for (int base = begin; base < end; base += PF) {
+        // -- issue every load of the round --------------------------------------
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int ch = min(base + u, last);
+            const int c0 = ch * 16 + 4 * q4;
+#pragma unroll
+            for (int x = 0; x < RT; ++x) {
+                if constexpr (MODE == MODE_DW) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) ra[u][x][s] = a.A[size_t(c0 + s) * a.N + irow[x]];
+                } else {
+                    const int ld = MODE == MODE_FWD ? a.K : a.N;
+                    const float4 v = *reinterpret_cast<const float4*>(a.A + size_t(irow[x]) * ld + c0);
+                    ra[u][x][0] = v.x; ra[u][x][1] = v.y; ra[u][x][2] = v.z; ra[u][x][3] = v.w;
+                }
+            }
+#pragma unroll
+            for (int y = 0; y < CT; ++y) {
+                const int j = jcol[y];
+                if constexpr (MODE == MODE_FWD) {
+                    const size_t idx = size_t(j) * a.K + c0;
+                    if constexpr (BITS == 32) {
+                        const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(a.B) + idx);
+                        rb[u][y][0] = v.x; rb[u][y][1] = v.y; rb[u][y][2] = v.z; rb[u][y][3] = v.w;
+                    } else {
+                        uint32_t w;
+                        if constexpr (BITS == 8)
+                            w = *reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(a.B) + idx);
+                        else
+                            w = *reinterpret_cast<const uint16_t*>(static_cast<const uint8_t*>(a.B) + (idx >> 1));
+                        rb[u][y][0] = __uint_as_float(w);
+                        rs[u][y][0] = a.scale[size_t(j) * a.groups + c0 / a.G];
+                    }
+                } else if constexpr (MODE == MODE_DX) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const size_t idx = size_t(c0 + s) * a.K + j;
+                        if constexpr (BITS == 32) {
+                            rb[u][y][s] = static_cast<const float*>(a.B)[idx];
+                        } else {
+                            const uint32_t w = BITS == 8 ? uint32_t(static_cast<const uint8_t*>(a.B)[idx])
+                                                         : uint32_t(static_cast<const uint8_t*>(a.B)[idx >> 1]);
+                            rb[u][y][s] = __uint_as_float(w);
+                            rs[u][y][s] = a.scale[size_t(c0 + s) * a.groups + j / a.G];
+                        }
+                    }
+                } else {
+                    const float* X = static_cast<const float*>(a.B);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) rb[u][y][s] = X[size_t(c0 + s) * a.K + j];
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // -- convert and multiply, chunk by chunk in issue order ------------------
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            if (base + u >= end) continue;
+            float bv[CT][4];
+#pragma unroll
+            for (int y = 0; y < CT; ++y) {
+                if constexpr (BITS == 32) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) bv[y][s] = rb[u][y][s];
+                } else if constexpr (MODE == MODE_FWD) {
+                    const uint32_t w = __float_as_uint(rb[u][y][0]);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        int c;
+                        if constexpr (BITS == 8) {
+                            c = int(int8_t((w >> (8 * s)) & 0xFF));
+                        } else {
+                            const int nib = int((w >> (4 * s)) & 0xF);
+                            c = nib >= 8 ? nib - 16 : nib;
+                        }
+                        bv[y][s] = float(c) * rs[u][y][0];
+                    }
+                } else {
+                    // DX: element s is row n = c0 + s of W at column j.
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const uint32_t w = __float_as_uint(rb[u][y][s]);
+                        int c;
+                        if constexpr (BITS == 8) {
+                            c = int(int8_t(w & 0xFF));
+                        } else {
+                            const int nib = int((jcol[y] & 1) ? (w >> 4) : (w & 0xF));
+                            c = nib >= 8 ? nib - 16 : nib;
+                        }
+                        bv[y][s] = float(c) * rs[u][y][s];
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int x = 0; x < RT; ++x)
+#pragma unroll
+                    for (int y = 0; y < CT; ++y)
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[u][x][s], bv[y][s], acc[x][y], 0, 0, 0);
+        }
+    }
+
+#pragma unroll
+    for (int x = 0; x < RT; ++x)
+#pragma unroll
+        for (int y = 0; y < CT; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                part[wave][(x * 16 + 4 * q4 + r) * TN + y * 16 + r16] = acc[x][y][r];
+    __syncthreads();
+
+    for (int e = threadIdx.x; e < TM * TN; e += kThreads) {
+        const int i = i0 + e / TN;
+        const int j = j0 + e % TN;
+        if (i >= a.rows || j >= a.cols) continue;
+        float v = part[0][e];
+        v += part[1][e];
+        v += part[2][e];
+        v += part[3][e];
+        float* o = a.out + size_t(i) * a.cols + j;
+        if constexpr (MODE == MODE_FWD) {
+            if (a.has_bias) v += a.bias[j];
+            *o = v;
+        } else if constexpr (MODE == MODE_DW) {
+            if (a.accumulate) *o += v;
+            else *o = v;
+        } else {
+            *o = v;
+        }
+    }
+}
+
+template <int MODE, int BITS, int TM, int TN, int PF>
+void launch_deep_tile(const GemmArgs& a, hipStream_t st) {
+    const int ti = int(dgm::ceil_div(a.rows, TM)), tj = int(dgm::ceil_div(a.cols, TN));
+    const int64_t nt = int64_t(ti) * tj;
+    const int per = int((nt + 7) / 8);
+    hipLaunchKernelGGL((gemm_deep_kernel<MODE, BITS, TM, TN, PF>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st,
+                       a, ti, tj, per);
+}
+
+// The deep variant needs a contraction that is a multiple of 16, 16-byte
+// aligned activation rows for the forward/dX, and (quantized forward) a group
+// that is a multiple of 4 so each lane's 4 consecutive weights share a scale.
+template <int MODE>
+bool deep_ok(const GemmArgs& a, int bits, bool vec) {
+    if (a.red % 16 != 0 || a.red == 0 || a.rows == 0 || a.cols == 0) return false;
+    if (int64_t(a.rows) * dgm::ceil_div(a.cols, 16) > (int64_t(1) << 30)) return false;
+    if (MODE == MODE_FWD) return vec && (bits == 32 || a.G % 4 == 0);
+    if (MODE == MODE_DX) return vec;
+    return true;
+}
+
+template <int MODE, int BITS>
+void launch_deep(const GemmArgs& a, int num_cus, hipStream_t st) {
+    const int64_t t32 = int64_t(dgm::ceil_div(a.rows, 32)) * dgm::ceil_div(a.cols, 32);
+    const int64_t t16x32 = int64_t(dgm::ceil_div(a.rows, 16)) * dgm::ceil_div(a.cols, 32);
+    if (t32 >= 2 * num_cus)
+        launch_deep_tile<MODE, BITS, 32, 32, 6>(a, st);
+    else if (t16x32 >= 2 * num_cus)
+        launch_deep_tile<MODE, BITS, 16, 32, 8>(a, st);
+    else
+        launch_deep_tile<MODE, BITS, 16, 16, 12>(a, st);
+}
+
+// ---- LDS-staged forward for short contractions (K <= 1024, K % 64 == 0) -------
+// The latency-bound shapes of the DiT linears. A workgroup owns 16 rows of Y
+// and 16*(4/KS) columns: its 16 x K block of X is read once with fully
+// coalesced 16-byte loads (each wave instruction covers 1 KB of whole rows)
+// and parked in LDS; every wave then reads it back in MFMA layout. Waves are
+// arranged KS (contraction parts) x 4/KS (16-column groups). Within a stage of
+// 64 contraction indices, lane (r, q) multiplies indices 16q .. 16q+15 (chunk c
+// of the stage uses 16q + 4c .. 16q + 4c + 3), so each lane's weight codes for
+// a stage are ONE contiguous 8-byte (int4) / 16-byte (int8) load and one
+// scale, instead of four 16-row gathers. X in LDS is stored with the 16-byte
+// slot index XOR-ed by (row & 15): the 16 rows read by one MFMA operand fetch
+// land in 16 distinct slots, free of bank conflicts. Contraction parts are
+// reduced through LDS in a fixed order.
+template <int BITS, int KS>
+__global__ __launch_bounds__(kThreads) void gemm_fwd_lds_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    constexpr int NS = 4 / KS;
+    constexpr int TN = 16 * NS;
+    extern __shared__ __align__(16) float4 xs[];   // [16][K/4] slots, swizzled
+
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_i * tiles_j) return;
+    const int ti = t / tiles_j, tj = t - ti * tiles_j;
+    const int i0 = ti * 16, j0 = tj * TN;
+    const int K = a.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int wk = wave % KS, wn = wave / KS;
+    const int nst = K >> 6;
+
+    // -- weight codes + scales of this wave's stages (issued first; they are
+    // consumed last, after X has been staged).
+    constexpr int MAXST = (BITS == 32 ? 8 : 16) / KS;   // K <= 1024 (512 for fp32 weights)
+    const int n = min(j0 + wn * 16 + r16, a.cols - 1);
+    uint32_t wc[MAXST][BITS == 4 ? 2 : 4];
+    float4 wf[MAXST][BITS == 32 ? 4 : 1];
+    float sc[MAXST];
+#pragma unroll
+    for (int u = 0; u < MAXST; ++u) {
+        const int st = wk + u * KS;
+        if (st >= nst) continue;   // wave-uniform; these loads are only read after the barrier
+        const int k = st * 64 + 16 * q4;
+        if constexpr (BITS == 32) {
+            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.B) + size_t(n) * K + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wf[u][e] = p[e];
+        } else if constexpr (BITS == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.B) + size_t(n) * K + k);
+            wc[u][0] = v.x; wc[u][1] = v.y; wc[u][2] = v.z; wc[u][3] = v.w;
+            sc[u] = a.scale[size_t(n) * a.groups + k / a.G];
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.B) + ((size_t(n) * K + k) >> 1));
+            wc[u][0] = v.x; wc[u][1] = v.y;
+            sc[u] = a.scale[size_t(n) * a.groups + k / a.G];
+        }
+    }
+
+    // -- X block: 16 rows x K floats straight into LDS (global_load_lds, 16 B
+    // per lane; a wave instruction fills 1 KB of LDS in lane order). LDS slot
+    // (row, pos) receives the row's global slot pos ^ (row & 15).
+    const int spr = K >> 2;                   // 16-byte slots per row
+    const int ninst = (16 * spr) >> 6;        // wave instructions for the block
+    uint8_t* xb = reinterpret_cast<uint8_t*>(xs);
+    for (int ii = wave; ii < ninst; ii += 4) {
+        const int L = ii * 64 + lane;
+        const int row = L / spr, pos = L - row * spr;
+        const int gr = min(i0 + row, a.rows - 1);
+        const float* src = a.A + size_t(gr) * K + ((pos ^ (row & 15)) << 2);
+        __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(xb + ii * 1024), 16, 0, 0);
+    }
+    __syncthreads();
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < MAXST; ++u) {
+        const int st = wk + u * KS;
+        if (st >= nst) break;
+        const float4* xrow = xs + r16 * spr;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 xv = xrow[(st * 16 + 4 * q4 + c) ^ r16];
+            float bv[4];
+            if constexpr (BITS == 32) {
+                const float4 w = wf[u][c];
+                bv[0] = w.x; bv[1] = w.y; bv[2] = w.z; bv[3] = w.w;
+            } else if constexpr (BITS == 8) {
+                const uint32_t w = wc[u][c];
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(int8_t((w >> (8 * s2)) & 0xFF))) * sc[u];
+            } else {
+                const uint32_t w = wc[u][c >> 1] >> (16 * (c & 1));
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    const int nib = int((w >> (4 * s2)) & 0xF);
+                    bv[s2] = float(nib >= 8 ? nib - 16 : nib) * sc[u];
+                }
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, bv[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, bv[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, bv[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, bv[3], acc, 0, 0, 0);
+        }
+    }
+
+    // -- reduce contraction parts in order and store. acc: rows 4*q4 + r, column r16.
+    if constexpr (KS == 1) {
+        const int j = j0 + wn * 16 + r16;
+        if (j < a.cols) {
+            const float bb = a.has_bias ? a.bias[j] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = i0 + 4 * q4 + r;
+                if (i < a.rows) {
+                    float v = acc[r];
+                    if (a.has_bias) v += bb;
+                    a.out[size_t(i) * a.cols + j] = v;
+                }
+            }
+        }
+    } else {
+        __syncthreads();   // X no longer read: reuse LDS for the partial tiles
+        float* part = reinterpret_cast<float*>(xs);   // [KS][16][TN]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[(wk * 16 + 4 * q4 + r) * TN + wn * 16 + r16] = acc[r];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 16 * TN; e += kThreads) {
+            const int i = i0 + e / TN, j = j0 + e % TN;
+            if (i >= a.rows || j >= a.cols) continue;
+            float v = part[e];
+#pragma unroll
+            for (int p2 = 1; p2 < KS; ++p2) v += part[p2 * 16 * TN + e];
+            if (a.has_bias) v += a.bias[j];
+            a.out[size_t(i) * a.cols + j] = v;
+        }
+    }
+}
+
+template <int BITS, int KS>
+void launch_fwd_lds_ks(const GemmArgs& a, hipStream_t st) {
+    constexpr int TN = 16 * (4 / KS);
+    const int ti = int(dgm::ceil_div(a.rows, 16)), tj = int(dgm::ceil_div(a.cols, TN));
+    const int64_t nt = int64_t(ti) * tj;
+    const int per = int((nt + 7) / 8);
+    const size_t lds = size_t(16) * a.K * sizeof(float);
+    hipLaunchKernelGGL((gemm_fwd_lds_kernel<BITS, KS>), dim3(unsigned(per) * 8u), dim3(kThreads), lds, st, a, ti, tj,
+                       per);
+}
+
+// K % 64 == 0 and K <= 1024 (the X block stays in LDS; 512 with fp32
+// weights, which take 16 registers per stage), a group that is a
+// multiple of 16 (one scale per lane per stage), 16-byte aligned rows.
+bool fwd_lds_ok(const GemmArgs& a, int bits, const void* X, const void* W) {
+    if (a.K % 64 != 0 || a.K == 0 || a.K > 1024 || a.rows == 0 || a.cols == 0) return false;
+    if (!dgm::aligned(X, 16)) return false;
+    if (bits == 32) return a.K <= 512 && dgm::aligned(W, 16);
+    if (a.G % 16 != 0) return false;
+    return dgm::aligned(W, bits == 8 ? 16 : 8);
+}
+
+template <int BITS>
+void launch_fwd_lds(const GemmArgs& a, int num_cus, hipStream_t st) {
+    // Largest contraction split that leaves each part at least one stage and
+    // the grid at least ~1.5 workgroups per CU.
+    const int nst = a.K / 64;
+    const int64_t ti = dgm::ceil_div(a.rows, 16);
+    const int64_t w4 = ti * dgm::ceil_div(a.cols, 16), w2 = ti * dgm::ceil_div(a.cols, 32);
+    if (nst >= 4 && (w2 < int64_t(num_cus) * 3 / 2 || nst >= 8))
+        launch_fwd_lds_ks<BITS, 4>(a, st);
+    else if (nst >= 2 && w2 < int64_t(num_cus) * 3)
+        launch_fwd_lds_ks<BITS, 2>(a, st);
+    else
+        launch_fwd_lds_ks<BITS, 1>(a, st);
+    (void)w4;
+}
+
 template <int MODE, int BITS, int TM, int TN>
 void launch_tile(const GemmArgs& a, bool vec, hipStream_t st) {
     dim3 grid(dgm::ceil_div(a.cols, TN), dgm::ceil_div(a.rows, TM));
@@ -296,6 +693,18 @@ int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const 
     a.has_bias = p->hasBias != 0;
     const size_t wal = bits == 32 ? 16 : (bits == 8 ? 4 : 2);
     const bool vec = (p->K % 4) == 0 && aligned(X, 16) && aligned(W, wal);
+    if (fwd_lds_ok(a, bits, X, W)) {
+        if (bits == 32) launch_fwd_lds<32>(a, g->num_cus, g->stream);
+        else if (bits == 8) launch_fwd_lds<8>(a, g->num_cus, g->stream);
+        else launch_fwd_lds<4>(a, g->num_cus, g->stream);
+        return DGM_OK;
+    }
+    if (deep_ok<MODE_FWD>(a, bits, vec)) {
+        if (bits == 32) launch_deep<MODE_FWD, 32>(a, g->num_cus, g->stream);
+        else if (bits == 8) launch_deep<MODE_FWD, 8>(a, g->num_cus, g->stream);
+        else launch_deep<MODE_FWD, 4>(a, g->num_cus, g->stream);
+        return DGM_OK;
+    }
     if (bits == 32) launch_gemm<MODE_FWD, 32>(a, vec, g->num_cus, g->stream);
     else if (bits == 8) launch_gemm<MODE_FWD, 8>(a, vec, g->num_cus, g->stream);
     else launch_gemm<MODE_FWD, 4>(a, vec, g->num_cus, g->stream);
@@ -311,6 +720,12 @@ int gemm_f32_dx(dgm_gpu* g, int bits, const void* W, const float* scale, const f
     a.G = bits == 32 ? 1 : int(p->qGroup);
     a.groups = bits == 32 ? 0 : int(p->K / p->qGroup);
     const bool vec = (p->N % 4) == 0 && aligned(dY, 16);
+    if (deep_ok<MODE_DX>(a, bits, vec)) {
+        if (bits == 32) launch_deep<MODE_DX, 32>(a, g->num_cus, g->stream);
+        else if (bits == 8) launch_deep<MODE_DX, 8>(a, g->num_cus, g->stream);
+        else launch_deep<MODE_DX, 4>(a, g->num_cus, g->stream);
+        return DGM_OK;
+    }
     if (bits == 32) launch_gemm<MODE_DX, 32>(a, vec, g->num_cus, g->stream);
     else if (bits == 8) launch_gemm<MODE_DX, 8>(a, vec, g->num_cus, g->stream);
     else launch_gemm<MODE_DX, 4>(a, vec, g->num_cus, g->stream);
@@ -325,7 +740,8 @@ int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dg
     a.rows = p->N; a.cols = p->K; a.red = p->M;
     a.G = 1; a.groups = 0;
     a.accumulate = accumulate;
-    launch_gemm<MODE_DW, 32>(a, false, g->num_cus, g->stream);
+    if (deep_ok<MODE_DW>(a, 32, false)) launch_deep<MODE_DW, 32>(a, g->num_cus, g->stream);
+    else launch_gemm<MODE_DW, 32>(a, false, g->num_cus, g->stream);
     return DGM_OK;
 }
 

@@ -148,6 +148,25 @@ def test_ragged_shapes(gpu, orc, bits, G, M, N, K_groups):
     assert max(errs.values()) <= TOL, errs
 
 
+@pytest.mark.parametrize("M,N,K,G,bits", [(48, 32, 40, 8, 8), (16, 48, 70, 14, 4), (80, 16, 24, 2, 4),
+                                          (32, 64, 100, 10, 8), (64, 16, 27, 1, 32), (17, 32, 48, 16, 4),
+                                          (96, 48, 36, 4, 8), (512, 192, 768, 32, 4), (512, 768, 192, 32, 8),
+                                          (1000, 272, 1040, 16, 8)])
+def test_multiple_of_16_contractions(gpu, orc, M, N, K, G, bits):
+    """Contractions that are multiples of 16 (K for the forward, N for dX, M
+    for dW) with ragged output tiles: the deep-prefetch kernels, whose rows and
+    columns past the matrix are clamped rather than masked."""
+    rng = np.random.default_rng(M + 3 * N + 7 * K + bits)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if M % 2 == 0 else None
+    dy = rng.standard_normal(M * N).astype(np.float32)
+    dw0 = rng.standard_normal(N * K).astype(np.float32)
+    out = run_step(gpu, bits, x, w, bias, dy, M, N, K, G, dw_init=dw0)
+    errs = _check_all(orc, out, x, w, bias, dy, M, N, K, G, bits, dw_init=dw0)
+    assert max(errs.values()) <= TOL, errs
+
+
 def test_unaligned_operands(gpu, orc):
     import torch
     M, N, K, G = 20, 24, 64, 16
