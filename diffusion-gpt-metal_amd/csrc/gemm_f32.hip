@@ -625,6 +625,140 @@ void launch_fwd_lds(const GemmArgs& a, int num_cus, hipStream_t st) {
     (void)w4;
 }
 
+// ---- LDS-staged STE dX for short contractions (N <= 448, N % 64 == 0) ---------
+// dX[m, k] = sum_n dY[m, n] * deq(W)[n, k]. A workgroup owns 16 rows x 64
+// columns of dX; each of its 4 waves owns 16 columns over the whole
+// contraction. The 16 x N block of dY goes to LDS as in the forward (direct
+// loads, swizzled slots). The weight strip W[0:N, k0:k0+64] is read with
+// 16-byte loads (consecutive lanes take consecutive rows n), dequantized once
+// per workgroup (code * scale, the reference's rounding) and written TRANSPOSED
+// to LDS as wt[k][n], rows padded to N + 4 floats, so a lane's 4 consecutive
+// contraction indices are one 16-byte LDS read and the 16 rows an MFMA operand
+// touches fall in distinct banks. Contraction order inside a 64-wide stage is
+// the same permutation for both operands (lane q takes 16q .. 16q+15).
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void gemm_dx_lds_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    extern __shared__ __align__(16) float4 sm4[];
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_i * tiles_j) return;
+    const int ti = t / tiles_j, tj = t - ti * tiles_j;
+    const int i0 = ti * 16, k0 = tj * 64;
+    const int N = a.N, K = a.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int spr = N >> 2;
+    float4* ys = sm4;                                          // [16][spr], swizzled
+    float* wt = reinterpret_cast<float*>(sm4 + 16 * spr);     // [64][N + 4]
+    const int wld = N + 4;
+
+    // -- weight strip: 16-byte units, unit u -> row n = u % N, part u / N.
+    constexpr int CPU = BITS == 4 ? 32 : (BITS == 8 ? 16 : 4);   // codes (or floats) per unit
+    constexpr int UPR = 64 / CPU;                                // units per row of the strip
+    constexpr int MAXU = (448 * UPR + kThreads - 1) / kThreads;
+    const int units = N * UPR;
+    uint4 wv[MAXU];
+    float ws[MAXU];
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        const int idx = min(int(threadIdx.x) + u * kThreads, units - 1);
+        const int n = idx % N, part = idx / N;
+        const int kc = min(k0 + part * CPU, K - CPU);   // strip columns past K: clamped, never stored
+        if constexpr (BITS == 32) {
+            wv[u] = *reinterpret_cast<const uint4*>(static_cast<const float*>(a.B) + size_t(n) * K + kc);
+        } else {
+            const size_t off = BITS == 8 ? size_t(n) * K + kc : (size_t(n) * K + kc) >> 1;
+            wv[u] = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.B) + off);
+            ws[u] = a.scale[size_t(n) * a.groups + kc / a.G];
+        }
+    }
+    // -- dY block via direct-to-LDS loads (slot pos of row r holds global slot pos ^ (r & 15)).
+    const int ninst = (16 * spr) >> 6;
+    uint8_t* yb = reinterpret_cast<uint8_t*>(ys);
+    for (int ii = wave; ii < ninst; ii += 4) {
+        const int L = ii * 64 + lane;
+        const int row = L / spr, pos = L - row * spr;
+        const int gr = min(i0 + row, a.rows - 1);
+        const float* src = a.A + size_t(gr) * N + ((pos ^ (row & 15)) << 2);
+        __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(yb + ii * 1024), 16, 0, 0);
+    }
+    // -- dequantize and transpose the strip into LDS.
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        const int idx = int(threadIdx.x) + u * kThreads;
+        if (idx >= units) break;
+        const int n = idx % N, part = idx / N;
+        float* dst = wt + (part * CPU) * wld + n;
+        const uint32_t w4[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+        if constexpr (BITS == 32) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[e * wld] = __uint_as_float(w4[e]);
+        } else if constexpr (BITS == 8) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) dst[e * wld] = float(int(int8_t((w4[e >> 2] >> (8 * (e & 3))) & 0xFF))) * ws[u];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const int nib = int((w4[e >> 3] >> (4 * (e & 7))) & 0xF);
+                dst[e * wld] = float(nib >= 8 ? nib - 16 : nib) * ws[u];
+            }
+        }
+    }
+    __syncthreads();
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const float4* yrow = ys + r16 * spr;
+    const float* wrow = wt + (wave * 16 + r16) * wld + 16 * q4;
+    const int nst = N >> 6;
+    for (int st = 0; st < nst; ++st) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 yv = yrow[(st * 16 + 4 * q4 + c) ^ r16];
+            const float4 wv4 = *reinterpret_cast<const float4*>(wrow + st * 64 + 4 * c);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.x, wv4.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.y, wv4.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.z, wv4.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.w, wv4.w, acc, 0, 0, 0);
+        }
+    }
+    const int k = k0 + wave * 16 + r16;
+    if (k < K) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i0 + 4 * q4 + r;
+            if (i < a.rows) a.out[size_t(i) * K + k] = acc[r];
+        }
+    }
+}
+
+size_t dx_lds_bytes(int N) { return size_t(16) * N * 4 + size_t(64) * (N + 4) * 4; }
+
+// N % 64 == 0 and N <= 448 (dY block and the transposed strip stay in LDS),
+// K a multiple of the 16-byte unit, a group that holds a whole unit, aligned rows.
+bool dx_lds_ok(const GemmArgs& a, int bits, const void* dY, const void* W) {
+    if (a.N % 64 != 0 || a.N == 0 || a.N > 448 || a.rows == 0 || a.K == 0) return false;
+    if (!dgm::aligned(dY, 16) || !dgm::aligned(W, 16)) return false;
+    const int cpu = bits == 4 ? 32 : (bits == 8 ? 16 : 4);
+    if (a.K % cpu != 0) return false;
+    return bits == 32 || a.G % cpu == 0;
+}
+
+template <int BITS>
+int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
+    const size_t lds = dx_lds_bytes(a.N);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_dx_lds_kernel<BITS>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "gemm_dx: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
+    }
+    const int ti = int(dgm::ceil_div(a.rows, 16)), tj = int(dgm::ceil_div(a.K, 64));
+    const int64_t nt = int64_t(ti) * tj;
+    const int per = int((nt + 7) / 8);
+    hipLaunchKernelGGL(gemm_dx_lds_kernel<BITS>, dim3(unsigned(per) * 8u), dim3(kThreads), lds, g->stream, a, ti, tj,
+                       per);
+    return DGM_OK;
+}
+
 template <int MODE, int BITS, int TM, int TN>
 void launch_tile(const GemmArgs& a, bool vec, hipStream_t st) {
     dim3 grid(dgm::ceil_div(a.cols, TN), dgm::ceil_div(a.rows, TM));
@@ -720,6 +854,11 @@ int gemm_f32_dx(dgm_gpu* g, int bits, const void* W, const float* scale, const f
     a.G = bits == 32 ? 1 : int(p->qGroup);
     a.groups = bits == 32 ? 0 : int(p->K / p->qGroup);
     const bool vec = (p->N % 4) == 0 && aligned(dY, 16);
+    if (dx_lds_ok(a, bits, dY, W)) {
+        if (bits == 32) return launch_dx_lds<32>(g, a);
+        if (bits == 8) return launch_dx_lds<8>(g, a);
+        return launch_dx_lds<4>(g, a);
+    }
     if (deep_ok<MODE_DX>(a, bits, vec)) {
         if (bits == 32) launch_deep<MODE_DX, 32>(a, g->num_cus, g->stream);
         else if (bits == 8) launch_deep<MODE_DX, 8>(a, g->num_cus, g->stream);

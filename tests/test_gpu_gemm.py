@@ -151,11 +151,13 @@ def test_ragged_shapes(gpu, orc, bits, G, M, N, K_groups):
 @pytest.mark.parametrize("M,N,K,G,bits", [(48, 32, 40, 8, 8), (16, 48, 70, 14, 4), (80, 16, 24, 2, 4),
                                           (32, 64, 100, 10, 8), (64, 16, 27, 1, 32), (17, 32, 48, 16, 4),
                                           (96, 48, 36, 4, 8), (512, 192, 768, 32, 4), (512, 768, 192, 32, 8),
-                                          (1000, 272, 1040, 16, 8)])
+                                          (1000, 272, 1040, 16, 8), (33, 64, 96, 32, 4), (70, 128, 80, 16, 8),
+                                          (9, 448, 36, 1, 32), (130, 256, 160, 32, 4), (1, 64, 64, 64, 8)])
 def test_multiple_of_16_contractions(gpu, orc, M, N, K, G, bits):
-    """Contractions that are multiples of 16 (K for the forward, N for dX, M
-    for dW) with ragged output tiles: the deep-prefetch kernels, whose rows and
-    columns past the matrix are clamped rather than masked."""
+    """Contractions that are multiples of 16 or 64 (K for the forward, N for
+    dX, M for dW) with ragged output tiles: the deep-prefetch and LDS-staged
+    kernels, whose rows and columns past the matrix are clamped rather than
+    masked."""
     rng = np.random.default_rng(M + 3 * N + 7 * K + bits)
     x = rng.standard_normal(M * K).astype(np.float32)
     w = (rng.standard_normal(N * K) * 0.1).astype(np.float32)
