@@ -25,6 +25,7 @@ int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const 
 namespace {
 
 constexpr int kThreads = 256;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -199,6 +200,168 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict_
     }
 }
 
+// ---- attention on fp32 MFMA (T % 16 == 0, D % 16 == 0) ----------------------------
+// Same three stages as attn_scores / attn_softmax / attn_av
+// (metal/kernels.metal:443-506), fused: a workgroup owns (b, h, 16 query
+// rows). Products run on v_mfma_f32_16x16x4_f32 (fp32 operands, fp32
+// accumulation); each lane reads 4 consecutive contraction indices with one
+// 16-byte LDS load and the 4 MFMA steps consume them, the same permutation for
+// both operands. Rows in LDS are padded to D+4 / T+4 floats so the 16 rows of an
+// operand fetch hit distinct banks. Optional prologue work of the DiT loop
+// body, applied while staging (each element computed exactly as the
+// standalone kernels compute it):
+//  * rope: rotate-half RoPE of q and k (rope_fwd, metal/kernels.metal:871-889);
+//  * kv_heads == 1: the single KV head is read for every query head
+//    (repeat_heads, metal/kernels.metal:980-993);
+//  * vmix: v = ca * v + cb * vfirst (mix_f, metal/kernels.metal:951-959).
+struct AttnArgs {
+    const float *q, *k, *v, *vfirst, *cosv, *sinv;
+    float *scores, *probs, *av;
+    int B, T, H, D;
+    int q_ld, kv_ld, vf_ld, av_ld;   // floats between consecutive token rows
+    int kv_heads;                    // 1 (shared head) or H
+    float scale, ca, cb;
+    int causal, rope, vmix;
+};
+
+__device__ __forceinline__ float rope_elem(const float* row, int d, int D, float c, float s) {
+#pragma clang fp contract(off)
+    const int mid = D >> 1;
+    const float rot = d < mid ? -row[d + mid] : row[d - mid];
+    const float a = row[d] * c;
+    const float b = rot * s;
+    return a + b;
+}
+
+__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float sm[];
+    const int T = a.T, D = a.D, H = a.H;
+    const int qs_ld = D + 4, vt_ld = T + 4;
+    float* qs = sm;                      // [16][D+4]
+    float* ks = qs + 16 * qs_ld;         // [T][D+4]
+    float* vt = ks + T * qs_ld;          // [D][T+4]  (V transposed)
+    float* ps = vt + D * vt_ld;          // [16][T+4]
+    const int tiles = T >> 4;
+    const int tb = blockIdx.x % tiles;
+    const int h = (blockIdx.x / tiles) % H;
+    const int b = blockIdx.x / (tiles * H);
+    const int t0 = tb * 16;
+    const int hk = a.kv_heads == 1 ? 0 : h;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+
+    // -- stage q (16 rows), k and v (T rows) of this (b, h).
+    for (int e = threadIdx.x; e < 16 * D; e += kThreads) {
+        const int t = e / D, d = e - t * D;
+        const float* row = a.q + size_t(b * T + t0 + t) * a.q_ld + h * D;
+        qs[t * qs_ld + d] = a.rope ? rope_elem(row, d, D, a.cosv[(t0 + t) * D + d], a.sinv[(t0 + t) * D + d]) : row[d];
+    }
+    for (int e = threadIdx.x; e < T * D; e += kThreads) {
+        const int t = e / D, d = e - t * D;
+        const float* krow = a.k + size_t(b * T + t) * a.kv_ld + hk * D;
+        ks[t * qs_ld + d] = a.rope ? rope_elem(krow, d, D, a.cosv[t * D + d], a.sinv[t * D + d]) : krow[d];
+        float vv = a.v[size_t(b * T + t) * a.kv_ld + hk * D + d];
+        if (a.vmix) {
+            const float p = a.ca * vv;
+            const float r = a.cb * a.vfirst[size_t(b * T + t) * a.vf_ld + d];
+            vv = p + r;
+        }
+        vt[d * vt_ld + t] = vv;
+    }
+    __syncthreads();
+
+    // -- scores: wave w takes key tiles w, w+4, ...
+    const size_t srow0 = (size_t(b) * H + h) * T + t0;   // row index into [B,H,T,T]
+    for (int kt = wave; kt < tiles; kt += 4) {
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* qa = qs + r16 * qs_ld + 4 * q4;
+        const float* kb = ks + (kt * 16 + r16) * qs_ld + 4 * q4;
+        for (int d0 = 0; d0 < D; d0 += 16) {
+            const float4 x = *reinterpret_cast<const float4*>(qa + d0);
+            const float4 y = *reinterpret_cast<const float4*>(kb + d0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, y.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, y.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, y.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, y.w, acc, 0, 0, 0);
+        }
+        // acc[r]: query row 4*q4 + r, key kt*16 + r16.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 4 * q4 + r, s2 = kt * 16 + r16;
+            float v = acc[r] * a.scale;
+            if (a.causal && s2 > t0 + t) v = -1.0e30f;
+            ps[t * vt_ld + s2] = v;
+        }
+    }
+    __syncthreads();
+
+    // -- row softmax: wave w takes rows w, w+4, ...; lanes stride the keys.
+    for (int t = wave; t < 16; t += 4) {
+        float* row = ps + t * vt_ld;
+        float* so = a.scores + (srow0 + t) * T;
+        float* po = a.probs + (srow0 + t) * T;
+        float mx = -INFINITY;
+        for (int s2 = lane; s2 < T; s2 += 64) {
+            so[s2] = row[s2];
+            mx = fmaxf(mx, row[s2]);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float sum = 0.0f;
+        for (int s2 = lane; s2 < T; s2 += 64) sum += expf(row[s2] - mx);
+        sum = wave_sum(sum);
+        const float inv = 1.0f / sum;
+        for (int s2 = lane; s2 < T; s2 += 64) {
+            const float pv = expf(row[s2] - mx) * inv;
+            row[s2] = pv;
+            po[s2] = pv;
+        }
+    }
+    __syncthreads();
+
+    // -- av = probs . v: wave w takes d tiles w, w+4, ...
+    for (int dt = wave; dt < (D >> 4); dt += 4) {
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* pa = ps + r16 * vt_ld + 4 * q4;
+        const float* vb = vt + (dt * 16 + r16) * vt_ld + 4 * q4;
+        for (int s0 = 0; s0 < T; s0 += 16) {
+            const float4 x = *reinterpret_cast<const float4*>(pa + s0);
+            const float4 y = *reinterpret_cast<const float4*>(vb + s0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, y.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, y.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, y.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, y.w, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 4 * q4 + r;
+            a.av[size_t(b * T + t) * a.av_ld + h * D + dt * 16 + r16] = acc[r];
+        }
+    }
+}
+
+size_t attn_mfma_lds_bytes(int T, int D) {
+    return sizeof(float) * (size_t(16 + T) * (D + 4) + size_t(D + 16) * (T + 4));
+}
+
+bool attn_mfma_ok(int T, int D) {
+    return T > 0 && D > 0 && T % 16 == 0 && D % 16 == 0 && attn_mfma_lds_bytes(T, D) <= 160 * 1024;
+}
+
+int launch_attn_mfma(dgm_gpu* g, const AttnArgs& a) {
+    const size_t lds = attn_mfma_lds_bytes(a.T, a.D);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_mfma_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "attn_fwd: cannot reserve %zu bytes of LDS: %s", lds,
+                             hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(attn_mfma_kernel, dim3(unsigned(a.B * a.H * (a.T / 16))), dim3(kThreads), lds, g->stream, a);
+    return dgm::check_launch(g, "attn_fwd");
+}
+
 inline unsigned blocks_for(int64_t n) { return unsigned((n + kThreads - 1) / kThreads); }
 
 size_t attn_lds_bytes(int T, int D) {
@@ -234,6 +397,16 @@ int launch_repeat(dgm_gpu* g, const float* src, float* dst, int B, int T, int H,
 int launch_attn(dgm_gpu* g, const float* q, const float* k, const float* v, float* scores, float* probs,
                 float* av, int B, int T, int H, int D, int causal) {
     if (int64_t(B) * T * H * D == 0) return DGM_OK;
+    if (attn_mfma_ok(T, D)) {
+        AttnArgs a{};
+        a.q = q; a.k = k; a.v = v; a.scores = scores; a.probs = probs; a.av = av;
+        a.B = B; a.T = T; a.H = H; a.D = D;
+        a.q_ld = a.kv_ld = a.av_ld = H * D;
+        a.kv_heads = H;
+        a.scale = 1.0f / sqrtf(float(D));
+        a.causal = causal;
+        return launch_attn_mfma(g, a);
+    }
     const size_t lds = attn_lds_bytes(T, D);
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel),
@@ -283,17 +456,98 @@ int check_bthd(dgm_gpu* g, const char* name, int64_t B, int64_t T, int64_t H, in
     return DGM_OK;
 }
 
-// ---- the block orchestrator (src/DiT.swift:520-550) ---------------------------------
+// ---- fused row kernels of the loop body ----------------------------------------------
+// One wave per row; every RMSNorm reduces its sum of squares in exactly the
+// lane order rmsnorm_kernel uses, and every add/product rounds as the
+// standalone kernels do, so the fused results equal running rmsFwd, add,
+// rmsFwd (, rmsFwd) in sequence, bit for bit.
+//   mid  = res + rms(a) * w1          (rmsnorm_fwd + add_f)
+//   out2 = rms(mid) * w2              (rmsnorm_fwd)
+//   out3 = rms(out2) * w3             (rmsnorm_fwd; when w3 != nullptr)
+constexpr int kRowMax = 16;   // columns per lane: cols <= 1024
 
-enum Buf { LN1, QPRE, KPRE, VPRE, VFIRST, VMIX, Q, KROT, KH, VH, SCORES, PROBS, AV, ATTN, T1, MID, LN2, GATE,
-           UP, SW, MLP, PRE, RSTD, NBUF };
+__device__ __forceinline__ float row_rstd(const float (&v)[kRowMax], int lane, int cols, float eps) {
+#pragma clang fp contract(off)
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kRowMax; ++u)
+        if (lane + 64 * u < cols) ss += v[u] * v[u];
+    ss = wave_sum(ss);
+    const float mean = ss / float(cols);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+__global__ __launch_bounds__(kThreads) void row_fuse_kernel(const float* __restrict__ a, const float* __restrict__ res,
+                                                            float* __restrict__ mid, float* __restrict__ out2,
+                                                            float* __restrict__ out3, const float* __restrict__ w1,
+                                                            const float* __restrict__ w2, const float* __restrict__ w3,
+                                                            float* __restrict__ rstd, int rows, int cols, float eps) {
+#pragma clang fp contract(off)
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = size_t(row) * cols;
+    float v[kRowMax];
+#pragma unroll
+    for (int u = 0; u < kRowMax; ++u) v[u] = lane + 64 * u < cols ? a[base + lane + 64 * u] : 0.0f;
+    float rs = row_rstd(v, lane, cols, eps);
+#pragma unroll
+    for (int u = 0; u < kRowMax; ++u) {
+        const int c = lane + 64 * u;
+        if (c < cols) {
+            const float t1 = (v[u] * rs) * w1[c];
+            v[u] = res[base + c] + t1;
+            if (mid) mid[base + c] = v[u];
+        }
+    }
+    rs = row_rstd(v, lane, cols, eps);
+#pragma unroll
+    for (int u = 0; u < kRowMax; ++u) {
+        const int c = lane + 64 * u;
+        if (c < cols) {
+            v[u] = (v[u] * rs) * w2[c];
+            out2[base + c] = v[u];
+        }
+    }
+    if (w3) {
+        rs = row_rstd(v, lane, cols, eps);
+#pragma unroll
+        for (int u = 0; u < kRowMax; ++u) {
+            const int c = lane + 64 * u;
+            if (c < cols) out3[base + c] = (v[u] * rs) * w3[c];
+        }
+    }
+    if (lane == 0 && rstd) rstd[row] = rs;
+}
+
+// swiglu_fwd over row-strided gate / up (the halves of a fused [gate; up]
+// projection, or two separate buffers): y[m, j] = gate * sigmoid(gate) * up.
+__global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(const float* __restrict__ gate,
+                                                               const float* __restrict__ up, float* __restrict__ y,
+                                                               int rows, int F, int ldg, int ldu) {
+#pragma clang fp contract(off)
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= int64_t(rows) * F) return;
+    const int m = int(i / F), j = int(i - int64_t(m) * F);
+    const float z = gate[size_t(m) * ldg + j];
+    const float act = z * silu_sigmoid(z);
+    y[i] = act * up[size_t(m) * ldu + j];
+}
+
+// ---- the block orchestrator (src/DiT.swift:520-550) ---------------------------------
+// Workspace (floats, each piece 256-byte aligned):
+//   ln1 [M,C] | qkv0 [M,C+2D] | qkv1 [M,C+2D] | scores [B,H,T,T] | probs [B,H,T,T]
+//   | av [M,C] | attn [M,C] | mid [M,C] | ln2 [M,C] | gu [M,2F] | sw [M,F] | mlp [M,C]
+//   | pre [M,C] | rstd [M]
+// qkv0 holds loop 0's projections (its v columns are the value-residual
+// source of later loops); later loops use qkv1.
+enum Buf { LN1, QKV0, QKV1, SCORES, PROBS, AV, ATTN, MID, LN2, GU, SW, MLP, PRE, RSTD, NBUF };
 
 void dit_sizes(const dgm_dit_cfg* c, int64_t* sz) {
     const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
     const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
-    const int64_t s[NBUF] = {M * C, M * C, M * KV, M * KV, M * KV, M * KV, M * C, M * KV, M * C, M * C,
-                             att,   att,   M * C,  M * C,  M * C,  M * C,  M * C, M * F,  M * F, M * F,
-                             M * C, M * C, M};
+    const int64_t s[NBUF] = {M * C, M * (C + 2 * KV), M * (C + 2 * KV), att, att, M * C, M * C, M * C, M * C,
+                             M * 2 * F, M * F, M * C, M * C, M};
     for (int i = 0; i < NBUF; ++i) sz[i] = s[i];
 }
 
@@ -302,6 +556,32 @@ int64_t dit_workspace_floats(const dgm_dit_cfg* c) {
     dit_sizes(c, sz);
     for (int i = 0; i < NBUF; ++i) total += (sz[i] + 63) & ~int64_t(63);   // 256-byte aligned pieces
     return total;
+}
+
+int launch_row_fuse(dgm_gpu* g, const float* a, const float* res, float* mid, float* out2, float* out3,
+                    const float* w1, const float* w2, const float* w3, float* rstd, int64_t rows, int64_t cols,
+                    float eps) {
+    if (rows == 0 || cols == 0) return DGM_OK;
+    hipLaunchKernelGGL(row_fuse_kernel, dim3(unsigned((rows + 3) / 4)), dim3(kThreads), 0, g->stream, a, res, mid,
+                       out2, out3, w1, w2, w3, rstd, int(rows), int(cols), eps);
+    return dgm::check_launch(g, "dit_forward row_fuse");
+}
+
+int launch_swiglu_rows(dgm_gpu* g, const float* gate, const float* up, float* y, int64_t rows, int64_t F,
+                       int64_t ldg, int64_t ldu) {
+    const int64_t n = rows * F;
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, gate, up, y, int(rows),
+                       int(F), int(ldg), int(ldu));
+    return dgm::check_launch(g, "dit_forward swiglu");
+}
+
+// Byte offset between two linears' codes / scales when laid out back to back.
+bool follows(const dgm_dit_linear& first, const dgm_dit_linear& next, int64_t rows, int64_t K, int bits, int G) {
+    if (bits == 32) return next.w == first.w + rows * K;
+    const int64_t code_bytes = bits == 4 ? rows * K / 2 : rows * K;
+    return static_cast<const uint8_t*>(next.q) == static_cast<const uint8_t*>(first.q) + code_bytes &&
+           next.scale == first.scale + rows * (K / G);
 }
 
 }  // namespace
@@ -424,12 +704,22 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, 
     if (c->B <= 0 || c->T <= 0 || c->C <= 0 || c->F <= 0 || c->H <= 0 || c->D <= 0 || c->loops < 0 ||
         c->H * c->D != c->C || c->D % 2 != 0)
         return dgm::fail(g, DGM_ERR_SHAPE, "dit_forward: bad config (C must be H*D, D even)");
+    if (c->C > 64 * kRowMax)
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: embd %d above %d", c->C, 64 * kRowMax);
     if (c->bits != 32 && (c->group <= 0 || c->C % c->group != 0 || c->F % c->group != 0 ||
                           (c->bits == 4 && c->group % 2 != 0)))
         return dgm::fail(g, DGM_ERR_SHAPE, "dit_forward: C and F must be multiples of an (even for int4) group");
-    if (attn_lds_bytes(c->T, c->D) > 160 * 1024)
-        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: T*D too large for the attention kernel");
+    if (!attn_mfma_ok(c->T, c->D))
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED,
+                         "dit_forward: tokens %d and head dim %d must be multiples of 16 (LDS-resident attention)",
+                         c->T, c->D);
+    if (int64_t(c->B) * c->T * (c->C + 2 * c->F) > (int64_t(1) << 31))
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: activations beyond 2^31 elements");
     if (ws_floats < dit_workspace_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: workspace too small");
+    const dgm_dit_linear* lins[7] = {&w->wq, &w->wk, &w->wv, &w->wo, &w->wgate, &w->wup, &w->wdown};
+    for (const dgm_dit_linear* L : lins)
+        if (c->bits == 32 ? !L->w : (!L->q || !L->scale)) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: null weight");
+    if (!w->n1 || !w->n1b || !w->n2 || !w->n2b || !w->nf) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: null norm");
 
     int64_t sz[NBUF];
     float* p[NBUF];
@@ -440,50 +730,74 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, 
         cur += (sz[i] + 63) & ~int64_t(63);
     }
     const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
-    const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D;
+    const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, QKV = C + 2 * KV;
+    // Back-to-back weights run as one GEMM: [wq; wk; wv] and [wgate; wup].
+    const bool fuse_qkv = follows(w->wq, w->wk, C, C, bits, G) && follows(w->wk, w->wv, KV, C, bits, G);
+    const bool fuse_gu = follows(w->wgate, w->wup, F, C, bits, G);
 
     auto gemm = [&](const dgm_dit_linear& L, const float* in, float* out, int64_t N, int64_t K) -> int {
         dgm_GemmP gp{uint32_t(M), uint32_t(N), uint32_t(K), 0u, uint32_t(bits == 32 ? 0 : G), 0, 0, 0};
         int r = dgm::gemm_check_sizes(g, "dit_forward", &gp, bits);
         if (r) return r;
         const void* wt = bits == 32 ? static_cast<const void*>(L.w) : L.q;
-        if (!wt || (bits != 32 && !L.scale)) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: null weight");
         r = dgm::gemm_f32_fwd(g, bits, wt, L.scale, in, nullptr, out, &gp);
         if (r) return r;
         return dgm::check_launch(g, "dit_forward gemm");
     };
-#define DGM_TRY(expr)              \
-    do {                           \
-        int _r = (expr);           \
+#define DGM_TRY(expr)                \
+    do {                             \
+        int _r = (expr);             \
         if (_r != DGM_OK) return _r; \
     } while (0)
+    DGM_TRY(launch_rms(g, x, p[LN1], p[RSTD], w->n1, M, C, c->eps));
     for (int loop = 0; loop < c->loops; ++loop) {
-        DGM_TRY(launch_rms(g, x, p[LN1], p[RSTD], w->n1, M, C, c->eps));
-        DGM_TRY(gemm(w->wq, p[LN1], p[QPRE], C, C));
-        DGM_TRY(gemm(w->wk, p[LN1], p[KPRE], KV, C));
-        DGM_TRY(gemm(w->wv, p[LN1], p[VPRE], KV, C));
-        if (loop == 0) {
-            DGM_TRY(launch_copy(g, p[VPRE], p[VFIRST], M * KV));
-            DGM_TRY(launch_repeat(g, p[VPRE], p[VH], B, T, H, D));
+        float* qkv = p[loop == 0 ? QKV0 : QKV1];
+        // q / k / v projections; fused: rows of qkv are [q | k | v], else three blocks.
+        const float *q, *k, *v;
+        int q_ld, kv_ld, v_ld;
+        if (fuse_qkv) {
+            DGM_TRY(gemm(w->wq, p[LN1], qkv, QKV, C));
+            q = qkv; k = qkv + C; v = qkv + C + KV;
+            q_ld = kv_ld = v_ld = int(QKV);
         } else {
-            DGM_TRY(launch_mix(g, p[VPRE], p[VFIRST], p[VMIX], M * KV, 1.0f - c->mix, c->mix));
-            DGM_TRY(launch_repeat(g, p[VMIX], p[VH], B, T, H, D));
+            DGM_TRY(gemm(w->wq, p[LN1], qkv, C, C));
+            DGM_TRY(gemm(w->wk, p[LN1], qkv + M * C, KV, C));
+            DGM_TRY(gemm(w->wv, p[LN1], qkv + M * (C + KV), KV, C));
+            q = qkv; k = qkv + M * C; v = qkv + M * (C + KV);
+            q_ld = int(C); kv_ld = v_ld = int(KV);
         }
-        DGM_TRY(launch_rope(g, p[QPRE], p[Q], cosv, sinv, B, T, H, D));
-        DGM_TRY(launch_rope(g, p[KPRE], p[KROT], cosv, sinv, B, T, 1, D));
-        DGM_TRY(launch_repeat(g, p[KROT], p[KH], B, T, H, D));
-        DGM_TRY(launch_attn(g, p[Q], p[KH], p[VH], p[SCORES], p[PROBS], p[AV], B, T, H, D, 0));
+        const float* vfirst = fuse_qkv ? p[QKV0] + C + KV : p[QKV0] + M * (C + KV);
+        // value residual (mix), RoPE on q and k, one KV head for all heads, full attention.
+        {
+            AttnArgs aa{};
+            aa.q = q; aa.k = k; aa.v = v; aa.vfirst = vfirst; aa.cosv = cosv; aa.sinv = sinv;
+            aa.scores = p[SCORES]; aa.probs = p[PROBS]; aa.av = p[AV];
+            aa.B = B; aa.T = T; aa.H = H; aa.D = D;
+            aa.q_ld = q_ld; aa.kv_ld = kv_ld; aa.vf_ld = v_ld; aa.av_ld = int(C);
+            aa.kv_heads = 1;
+            aa.scale = 1.0f / sqrtf(float(D));
+            aa.ca = 1.0f - c->mix; aa.cb = c->mix;
+            aa.causal = 0; aa.rope = 1; aa.vmix = loop > 0;
+            (void)v_ld;   // == kv_ld in both layouts
+            DGM_TRY(launch_attn_mfma(g, aa));
+        }
         DGM_TRY(gemm(w->wo, p[AV], p[ATTN], C, C));
-        DGM_TRY(launch_rms(g, p[ATTN], p[T1], p[RSTD], w->n1b, M, C, c->eps));
-        DGM_TRY(launch_add(g, x, p[T1], p[MID], M * C));
-        DGM_TRY(launch_rms(g, p[MID], p[LN2], p[RSTD], w->n2, M, C, c->eps));
-        DGM_TRY(gemm(w->wgate, p[LN2], p[GATE], F, C));
-        DGM_TRY(gemm(w->wup, p[LN2], p[UP], F, C));
-        DGM_TRY(launch_swiglu(g, p[GATE], p[UP], p[SW], M * F));
+        // mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2
+        DGM_TRY(launch_row_fuse(g, p[ATTN], x, p[MID], p[LN2], nullptr, w->n1b, w->n2, nullptr, p[RSTD], M, C,
+                                c->eps));
+        if (fuse_gu) {
+            DGM_TRY(gemm(w->wgate, p[LN2], p[GU], 2 * F, C));
+            DGM_TRY(launch_swiglu_rows(g, p[GU], p[GU] + F, p[SW], M, F, 2 * F, 2 * F));
+        } else {
+            DGM_TRY(gemm(w->wgate, p[LN2], p[GU], F, C));
+            DGM_TRY(gemm(w->wup, p[LN2], p[GU] + M * F, F, C));
+            DGM_TRY(launch_swiglu_rows(g, p[GU], p[GU] + M * F, p[SW], M, F, F, F));
+        }
         DGM_TRY(gemm(w->wdown, p[SW], p[MLP], C, F));
-        DGM_TRY(launch_rms(g, p[MLP], p[T1], p[RSTD], w->n2b, M, C, c->eps));
-        DGM_TRY(launch_add(g, p[MID], p[T1], p[PRE], M * C));
-        DGM_TRY(launch_rms(g, p[PRE], x, p[RSTD], w->nf, M, C, c->eps));
+        // pre = mid + rms(mlp) * n2b; x = rms(pre) * nf; next ln1 = rms(x) * n1
+        const bool more = loop + 1 < c->loops;
+        DGM_TRY(launch_row_fuse(g, p[MLP], p[MID], p[PRE], x, more ? p[LN1] : nullptr, w->n2b, w->nf,
+                                more ? w->n1 : nullptr, p[RSTD], M, C, c->eps));
     }
 #undef DGM_TRY
     return DGM_OK;

@@ -76,24 +76,43 @@ class DiTBlock:
         self.keep = []
         self.codes: Dict[str, object] = {}
         self.scales: Dict[str, object] = {}
-        lin = {}
-        gpu.begin()
+        shapes = cfg.linear_shapes()
         for name in DIT_LINEARS:
-            N, K = cfg.linear_shapes()[name]
+            N, K = shapes[name]
             w = weights[name]
             if w.numel() != N * K or w.dtype != torch.float32 or not w.is_cuda:
                 raise ValueError(f"{name}: expected {N}x{K} fp32 device tensor")
-            w = w.contiguous()
-            self.keep.append(w)
+        # [wq; wk; wv] and [wgate; wup] are laid out back to back so that the
+        # library runs each group as one GEMM (quantization is per row, so the
+        # codes and scales of a row do not depend on its neighbours).
+        groups = [("wq", "wk", "wv"), ("wo",), ("wgate", "wup"), ("wdown",)]
+        lin = {}
+        dev = weights["wq"].device
+        gpu.begin()
+        for grp in groups:
+            rows = sum(shapes[n][0] for n in grp)
+            K = shapes[grp[0]][1]
             if cfg.bits == 32:
-                lin[name] = DiTLinear(_ptr(w), None, None)
+                cat = torch.cat([weights[n].reshape(-1).contiguous() for n in grp])
+                self.keep.append(cat)
+                off = 0
+                for n in grp:
+                    lin[n] = DiTLinear(cat.data_ptr() + 4 * off, None, None)
+                    off += shapes[n][0] * K
                 continue
-            nbytes = N * K // 2 if cfg.bits == 4 else N * K
-            q = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=w.device)
-            s = torch.zeros(max(N * (K // cfg.group), 1), dtype=torch.float32, device=w.device)
-            gpu.quantize(w, q, s, N, K, cfg.bits, cfg.group)
-            self.codes[name], self.scales[name] = q, s
-            lin[name] = DiTLinear(None, _ptr(q), _ptr(s))
+            per = (lambda r: r * K // 2) if cfg.bits == 4 else (lambda r: r * K)
+            q = torch.zeros(max(per(rows), 16), dtype=torch.uint8, device=dev)
+            s = torch.zeros(max(rows * (K // cfg.group), 1), dtype=torch.float32, device=dev)
+            self.keep += [q, s]
+            r0 = 0
+            for n in grp:
+                N = shapes[n][0]
+                qv = q[per(r0): per(r0 + N)]
+                sv = s[r0 * (K // cfg.group): (r0 + N) * (K // cfg.group)]
+                gpu.quantize(weights[n].contiguous(), qv, sv, N, K, cfg.bits, cfg.group)
+                self.codes[n], self.scales[n] = qv, sv
+                lin[n] = DiTLinear(None, qv.data_ptr(), sv.data_ptr())
+                r0 += N
         gpu.end()
         norms = {}
         for name in DIT_NORMS:
@@ -105,7 +124,6 @@ class DiTBlock:
         self.c = cfg.c_cfg()
         self.w = DiTWeights(*[lin[n] for n in DIT_LINEARS], *[norms[n] for n in DIT_NORMS])
         cos, sin = rope_tables(cfg.T, cfg.D, cfg.theta)
-        dev = self.keep[0].device
         self.cos = torch.from_numpy(cos).to(dev)
         self.sin = torch.from_numpy(sin).to(dev)
         self.ws_floats = gpu.dit_workspace_floats(self.c)
@@ -134,12 +152,12 @@ class DiTBlock:
 
 
 def _ws_sizes(cfg: DiTConfig):
+    """The pieces of dgm_dit_forward's workspace, in order (each 256-byte aligned)."""
     M, C, F, KV = cfg.B * cfg.T, cfg.C, cfg.F, cfg.D
     att = cfg.B * cfg.H * cfg.T * cfg.T
-    names = ["ln1", "qpre", "kpre", "vpre", "vfirst", "vmix", "q", "krot", "k", "v", "scores", "probs", "av",
-             "attn", "t1", "mid", "ln2", "gate", "up", "sw", "mlp", "pre", "rstd"]
-    sizes = [M * C, M * C, M * KV, M * KV, M * KV, M * KV, M * C, M * KV, M * C, M * C, att, att, M * C,
-             M * C, M * C, M * C, M * C, M * F, M * F, M * F, M * C, M * C, M]
+    names = ["ln1", "qkv0", "qkv1", "scores", "probs", "av", "attn", "mid", "ln2", "gu", "sw", "mlp", "pre", "rstd"]
+    sizes = [M * C, M * (C + 2 * KV), M * (C + 2 * KV), att, att, M * C, M * C, M * C, M * C, M * 2 * F, M * F,
+             M * C, M * C, M]
     return list(zip(names, sizes))
 
 

@@ -219,7 +219,14 @@ int64_t dgm_dit_workspace_floats(const dgm_dit_cfg* cfg);
  * entry and xs[loops] on exit. cos_t/sin_t are device copies of
  * ropeTables(T, D, theta). ws: device workspace of at least
  * dgm_dit_workspace_floats(cfg) floats; on exit it holds the last loop's
- * intermediates (scores and probs included). Enqueued on the context's
+ * intermediates (projections, scores and probs [B,H,T,T], attention output,
+ * residual stream, SwiGLU input and output). When wq, wk, wv (and wgate,
+ * wup) are laid out back to back in memory (codes and scales, or fp32
+ * weights), each group runs as one GEMM. RoPE, the value-residual mix and the
+ * KV-head broadcast are applied inside the attention kernel, and each
+ * RMSNorm + residual chain is one row kernel; every element is computed as
+ * the standalone wrappers compute it. Needs T and D multiples of 16 and
+ * C <= 1024 (DGM_ERR_UNSUPPORTED otherwise). Enqueued on the context's
  * stream; graph-capturable (no allocation, no host sync). */
 int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w,
                     const float* cos_t, const float* sin_t, float* x, float* ws,

@@ -214,6 +214,43 @@ def test_dit_block_other_widths(gpu, dgm, orc, bits, group):
         _check_block(gpu, dgm, orc, cfg, w, x0, 1e-5)
 
 
+def test_dit_forward_separate_weight_buffers(gpu, dgm, orc):
+    """Linears in unrelated allocations (not back to back): the projections run
+    as separate GEMMs; the result still matches the oracle."""
+    import torch
+    cfg = dgm.DiTConfig(B=2, T=32, C=96, F=192, H=2, D=48, loops=2, group=32, bits=8)
+    w = _dit_weights(orc, cfg, seed=11)
+    x0 = orc.RNG(12).randn(cfg.B * cfg.T * cfg.C, 1.0)
+    keep, lins, codes = [], {}, {}
+    gpu.begin()
+    for name in orc.DIT_LINEARS:
+        N, K = cfg.linear_shapes()[name]
+        pad = torch.zeros(4096, dtype=torch.uint8, device="cuda")     # keeps allocations apart
+        q = torch.zeros(N * K, dtype=torch.int8, device="cuda")
+        s = torch.zeros(N * (K // cfg.group), device="cuda")
+        wd = to_dev(w[name])
+        gpu.quantize(wd, q, s, N, K, 8, cfg.group)
+        keep += [pad, q, s, wd]
+        lins[name] = dgm.DiTLinear(None, q.data_ptr(), s.data_ptr())
+    gpu.end()
+    for name in orc.DIT_LINEARS:
+        N, K = cfg.linear_shapes()[name]
+        codes[name] = orc.quant(w[name], N, K, cfg.group, 8)
+    norms = {n: to_dev(w[n]) for n in orc.DIT_NORMS}
+    wts = dgm.DiTWeights(*[lins[n] for n in orc.DIT_LINEARS], *[norms[n].data_ptr() for n in orc.DIT_NORMS])
+    c = cfg.c_cfg()
+    cos, sin = dgm.rope_tables(cfg.T, cfg.D, cfg.theta)
+    cd, sd = to_dev(cos), to_dev(sin)
+    nws = gpu.dit_workspace_floats(c)
+    ws = torch.zeros(nws, device="cuda")
+    x = to_dev(x0)
+    gpu.begin()
+    gpu.dit_forward(c, wts, cd, sd, x, ws, nws)
+    gpu.end()
+    ref = _oracle_forward(orc, cfg, w, x0, codes)
+    assert rel_err(from_dev(x), ref) <= 1e-5
+
+
 def test_dit_forward_rejects_bad_config(gpu, dgm):
     import torch
     cfg = dgm.DiTConfig(B=1, T=4, C=30, F=32, H=4, D=8, group=8)   # C != H*D
