@@ -12,6 +12,7 @@
 //    KV head when the caller repeats it, or of any head) stay in LDS, scores
 //    and probabilities of the 16 rows in LDS too. It also writes the scores
 //    and probabilities the reference's API returns.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -224,15 +225,6 @@ struct AttnArgs {
     int causal, rope, vmix;
 };
 
-__device__ __forceinline__ float rope_elem(const float* row, int d, int D, float c, float s) {
-#pragma clang fp contract(off)
-    const int mid = D >> 1;
-    const float rot = d < mid ? -row[d + mid] : row[d - mid];
-    const float a = row[d] * c;
-    const float b = rot * s;
-    return a + b;
-}
-
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) float sm[];
@@ -251,23 +243,88 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
 
-    // -- stage q (16 rows), k and v (T rows) of this (b, h).
-    for (int e = threadIdx.x; e < 16 * D; e += kThreads) {
-        const int t = e / D, d = e - t * D;
-        const float* row = a.q + size_t(b * T + t0 + t) * a.q_ld + h * D;
-        qs[t * qs_ld + d] = a.rope ? rope_elem(row, d, D, a.cosv[(t0 + t) * D + d], a.sinv[(t0 + t) * D + d]) : row[d];
-    }
-    for (int e = threadIdx.x; e < T * D; e += kThreads) {
-        const int t = e / D, d = e - t * D;
-        const float* krow = a.k + size_t(b * T + t) * a.kv_ld + hk * D;
-        ks[t * qs_ld + d] = a.rope ? rope_elem(krow, d, D, a.cosv[t * D + d], a.sinv[t * D + d]) : krow[d];
-        float vv = a.v[size_t(b * T + t) * a.kv_ld + hk * D + d];
-        if (a.vmix) {
-            const float p = a.ca * vv;
-            const float r = a.cb * a.vfirst[size_t(b * T + t) * a.vf_ld + d];
-            vv = p + r;
+    // -- stage q (16 rows), k and v (T rows) of this (b, h) in one pass of
+    // 16-byte loads, all issued before any is used (D % 16 == 0, rows 16-byte
+    // aligned). q and k are handled as chunk pairs (d .. d+3, d+D/2 .. d+D/2+3)
+    // so RoPE is applied in registers: each element from the unrotated pair
+    // and the table entries at its own index, as rope_fwd computes it.
+    const int cpr = D >> 2;                        // float4 chunks per row
+    const int hc = cpr >> 1, half = D >> 1;        // chunk pairs per row
+    const int nqp = 16 * hc, np = (16 + T) * hc;   // pairs: q rows first, then k rows
+    const int nv = T * cpr;                        // v chunks
+    constexpr int PB = 2, VB = 3;                  // pairs / v chunks per thread per batch
+    for (int bp = 0, bv = 0; bp < np || bv < nv; bp += PB * kThreads, bv += VB * kThreads) {
+        float4 x1[PB], x2[PB], c1[PB], c2[PB], s1[PB], s2[PB], vv[VB], fv[VB];
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+            const int e = min(bp + u * kThreads + int(threadIdx.x), np - 1);
+            const int row = e / hc, c = e - row * hc;
+            const int t = row < 16 ? t0 + row : row - 16;
+            const float* src = row < 16 ? a.q + size_t(b * T + t) * a.q_ld + h * D
+                                        : a.k + size_t(b * T + t) * a.kv_ld + hk * D;
+            x1[u] = *reinterpret_cast<const float4*>(src + 4 * c);
+            x2[u] = *reinterpret_cast<const float4*>(src + 4 * c + half);
+            if (a.rope) {
+                c1[u] = *reinterpret_cast<const float4*>(a.cosv + t * D + 4 * c);
+                c2[u] = *reinterpret_cast<const float4*>(a.cosv + t * D + 4 * c + half);
+                s1[u] = *reinterpret_cast<const float4*>(a.sinv + t * D + 4 * c);
+                s2[u] = *reinterpret_cast<const float4*>(a.sinv + t * D + 4 * c + half);
+            }
         }
-        vt[d * vt_ld + t] = vv;
+#pragma unroll
+        for (int u = 0; u < VB; ++u) {
+            const int e = min(bv + u * kThreads + int(threadIdx.x), nv - 1);
+            const int t = e / cpr, c = e - t * cpr;
+            const size_t r = size_t(b * T + t);
+            vv[u] = *reinterpret_cast<const float4*>(a.v + r * a.kv_ld + hk * D + 4 * c);
+            if (a.vmix) fv[u] = *reinterpret_cast<const float4*>(a.vfirst + r * a.vf_ld + 4 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+            const int e = bp + u * kThreads + int(threadIdx.x);
+            if (e >= np) break;
+            const int row = e / hc, c = e - row * hc;
+            float* dst = row < 16 ? qs + row * qs_ld : ks + (row - 16) * qs_ld;
+            float4 y1 = x1[u], y2 = x2[u];
+            if (a.rope) {
+                const float xa[4] = {x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+                const float xb[4] = {x2[u].x, x2[u].y, x2[u].z, x2[u].w};
+                const float ca4[4] = {c1[u].x, c1[u].y, c1[u].z, c1[u].w};
+                const float cb4[4] = {c2[u].x, c2[u].y, c2[u].z, c2[u].w};
+                const float sa4[4] = {s1[u].x, s1[u].y, s1[u].z, s1[u].w};
+                const float sb4[4] = {s2[u].x, s2[u].y, s2[u].z, s2[u].w};
+                float ya[4], yb[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p1 = xa[i] * ca4[i], r1 = -xb[i] * sa4[i];   // d < D/2: rot = -x[d + D/2]
+                    const float p2 = xb[i] * cb4[i], r2 = xa[i] * sb4[i];    // d >= D/2: rot = x[d - D/2]
+                    ya[i] = p1 + r1;
+                    yb[i] = p2 + r2;
+                }
+                y1 = make_float4(ya[0], ya[1], ya[2], ya[3]);
+                y2 = make_float4(yb[0], yb[1], yb[2], yb[3]);
+            }
+            *reinterpret_cast<float4*>(dst + 4 * c) = y1;
+            *reinterpret_cast<float4*>(dst + 4 * c + half) = y2;
+        }
+#pragma unroll
+        for (int u = 0; u < VB; ++u) {
+            const int e = bv + u * kThreads + int(threadIdx.x);
+            if (e >= nv) break;
+            const int t = e / cpr, c = e - t * cpr;
+            float v4[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+            if (a.vmix) {
+                const float f4[4] = {fv[u].x, fv[u].y, fv[u].z, fv[u].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = a.ca * v4[i];
+                    const float r = a.cb * f4[i];
+                    v4[i] = p + r;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vt[(4 * c + i) * vt_ld + t] = v4[i];
+        }
     }
     __syncthreads();
 
@@ -296,23 +353,27 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // -- row softmax: wave w takes rows w, w+4, ...; lanes stride the keys.
-    for (int t = wave; t < 16; t += 4) {
+    // -- row softmax (max, sum of exp, normalize as attn_softmax does): wave w
+    // takes rows 4w .. 4w+3 at once, 16 lanes per row, each lane T/16 keys.
+    {
+        const int t = 4 * wave + q4;
         float* row = ps + t * vt_ld;
         float* so = a.scores + (srow0 + t) * T;
         float* po = a.probs + (srow0 + t) * T;
         float mx = -INFINITY;
-        for (int s2 = lane; s2 < T; s2 += 64) {
-            so[s2] = row[s2];
-            mx = fmaxf(mx, row[s2]);
+        for (int s2 = r16; s2 < T; s2 += 16) {
+            const float v = row[s2];
+            so[s2] = v;
+            mx = fmaxf(mx, v);
         }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        for (int off = 8; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
         float sum = 0.0f;
-        for (int s2 = lane; s2 < T; s2 += 64) sum += expf(row[s2] - mx);
-        sum = wave_sum(sum);
+        for (int s2 = r16; s2 < T; s2 += 16) sum += expf(row[s2] - mx);
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 16);
         const float inv = 1.0f / sum;
-        for (int s2 = lane; s2 < T; s2 += 64) {
+        for (int s2 = r16; s2 < T; s2 += 16) {
             const float pv = expf(row[s2] - mx) * inv;
             row[s2] = pv;
             po[s2] = pv;
@@ -699,6 +760,8 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, 
     int rc = dgm::enter(g, "dit_forward");
     if (rc) return rc;
     if (!c || !w || !x || !ws || !cosv || !sinv) return dgm::fail(g, DGM_ERR_ARG, "dit_forward: null argument");
+    if (!dgm::aligned(x, 16) || !dgm::aligned(ws, 16) || !dgm::aligned(cosv, 16) || !dgm::aligned(sinv, 16))
+        return dgm::fail(g, DGM_ERR_ARG, "dit_forward: x, ws and the RoPE tables must be 16-byte aligned");
     if (c->bits != 4 && c->bits != 8 && c->bits != 32)
         return dgm::fail(g, DGM_ERR_BITS, "dit_forward: unsupported bits %d", c->bits);
     if (c->B <= 0 || c->T <= 0 || c->C <= 0 || c->F <= 0 || c->H <= 0 || c->D <= 0 || c->loops < 0 ||

@@ -226,7 +226,8 @@ int64_t dgm_dit_workspace_floats(const dgm_dit_cfg* cfg);
  * KV-head broadcast are applied inside the attention kernel, and each
  * RMSNorm + residual chain is one row kernel; every element is computed as
  * the standalone wrappers compute it. Needs T and D multiples of 16 and
- * C <= 1024 (DGM_ERR_UNSUPPORTED otherwise). Enqueued on the context's
+ * C <= 1024 (DGM_ERR_UNSUPPORTED otherwise); x, ws and the tables 16-byte
+ * aligned. Enqueued on the context's
  * stream; graph-capturable (no allocation, no host sync). */
 int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w,
                     const float* cos_t, const float* sin_t, float* x, float* ws,
