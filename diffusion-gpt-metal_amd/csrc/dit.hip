@@ -595,6 +595,256 @@ __global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(const float* __re
     y[i] = act * up[size_t(m) * ldu + j];
 }
 
+// ---- projection GEMM with the loop body's row chains fused in -------------------------
+// Y = X W^T over the group-quantized (or fp32) weights, for K = C (the rows of
+// the residual stream), where X is produced in the prologue from whole rows:
+//   pro 1: X = rms(a) * w1                                    (ln1 of loop 0)
+//   pro 2: mid = res + rms(a) * w1 -> side;  X = rms(mid) * w2  (ln2)
+//   pro 3: pre = res + rms(a) * w1;  x = rms(pre) * w2 -> side;  X = rms(x) * w3
+//          (the end of one loop and ln1 of the next)
+// A workgroup owns 16 rows; each of its 4 waves normalizes 4 of them (16 lanes
+// per row, each RMSNorm exactly rmsnorm_fwd's formula with a 16-lane
+// reduction), writes its rows into the LDS X block, and the column-tile-0
+// workgroup stores the side output. The GEMM part is the LDS-staged forward
+// (one contraction part per wave, 16-k weight runs per lane).
+// PAIR: the weight holds [gate; up] (F rows each); waves 0-1 compute gate and
+// waves 2-3 up for the same 32 columns, and the epilogue stores
+// swiglu = gate * sigmoid(gate) * up (swiglu_fwd) instead of the projections.
+struct DitGemmArgs {
+    const float *a, *res, *w1, *w2, *w3;
+    float* side;
+    const void* W;
+    const float* S;
+    float* out;
+    int M, N, K, G, groups, F;
+    float eps;
+    int pro;
+};
+
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
+    return v;
+}
+
+template <int J>
+__device__ __forceinline__ float rstd16(const float4 (&v)[J], int cols, float eps) {
+#pragma clang fp contract(off)
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        ss += v[j].x * v[j].x;
+        ss += v[j].y * v[j].y;
+        ss += v[j].z * v[j].z;
+        ss += v[j].w * v[j].w;
+    }
+    ss = sum16(ss);
+    const float mean = ss / float(cols);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+__device__ __forceinline__ float4 norm4(float4 v, float rs, float4 w) {
+#pragma clang fp contract(off)
+    return make_float4((v.x * rs) * w.x, (v.y * rs) * w.y, (v.z * rs) * w.z, (v.w * rs) * w.w);
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+template <int BITS, bool PAIR, int J>
+__global__ __launch_bounds__(kThreads) void dit_gemm_kernel(DitGemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) float4 xs4[];   // [16][K/4] slots, swizzled
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_i * tiles_j) return;
+    const int ti = t / tiles_j, tj = t - ti * tiles_j;
+    constexpr int TN = PAIR ? 32 : 64;
+    const int i0 = ti * 16, j0 = tj * TN;
+    const int K = a.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    // K == 64 * J: J stages of 64 contraction indices.
+    // -- weight row of this lane's column, all stages, issued first.
+    int n;
+    if constexpr (PAIR) n = (wave & 1) * 16 + r16 + j0, n = min(n, a.F - 1) + (wave >= 2 ? a.F : 0);
+    else n = min(j0 + wave * 16 + r16, a.N - 1);
+    uint32_t wc[J][BITS == 4 ? 2 : 4];
+    float4 wf[J][BITS == 32 ? 4 : 1];
+    float sc[J];
+#pragma unroll
+    for (int u = 0; u < J; ++u) {
+        const int k = u * 64 + 16 * q4;
+        if constexpr (BITS == 32) {
+            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.W) + size_t(n) * K + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wf[u][e] = p[e];
+        } else if constexpr (BITS == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.W) + size_t(n) * K + k);
+            wc[u][0] = v.x; wc[u][1] = v.y; wc[u][2] = v.z; wc[u][3] = v.w;
+            sc[u] = a.S[size_t(n) * a.groups + k / a.G];
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.W) + ((size_t(n) * K + k) >> 1));
+            wc[u][0] = v.x; wc[u][1] = v.y;
+            sc[u] = a.S[size_t(n) * a.groups + k / a.G];
+        }
+    }
+
+    // -- prologue: rows 4*wave + q4, lane r16 holds chunks r16 + 16 j (J = K / 64).
+    {
+        const int row = 4 * wave + q4;
+        const int gi = i0 + row;
+        const size_t base = size_t(min(gi, a.M - 1)) * K;
+        float4 v[J], rr[J], w1[J], w2[J], w3[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = 4 * (r16 + 16 * j);
+            v[j] = *reinterpret_cast<const float4*>(a.a + base + c);
+            w1[j] = *reinterpret_cast<const float4*>(a.w1 + c);
+            if (a.pro >= 2) {
+                rr[j] = *reinterpret_cast<const float4*>(a.res + base + c);
+                w2[j] = *reinterpret_cast<const float4*>(a.w2 + c);
+            }
+            if (a.pro == 3) w3[j] = *reinterpret_cast<const float4*>(a.w3 + c);
+        }
+        float rs = rstd16<J>(v, K, a.eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) v[j] = norm4(v[j], rs, w1[j]);
+        if (a.pro >= 2) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) v[j] = add4(rr[j], v[j]);
+            if (a.pro == 2 && tj == 0 && gi < a.M) {
+#pragma unroll
+                for (int j = 0; j < J; ++j) *reinterpret_cast<float4*>(a.side + base + 4 * (r16 + 16 * j)) = v[j];
+            }
+            rs = rstd16<J>(v, K, a.eps);
+#pragma unroll
+            for (int j = 0; j < J; ++j) v[j] = norm4(v[j], rs, w2[j]);
+            if (a.pro == 3) {
+                if (tj == 0 && gi < a.M) {
+#pragma unroll
+                    for (int j = 0; j < J; ++j) *reinterpret_cast<float4*>(a.side + base + 4 * (r16 + 16 * j)) = v[j];
+                }
+                rs = rstd16<J>(v, K, a.eps);
+#pragma unroll
+                for (int j = 0; j < J; ++j) v[j] = norm4(v[j], rs, w3[j]);
+            }
+        }
+        const int spr = K >> 2;
+#pragma unroll
+        for (int j = 0; j < J; ++j) xs4[row * spr + ((r16 + 16 * j) ^ (row & 15))] = v[j];
+    }
+    __syncthreads();
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int spr = K >> 2;
+    const float4* xrow = xs4 + r16 * spr;
+#pragma unroll
+    for (int u = 0; u < J; ++u) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 xv = xrow[(u * 16 + 4 * q4 + c) ^ r16];
+            float bv[4];
+            if constexpr (BITS == 32) {
+                const float4 w = wf[u][c];
+                bv[0] = w.x; bv[1] = w.y; bv[2] = w.z; bv[3] = w.w;
+            } else if constexpr (BITS == 8) {
+                const uint32_t w = wc[u][c];
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(int8_t((w >> (8 * s2)) & 0xFF))) * sc[u];
+            } else {
+                const uint32_t w = wc[u][c >> 1] >> (16 * (c & 1));
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    const int nib = int((w >> (4 * s2)) & 0xF);
+                    bv[s2] = float(nib >= 8 ? nib - 16 : nib) * sc[u];
+                }
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, bv[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, bv[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, bv[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, bv[3], acc, 0, 0, 0);
+        }
+    }
+
+    // acc[r]: row 4*q4 + r, column r16 of this wave's 16.
+    if constexpr (!PAIR) {
+        const int j = j0 + wave * 16 + r16;
+        if (j < a.N) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = i0 + 4 * q4 + r;
+                if (i < a.M) a.out[size_t(i) * a.N + j] = acc[r];
+            }
+        }
+    } else {
+        __syncthreads();   // X no longer read: reuse LDS for the up half
+        float* up = reinterpret_cast<float*>(xs4);   // [16][32]
+        if (wave >= 2) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) up[(4 * q4 + r) * 32 + (wave - 2) * 16 + r16] = acc[r];
+        }
+        __syncthreads();
+        if (wave < 2) {
+            const int j = j0 + wave * 16 + r16;
+            if (j < a.F) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = i0 + 4 * q4 + r;
+                    if (i < a.M) {
+                        const float z = acc[r];
+                        const float act = z * silu_sigmoid(z);
+                        a.out[size_t(i) * a.F + j] = act * up[(4 * q4 + r) * 32 + wave * 16 + r16];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int BITS, bool PAIR, int J>
+void launch_dit_gemm_j(const DitGemmArgs& a, hipStream_t st) {
+    constexpr int TN = PAIR ? 32 : 64;
+    const int ti = int(dgm::ceil_div(a.M, 16)), tj = int(dgm::ceil_div(PAIR ? a.F : a.N, TN));
+    const int64_t nt = int64_t(ti) * tj;
+    const int per = int((nt + 7) / 8);
+    hipLaunchKernelGGL((dit_gemm_kernel<BITS, PAIR, J>), dim3(unsigned(per) * 8u), dim3(kThreads),
+                       size_t(16) * a.K * sizeof(float), st, a, ti, tj, per);
+}
+
+template <int BITS, bool PAIR>
+int launch_dit_gemm_b(dgm_gpu* g, const DitGemmArgs& a) {
+    switch (a.K / 64) {
+        case 1: launch_dit_gemm_j<BITS, PAIR, 1>(a, g->stream); break;
+        case 2: launch_dit_gemm_j<BITS, PAIR, 2>(a, g->stream); break;
+        case 3: launch_dit_gemm_j<BITS, PAIR, 3>(a, g->stream); break;
+        case 4: launch_dit_gemm_j<BITS, PAIR, 4>(a, g->stream); break;
+        case 6: launch_dit_gemm_j<BITS, PAIR, 6>(a, g->stream); break;
+        case 8: launch_dit_gemm_j<BITS, PAIR, 8>(a, g->stream); break;
+        default: return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: fused projection needs C in {64,...,512}");
+    }
+    return dgm::check_launch(g, "dit_forward fused gemm");
+}
+
+int launch_dit_gemm(dgm_gpu* g, int bits, bool pair, const DitGemmArgs& a) {
+    if (bits == 8) return pair ? launch_dit_gemm_b<8, true>(g, a) : launch_dit_gemm_b<8, false>(g, a);
+    if (bits == 4) return pair ? launch_dit_gemm_b<4, true>(g, a) : launch_dit_gemm_b<4, false>(g, a);
+    return pair ? launch_dit_gemm_b<32, true>(g, a) : launch_dit_gemm_b<32, false>(g, a);
+}
+
+// The fused path's conditions: C a multiple of 64 with C / 64 in {1,2,3,4,6,8},
+// groups holding a 16-wide run, weights aligned for 8- / 16-byte loads.
+bool dit_fused_ok(const dgm_dit_cfg* c, const dgm_dit_weights* w) {
+    const int jb = c->C / 64;
+    if (c->C % 64 != 0 || !(jb == 1 || jb == 2 || jb == 3 || jb == 4 || jb == 6 || jb == 8)) return false;
+    if (c->bits == 32) return dgm::aligned(w->wq.w, 16) && dgm::aligned(w->wgate.w, 16);
+    if (c->group % 16 != 0) return false;
+    const size_t al = c->bits == 8 ? 16 : 8;
+    return dgm::aligned(w->wq.q, al) && dgm::aligned(w->wgate.q, al) && dgm::aligned(w->n1, 16) &&
+           dgm::aligned(w->n1b, 16) && dgm::aligned(w->n2, 16) && dgm::aligned(w->n2b, 16) &&
+           dgm::aligned(w->nf, 16);
+}
+
 // ---- the block orchestrator (src/DiT.swift:520-550) ---------------------------------
 // Workspace (floats, each piece 256-byte aligned):
 //   ln1 [M,C] | qkv0 [M,C+2D] | qkv1 [M,C+2D] | scores [B,H,T,T] | probs [B,H,T,T]
@@ -812,6 +1062,49 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, 
         int _r = (expr);             \
         if (_r != DGM_OK) return _r; \
     } while (0)
+    if (fuse_qkv && fuse_gu && dit_fused_ok(c, w)) {
+        // Five launches per loop: [row chain +] qkv projection, attention, wo,
+        // [row chain +] gate/up with SwiGLU, wdown; one row chain at the end.
+        auto pgemm = [&](const dgm_dit_linear& L, bool pair, int pro, const float* a_in, const float* res,
+                         const float* n_a, const float* n_b, const float* n_c, float* side, float* out,
+                         int64_t N) -> int {
+            DitGemmArgs d{};
+            d.a = a_in; d.res = res; d.w1 = n_a; d.w2 = n_b; d.w3 = n_c; d.side = side;
+            d.W = bits == 32 ? static_cast<const void*>(L.w) : L.q;
+            d.S = L.scale;
+            d.out = out;
+            d.M = int(M); d.N = int(N); d.K = int(C); d.G = bits == 32 ? 1 : G;
+            d.groups = bits == 32 ? 0 : int(C / G);
+            d.F = int(F); d.eps = c->eps; d.pro = pro;
+            return launch_dit_gemm(g, bits, pair, d);
+        };
+        for (int loop = 0; loop < c->loops; ++loop) {
+            float* qkv = p[loop == 0 ? QKV0 : QKV1];
+            if (loop == 0)
+                DGM_TRY(pgemm(w->wq, false, 1, x, nullptr, w->n1, nullptr, nullptr, nullptr, qkv, QKV));
+            else   // x = rms(mid + rms(mlp) * n2b) * nf; ln1 = rms(x) * n1
+                DGM_TRY(pgemm(w->wq, false, 3, p[MLP], p[MID], w->n2b, w->nf, w->n1, x, qkv, QKV));
+            AttnArgs aa{};
+            aa.q = qkv; aa.k = qkv + C; aa.v = qkv + C + KV; aa.vfirst = p[QKV0] + C + KV;
+            aa.cosv = cosv; aa.sinv = sinv;
+            aa.scores = p[SCORES]; aa.probs = p[PROBS]; aa.av = p[AV];
+            aa.B = B; aa.T = T; aa.H = H; aa.D = D;
+            aa.q_ld = aa.kv_ld = aa.vf_ld = int(QKV); aa.av_ld = int(C);
+            aa.kv_heads = 1;
+            aa.scale = 1.0f / sqrtf(float(D));
+            aa.ca = 1.0f - c->mix; aa.cb = c->mix;
+            aa.causal = 0; aa.rope = 1; aa.vmix = loop > 0;
+            DGM_TRY(launch_attn_mfma(g, aa));
+            DGM_TRY(gemm(w->wo, p[AV], p[ATTN], C, C));
+            // mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2; sw = swiglu(ln2 Wg^T, ln2 Wu^T)
+            DGM_TRY(pgemm(w->wgate, true, 2, p[ATTN], x, w->n1b, w->n2, nullptr, p[MID], p[SW], 2 * F));
+            DGM_TRY(gemm(w->wdown, p[SW], p[MLP], C, F));
+        }
+        if (c->loops > 0)
+            DGM_TRY(launch_row_fuse(g, p[MLP], p[MID], p[PRE], x, nullptr, w->n2b, w->nf, nullptr, p[RSTD], M, C,
+                                    c->eps));
+        return DGM_OK;
+    }
     DGM_TRY(launch_rms(g, x, p[LN1], p[RSTD], w->n1, M, C, c->eps));
     for (int loop = 0; loop < c->loops; ++loop) {
         float* qkv = p[loop == 0 ? QKV0 : QKV1];
