@@ -493,10 +493,13 @@ def main() -> int:
     per_kernel = {k: b.time_launches(kern[k], args.reps) for k in order}
     dom = max(per_kernel, key=per_kernel.get)
     flops_k = 2 * C2["M"] * C2["N"] * C2["K"]
+    # HIP kernel behind each entry point at the c2 shape (names as rocprofv3 prints them).
+    device_kernel = {"gemm_nt_i4": "gemm_fwd_lds_kernel<4, 4>", "gemm_dx_i4": "gemm_dx_lds_kernel<4>",
+                     "gemm_dw": "gemm_deep_kernel<2, 32, 16, 16, 12>"}
     roof = roofline(flops_k / per_kernel[dom] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
-                    traffic_for("c2", {"gemm_nt_i4": "gemm_f32_kernel<0", "gemm_dx_i4": "gemm_f32_kernel<1",
-                                       "gemm_dw": "gemm_f32_kernel<2"}[dom]))
+                    traffic_for("c2", device_kernel[dom]))
     roof["kernel"] = dom
+    roof["device_kernel"] = device_kernel[dom]
     roof["avg_launch_us"] = round(per_kernel[dom] * 1e3, 3)
     roof["algorithmic_bytes"] = c2_bytes()[dom]
     roof["algorithmic_flop"] = flops_k
