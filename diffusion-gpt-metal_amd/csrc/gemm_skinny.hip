@@ -40,7 +40,9 @@
 //
 // X pieces come either from LDS, computed by every workgroup for the few rows
 // of a GEMV-like call (FUSED), or from a workspace written by a one-pass
-// prepare kernel (larger M).
+// prepare kernel (larger M) in fragment-major order: each (k-block, tile, MFMA
+// half) is the 64 lanes' 16-byte A fragments as one contiguous 1 KB. Above 64
+// virtual rows the tiled kernel (further down) takes over.
 #include "common.hpp"
 
 namespace {
@@ -144,38 +146,6 @@ __device__ __forceinline__ void store_pieces16(int8_t* const (&base)[P], int k0,
             for (int i = 0; i < 16; ++i) w[i >> 2] |= (uint32_t(c[i][p]) & 0xFFu) << (8 * (i & 3));
             *reinterpret_cast<uint4*>(base[p] + k0) = make_uint4(w[0], w[1], w[2], w[3]);
         }
-    }
-}
-
-// ---- prepare kernel: X fp32 -> pieces + row multipliers ----------------------
-// One workgroup per row m of X. XP rows v = p * M + m.
-template <int BITS, int P>
-__global__ __launch_bounds__(256) void skinny_prepare_kernel(const float* __restrict__ X, int8_t* __restrict__ XP,
-                                                             float* __restrict__ XS, int M, int K) {
-    __shared__ float red[4];
-    const int m = blockIdx.x;
-    const float* xr = X + size_t(m) * K;
-    float mx = 0.0f;
-    for (int k = threadIdx.x * 4; k < K; k += 256 * 4) {
-        mx = absmax4(mx, *reinterpret_cast<const float4*>(xr + k));
-    }
-    mx = wave_max(mx);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = nmax(nmax(red[0], red[1]), nmax(red[2], red[3]));
-    const int sigma = row_sigma(mx);
-    if (threadIdx.x == 0) XS[m] = (mx <= 3.4e38f) ? ldexpf(1.0f, -sigma) : __builtin_nanf("");
-    int8_t* base[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) base[p] = XP + size_t(p * M + m) * K;
-    for (int k0 = threadIdx.x * 16; k0 < K; k0 += 256 * 16) {
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = *reinterpret_cast<const float4*>(xr + k0 + 4 * i);
-            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-        }
-        store_pieces16<BITS, P>(base, k0, x, sigma);
     }
 }
 
@@ -324,11 +294,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
         }
     } else {
         fetch_w(kb_begin);
+        // Prepared pieces are fragment-major (tiled_prepare_kernel with TP = T):
+        // fragment (kb, t, h) is 1 KB, lane-contiguous.
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const int v = t * 16 + l16;
-            alane[t] = a.XP + size_t(v < PM ? v : 0) * K + (BITS == 4 ? q * 32 : q * 16);
-        }
+        for (int t = 0; t < T; ++t) alane[t] = a.XP + size_t(t * H) * 1024 + lane * 16;
     }
 
     i32x4 af[2][T][H];
@@ -337,8 +306,12 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int h = 0; h < H; ++h)
-                af[st][t][h] = *reinterpret_cast<const i32x4*>(alane[t] + size_t(kb) * KBK + h * 16);
+            for (int h = 0; h < H; ++h) {
+                if constexpr (FUSED)
+                    af[st][t][h] = *reinterpret_cast<const i32x4*>(alane[t] + size_t(kb) * KBK + h * 16);
+                else
+                    af[st][t][h] = *reinterpret_cast<const i32x4*>(alane[t] + (size_t(kb) * T * H + h) * 1024);
+            }
     };
 
     f32x4 acc[S][T];
@@ -483,6 +456,275 @@ int launch_skinny(dgm_gpu* g, const SkinnyArgs& a, hipStream_t st) {
     return launch_kernel<BITS, P, T, S, KBW, WAVES, FM, false>(g, a, st);
 }
 
+// ---- tiled decode kernel (virtual rows 17 .. 192, i.e. 8 <= M <= 64) ----------
+// For more than a handful of rows the per-workgroup share of X pieces, not W,
+// sets the time: the k-split kernel above makes every workgroup read all
+// P*M*K bytes of pieces with 16-row fragment loads. Here:
+//  * the prepare pass writes the pieces fragment-major: for each k-block, tile
+//    and MFMA half, the 64 lanes' 16-byte A fragments are one contiguous 1 KB,
+//    so staging is whole-line traffic;
+//  * a workgroup owns 64 columns of W (4 strips) over all of K, and its 4 waves
+//    split the virtual-row tiles (TW each), so a wave holds only TW x 4 tiles of
+//    accumulators;
+//  * per chunk of KC k-blocks, the A fragments and the 64 W rows go global ->
+//    LDS with direct loads (double-buffered, one barrier per chunk); the W rows
+//    land with 16-byte slots XOR-swizzled by row so fragment reads are free of
+//    bank conflicts; the scales of the 64 rows are staged once.
+// Each k-block: int32 MFMA partials over the k-block, then one fp32 scaling per
+// group as in the k-split kernel (the reference's order).
+
+// Prepare: one workgroup per row m of X; fragment-major pieces, zero rows up to
+// 16 * TP.
+template <int BITS, int P>
+__global__ __launch_bounds__(256) void tiled_prepare_kernel(const float* __restrict__ X, int8_t* __restrict__ XP,
+                                                            float* __restrict__ XS, int M, int K, int TP) {
+    constexpr int KBK = KBlock<BITS>::K, H = KBlock<BITS>::H;
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const float* xr = X + size_t(m) * K;
+    float mx = 0.0f;
+    for (int k = threadIdx.x * 4; k < K; k += 256 * 4) mx = absmax4(mx, *reinterpret_cast<const float4*>(xr + k));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = nmax(nmax(red[0], red[1]), nmax(red[2], red[3]));
+    const int sigma = row_sigma(mx);
+    if (threadIdx.x == 0) XS[m] = (mx <= 3.4e38f) ? ldexpf(1.0f, -sigma) : __builtin_nanf("");
+    for (int k0 = threadIdx.x * 16; k0 < K; k0 += 256 * 16) {
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + k0 + 4 * i);
+            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+        }
+        int c[16][3];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) split_pieces(x[i], sigma, c[i]);
+        const int kb = k0 / KBK, kk = k0 - kb * KBK;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int v = p * M + m, t = v >> 4, l16 = v & 15;
+            if constexpr (BITS == 4) {
+                const int q = kk >> 5, half = (kk >> 4) & 1;
+                uint32_t e0 = 0, e1 = 0, o0 = 0, o1 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    e0 |= (uint32_t(c[2 * i][p]) & 0xFFu) << (8 * i);
+                    e1 |= (uint32_t(c[8 + 2 * i][p]) & 0xFFu) << (8 * i);
+                    o0 |= (uint32_t(c[2 * i + 1][p]) & 0xFFu) << (8 * i);
+                    o1 |= (uint32_t(c[8 + 2 * i + 1][p]) & 0xFFu) << (8 * i);
+                }
+                int8_t* f = XP + size_t((kb * TP + t) * H) * 1024 + (q * 16 + l16) * 16 + half * 8;
+                *reinterpret_cast<uint2*>(f) = make_uint2(e0, e1);
+                *reinterpret_cast<uint2*>(f + 1024) = make_uint2(o0, o1);
+            } else {
+                const int q = kk >> 4;
+                uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 16; ++i) w[i >> 2] |= (uint32_t(c[i][p]) & 0xFFu) << (8 * (i & 3));
+                *reinterpret_cast<uint4*>(XP + size_t(kb * TP + t) * 1024 + (q * 16 + l16) * 16) =
+                    make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+    }
+    // Padding rows (P*M .. 16*TP - 1) are zero so their products vanish.
+    const int nkb = K / KBK;
+    for (int v = P * M + m; v < 16 * TP; v += M) {
+        const int t = v >> 4, l16 = v & 15;
+        for (int e = threadIdx.x; e < nkb * H * 4; e += 256) {
+            const int q = e & 3, h = (e >> 2) % H, kb = (e >> 2) / H;
+            *reinterpret_cast<uint4*>(XP + size_t((kb * TP + t) * H + h) * 1024 + (q * 16 + l16) * 16) =
+                make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+struct TiledArgs {
+    const uint8_t* W;
+    const float* S;
+    const int8_t* XP;
+    const float* XS;
+    const float* bias;
+    float* Y;
+    int M, N, K, groups, gshift, has_bias;
+};
+
+typedef __attribute__((address_space(1))) const void global_cvoid;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BITS, int TW>
+struct TiledShape {
+    static constexpr int KBK = KBlock<BITS>::K, H = KBlock<BITS>::H;
+    static constexpr int TP = 4 * TW;
+    static constexpr int KC = TW == 1 ? 4 : 2;               // k-blocks per chunk
+    static constexpr int ABYTES = TP * H * KC * 1024;       // A fragments of a chunk
+    static constexpr int SPR = KC * 4;                      // 16-byte slots of a W row per chunk
+    static constexpr int WBYTES = 64 * SPR * 16;            // 64 W rows
+    static constexpr int BUF = ABYTES + WBYTES;
+};
+
+template <int BITS, int P, int TW>
+__global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
+    using SH = TiledShape<BITS, TW>;
+    constexpr int KBK = SH::KBK, H = SH::H, TP = SH::TP, KC = SH::KC, SPR = SH::SPR;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, q = lane >> 4;
+    const int K = a.K, N = a.N, M = a.M, groups = a.groups;
+    const int n0 = blockIdx.x * 64;
+    const int nch = K / (KBK * KC);
+    const size_t wrow = BITS == 4 ? size_t(K) / 2 : size_t(K);
+    float* scl = reinterpret_cast<float*>(smem);                       // [64][groups]
+    const int sbytes = (64 * groups * 4 + 15) & ~15;
+    uint8_t* bufs = smem + sbytes;
+
+    // -- scales of the 64 rows, once (16-byte units; groups % 4 == 0).
+    {
+        const int upr = groups >> 2, units = 64 * upr;
+        for (int u0 = wave * 64; u0 < units; u0 += 256) {
+            const int u = u0 + lane;
+            const int row = u / upr, c = u - row * upr;
+            const float* src = a.S + size_t(min(n0 + row, N - 1)) * groups + 4 * c;
+            __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(smem + u0 * 16), 16, 0, 0);
+        }
+    }
+    // -- one chunk: A fragments (contiguous in XP) and 64 W rows x KC k-blocks.
+    auto issue = [&](int ch, int b) {
+        uint8_t* dst = bufs + b * SH::BUF;
+        const int8_t* asrc = a.XP + size_t(ch) * SH::ABYTES;
+        for (int i = wave; i < SH::ABYTES / 1024; i += 4)
+            __builtin_amdgcn_global_load_lds((global_cvoid*)(asrc + i * 1024 + lane * 16), (lds_void*)(dst + i * 1024),
+                                             16, 0, 0);
+        uint8_t* wdst = dst + SH::ABYTES;
+        constexpr int RPI = 64 / SPR;   // W rows per instruction
+        for (int i = wave; i < SH::WBYTES / 1024; i += 4) {
+            const int row = i * RPI + lane / SPR, slot = lane % SPR;
+            const uint8_t* src = a.W + size_t(min(n0 + row, N - 1)) * wrow + size_t(ch) * KC * 64 +
+                                 ((slot ^ (row & (SPR - 1))) << 4);
+            __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(wdst + i * 1024), 16, 0, 0);
+        }
+    };
+
+    f32x4 acc[4][TW];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < TW; ++t) acc[s][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](int ch, int b) {
+        const uint8_t* src = bufs + b * SH::BUF;
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+            i32x4 af[TW][H];
+#pragma unroll
+            for (int t = 0; t < TW; ++t)
+#pragma unroll
+                for (int h = 0; h < H; ++h)
+                    af[t][h] = *reinterpret_cast<const i32x4*>(src + ((kk * TP + wave * TW + t) * H + h) * 1024 + lane * 16);
+            const int g = (ch * KC + kk) >> a.gshift;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int row = 16 * s + l16;
+                const i32x4 w = *reinterpret_cast<const i32x4*>(src + SH::ABYTES + row * (SPR * 16) +
+                                                                (((kk * 4 + q) ^ (row & (SPR - 1))) << 4));
+                i32x4 bw[H];
+                if constexpr (BITS == 4) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        bw[0][j] = int((uint32_t(w[j]) << 4) & 0xF0F0F0F0u);   // even k: 16*code
+                        bw[H - 1][j] = int(uint32_t(w[j]) & 0xF0F0F0F0u);      // odd k: 16*code
+                    }
+                } else {
+                    bw[0] = w;
+                }
+                const float sv = scl[row * groups + g];
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    i32x4 part = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[t][0], bw[0], i32x4{0, 0, 0, 0}, 0, 0, 0);
+                    if constexpr (H == 2) part = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[t][1], bw[1], part, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[s][t][r] += float(part[r]) * sv;
+                }
+            }
+        }
+    };
+
+    issue(0, 0);
+    for (int ch = 0; ch < nch; ch += 2) {
+        __syncthreads();   // chunk ch (and the scales) landed; buffer 1 is free
+        issue(min(ch + 1, nch - 1), 1);
+        compute(ch, 0);
+        if (ch + 1 >= nch) break;
+        __syncthreads();
+        issue(min(ch + 2, nch - 1), 0);
+        compute(ch + 1, 1);
+    }
+
+    // -- combine the pieces of each row: y = 2^-sigma (a0 + a1/128 + a2/128^2) [/16] + bias.
+    __syncthreads();   // also drains the last (redundant) chunk load
+    float* tile = reinterpret_cast<float*>(bufs);   // [16 * TP][64]
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tile[(16 * (wave * TW + t) + 4 * q + r) * 64 + 16 * s + l16] = acc[s][t][r];
+    __syncthreads();
+    const float kshift = BITS == 4 ? 0.0625f : 1.0f;
+    for (int idx = threadIdx.x; idx < M * 64; idx += 256) {
+        const int m = idx >> 6, c = idx & 63;
+        const int n = n0 + c;
+        if (n >= N) continue;
+        float u = 0.0f;
+#pragma unroll
+        for (int p = P - 1; p >= 0; --p) u = tile[(p * M + m) * 64 + c] + u * 0.0078125f;
+        float y = u * a.XS[m];
+        y *= kshift;
+        if (a.has_bias) y += a.bias[n];
+        a.Y[size_t(m) * N + n] = y;
+    }
+}
+
+inline int K_of(const SkinnyArgs& s) { return s.K; }
+
+template <int BITS, int P, int TW>
+int launch_tiled(dgm_gpu* g, const SkinnyArgs& s, hipStream_t st) {
+    using SH = TiledShape<BITS, TW>;
+    const int TP = SH::TP;
+    const size_t xp_bytes = size_t(K_of(s)) / SH::KBK * TP * SH::H * 1024;
+    uint8_t* ws = static_cast<uint8_t*>(dgm::workspace(g, xp_bytes + 64 * sizeof(float) + 256));
+    if (!ws) return DGM_ERR_HIP;
+    int8_t* xp = reinterpret_cast<int8_t*>(ws);
+    float* xs = reinterpret_cast<float*>(ws + ((xp_bytes + 255) & ~size_t(255)));
+    hipLaunchKernelGGL((tiled_prepare_kernel<BITS, P>), dim3(s.M), dim3(256), 0, st, s.X, xp, xs, s.M, s.K, TP);
+    TiledArgs a{};
+    a.W = s.W; a.S = s.S; a.XP = xp; a.XS = xs; a.bias = s.bias; a.Y = s.Y;
+    a.M = s.M; a.N = s.N; a.K = s.K; a.groups = s.groups; a.gshift = s.gshift; a.has_bias = s.has_bias;
+    const size_t sbytes = (size_t(64) * s.groups * 4 + 15) & ~size_t(15);
+    const size_t lds = sbytes + 2 * size_t(SH::BUF);
+    auto kern = tiled_kernel<BITS, P, TW>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "skinny: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(kern, dim3(unsigned((s.N + 63) / 64)), dim3(256), lds, st, a);
+    return DGM_OK;
+}
+
+// The tiled kernel's conditions: whole chunks of k-blocks, scale rows in
+// 16-byte units that fit LDS next to two buffers, and the combine tile
+// (16 * TP x 64 floats) inside the two buffers.
+template <int BITS, int TW>
+bool tiled_fits(const SkinnyArgs& s) {
+    using SH = TiledShape<BITS, TW>;
+    if (s.K % (SH::KBK * SH::KC) != 0) return false;
+    if (s.groups % 4 != 0 || !dgm::aligned(s.S, 16)) return false;
+    const size_t lds = ((size_t(64) * s.groups * 4 + 15) & ~size_t(15)) + 2 * size_t(SH::BUF);
+    return lds <= 160 * 1024 && size_t(16) * SH::TP * 64 * 4 <= 2 * size_t(SH::BUF);
+}
+
 template <int BITS, int P>
 int dispatch_pieces(dgm_gpu* g, SkinnyArgs& a, hipStream_t st) {
     const int M = a.M;
@@ -494,17 +736,25 @@ int dispatch_pieces(dgm_gpu* g, SkinnyArgs& a, hipStream_t st) {
         if (M == 1) return launch_skinny<BITS, P, 1, 2, 8, 4, 1>(g, a, st);
         if (M <= 4) return launch_skinny<BITS, P, 1, 2, 8, 4, 4>(g, a, st);
     }
-    const size_t xp_bytes = size_t(rows) * a.K;
+    // Beyond 4 tiles of virtual rows the accumulators of the k-split kernel
+    // crowd the register file; the tiled kernel splits the rows over waves.
+    if (rows > 64 && rows <= 192) {
+        if (rows <= 128 && tiled_fits<BITS, 2>(a)) return launch_tiled<BITS, P, 2>(g, a, st);
+        if (tiled_fits<BITS, 3>(a)) return launch_tiled<BITS, P, 3>(g, a, st);
+    }
+    // Every workgroup reads all of the pieces (P*M*K bytes), so many strips per
+    // workgroup; registers then bound waves x k-blocks per round. The pieces
+    // are prepared fragment-major for the chosen tile count.
+    const int T = (rows + 15) / 16;
+    const int TT = T <= 4 ? T : (T <= 8 ? 8 : 12);
+    const size_t xp_bytes = size_t(a.K / KBlock<BITS>::K) * TT * KBlock<BITS>::H * 1024;
     uint8_t* ws = static_cast<uint8_t*>(dgm::workspace(g, xp_bytes + 64 * sizeof(float) + 256));
     if (!ws) return DGM_ERR_HIP;
     int8_t* xp = reinterpret_cast<int8_t*>(ws);
     float* xs = reinterpret_cast<float*>(ws + ((xp_bytes + 255) & ~size_t(255)));
-    hipLaunchKernelGGL((skinny_prepare_kernel<BITS, P>), dim3(M), dim3(256), 0, st, a.X, xp, xs, M, a.K);
+    hipLaunchKernelGGL((tiled_prepare_kernel<BITS, P>), dim3(M), dim3(256), 0, st, a.X, xp, xs, M, a.K, TT);
     a.XP = xp;
     a.XS = xs;
-    // Every workgroup reads all of the pieces (P*M*K bytes), so many strips per
-    // workgroup; registers then bound waves x k-blocks per round.
-    const int T = (rows + 15) / 16;
     if (T <= 1) return launch_skinny<BITS, P, 1, 4, 4, 8, 0>(g, a, st);
     if (T <= 2) return launch_skinny<BITS, P, 2, 4, 4, 8, 0>(g, a, st);
     if (T <= 3) return launch_skinny<BITS, P, 3, 4, 8, 4, 0>(g, a, st);

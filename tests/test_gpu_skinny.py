@@ -88,6 +88,25 @@ def test_ragged_skinny(gpu, dgm, orc, bits, G, M, N, Kb):
     assert rel_err(y, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("bits,G,K", [(4, 128, 4096), (4, 256, 2048), (8, 64, 2048), (8, 128, 1536)])
+@pytest.mark.parametrize("M", [6, 8, 16, 22, 43, 64])
+def test_tiled_decode_many_chunks(gpu, dgm, orc, bits, G, K, M):
+    """8 <= P*M <= 192 virtual rows with long K: the tiled decode kernel (fragment-major
+    pieces, double-buffered chunks, ragged N); both math modes."""
+    N = 300
+    rng = np.random.default_rng(M * 31 + K + bits)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    x[: K] *= np.float32(1e-3)                     # rows of different magnitude
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if M % 2 == 0 else None
+    q, s = _quantize(gpu, to_dev(w), N, K, G, bits)
+    ref = _ref(orc, q, s, x, bias, M, N, K, G, bits)
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_FP32)
+    assert rel_err(y, ref) <= 1e-5
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16)
+    assert rel_err(y, ref) <= 1e-2
+
+
 def test_rows_of_very_different_magnitude(gpu, dgm, orc):
     """Each row carries its own power-of-two scale: a tiny row next to a huge
     one keeps its own relative accuracy."""
