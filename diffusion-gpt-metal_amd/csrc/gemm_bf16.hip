@@ -152,15 +152,21 @@ __global__ __launch_bounds__(NT8) void gemm_bf16_w8_kernel(Bf16Args a) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) {   // 8 nibbles = k 8d..8d+7 of the half
                 const uint32_t x = w4[d] ^ 0x88888888u;
-                const uint32_t lo = (x << 4) & 0xF0F0F0F0u;
-                const uint32_t hi = x & 0xF0F0F0F0u;
+                uint32_t lo = (x << 4) & 0xF0F0F0F0u;
+                uint32_t hi = x & 0xF0F0F0F0u;
+                // Opaque to the optimizer (no instruction): keeps each byte
+                // extraction below a single v_cvt_f32_ubyte{0..3} instead of a
+                // shift and mask folded into every byte.
+                asm("" : "+v"(lo));
+                asm("" : "+v"(hi));
+                const float fe[4] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
+                                     float(lo >> 24)};
+                const float fo[4] = {float(hi & 0xFFu), float((hi >> 8) & 0xFFu), float((hi >> 16) & 0xFFu),
+                                     float(hi >> 24)};
                 uint32_t o[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float fe = float((lo >> (8 * i)) & 0xFFu);
-                    const float fo = float((hi >> (8 * i)) & 0xFFu);
-                    o[i] = pack_bf16(__builtin_fmaf(fe, s16, off), __builtin_fmaf(fo, s16, off));
-                }
+                for (int i = 0; i < 4; ++i)
+                    o[i] = pack_bf16(__builtin_fmaf(fe[i], s16, off), __builtin_fmaf(fo[i], s16, off));
                 *reinterpret_cast<uint4*>(Bs + swz(brow, bh * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
             }
         } else {
