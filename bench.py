@@ -495,7 +495,7 @@ def main() -> int:
     flops_k = 2 * C2["M"] * C2["N"] * C2["K"]
     # HIP kernel behind each entry point at the c2 shape (names as rocprofv3 prints them).
     device_kernel = {"gemm_nt_i4": "gemm_fwd_lds_kernel<4, 4>", "gemm_dx_i4": "gemm_dx_lds_kernel<4>",
-                     "gemm_dw": "gemm_deep_kernel<2, 32, 16, 16, 12>"}
+                     "gemm_dw": "gemm_dw_pair_kernel"}
     roof = roofline(flops_k / per_kernel[dom] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
                     traffic_for("c2", device_kernel[dom]))
     roof["kernel"] = dom

@@ -759,6 +759,89 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
     return DGM_OK;
 }
 
+// ---- dW with paired columns (M % 64 == 0, N % 2 == 0) ---------------------------
+// dW[n, k] (=|+=) sum_m dY[m, n] * X[m, k]. A workgroup owns 32 rows (n) x 16
+// columns (k) of dW; its 4 waves split M and load their operands straight into
+// registers, every load of the wave's range issued before the first MFMA. A
+// lane reads dY[m, n0 + 2i .. n0 + 2i + 1] as one 8-byte load, so 16 lanes cover
+// a whole 128-byte line of a dY row; the even and odd columns feed two MFMA
+// tiles (dW rows n0 + 2r and n0 + 2r + 1). At step s a lane group q uses row
+// m = m0 + q + 4 s. Wave partials are reduced through LDS in a fixed order.
+constexpr int DWP_CH = 8;   // 16-row chunks per wave and round
+
+__global__ __launch_bounds__(kThreads) void gemm_dw_pair_kernel(GemmArgs a, int tiles_n, int tiles_k, int per_xcd) {
+    __shared__ float part[4][2][16][16];
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_n * tiles_k) return;
+    const int tk = t / tiles_n, tn = t - tk * tiles_n;
+    const int n0 = tn * 32, k0 = tk * 16;
+    const int M = a.M, N = a.N, K = a.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int nc = min(n0 + 2 * r16, N - 2);   // pairs past N: clamped, never stored
+    const int kc = min(k0 + r16, K - 1);
+    const float* X = static_cast<const float*>(a.B);
+    const int per = M >> 2;
+    const int mb = wave * per;
+
+    f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    for (int r0 = mb; r0 < mb + per; r0 += 16 * DWP_CH) {
+        float2 av[DWP_CH][4];
+        float bv[DWP_CH][4];
+#pragma unroll
+        for (int c = 0; c < DWP_CH; ++c) {
+            const int m0 = min(r0 + 16 * c, mb + per - 16);   // past the range: re-read, not computed
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const int m = m0 + q4 + 4 * s2;
+                av[c][s2] = *reinterpret_cast<const float2*>(a.A + size_t(m) * N + nc);
+                bv[c][s2] = X[size_t(m) * K + kc];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // every load of the round before the first MFMA
+#pragma unroll
+        for (int c = 0; c < DWP_CH; ++c) {
+            if (r0 + 16 * c >= mb + per) continue;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][s2].x, bv[c][s2], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][s2].y, bv[c][s2], acc1, 0, 0, 0);
+            }
+        }
+    }
+    // acc_e[r]: dW row n0 + 2 (4 q4 + r) + e, column k0 + r16.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        part[wave][0][4 * q4 + r][r16] = acc0[r];
+        part[wave][1][4 * q4 + r][r16] = acc1[r];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 32 * 16; e += kThreads) {
+        const int il = e >> 4, j = e & 15;   // il: local dW row 0..31
+        const int i = n0 + il, k = k0 + j;
+        if (i >= N || k >= K) continue;
+        const int rr = il >> 1, par = il & 1;
+        float v = part[0][par][rr][j];
+        v += part[1][par][rr][j];
+        v += part[2][par][rr][j];
+        v += part[3][par][rr][j];
+        float* o = a.out + size_t(i) * K + k;
+        if (a.accumulate) *o += v;
+        else *o = v;
+    }
+}
+
+bool dw_pair_ok(const GemmArgs& a, const void* dY) {
+    return a.M > 0 && a.M % 64 == 0 && a.N >= 2 && a.N % 2 == 0 && a.K > 0 && dgm::aligned(dY, 8);
+}
+
+void launch_dw_pair(const GemmArgs& a, hipStream_t st) {
+    const int tn = int(dgm::ceil_div(a.N, 32)), tk = int(dgm::ceil_div(a.K, 16));
+    const int64_t nt = int64_t(tn) * tk;
+    const int per = int((nt + 7) / 8);
+    hipLaunchKernelGGL(gemm_dw_pair_kernel, dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn, tk, per);
+}
+
 template <int MODE, int BITS, int TM, int TN>
 void launch_tile(const GemmArgs& a, bool vec, hipStream_t st) {
     dim3 grid(dgm::ceil_div(a.cols, TN), dgm::ceil_div(a.rows, TM));
@@ -879,6 +962,10 @@ int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dg
     a.rows = p->N; a.cols = p->K; a.red = p->M;
     a.G = 1; a.groups = 0;
     a.accumulate = accumulate;
+    if (dw_pair_ok(a, dY)) {
+        launch_dw_pair(a, g->stream);
+        return DGM_OK;
+    }
     if (deep_ok<MODE_DW>(a, 32, false)) launch_deep<MODE_DW, 32>(a, g->num_cus, g->stream);
     else launch_gemm<MODE_DW, 32>(a, false, g->num_cus, g->stream);
     return DGM_OK;

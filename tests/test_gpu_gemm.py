@@ -169,6 +169,28 @@ def test_multiple_of_16_contractions(gpu, orc, M, N, K, G, bits):
     assert max(errs.values()) <= TOL, errs
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 20, 36), (128, 36, 100), (448, 52, 44), (192, 12, 8), (512, 192, 768),
+                                   (64, 4, 4), (320, 100, 260)])
+def test_dw_shapes(gpu, orc, M, N, K):
+    """dW / dW += over contractions that are multiples of 64 with ragged output
+    tiles (rows and columns past N or K clamped, never stored)."""
+    import torch
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    dy = rng.standard_normal(M * N).astype(np.float32)
+    dw0 = rng.standard_normal(N * K).astype(np.float32)
+    xd, dyd = to_dev(x), to_dev(dy)
+    dw = torch.full((N * K,), float("nan"), device="cuda")
+    dwa = to_dev(dw0)
+    gpu.begin()
+    gpu.gemmDW(dyd, xd, dw, M, N, K)
+    gpu.gemmDWAcc(dyd, xd, dwa, M, N, K)
+    gpu.end()
+    ref = dy.reshape(M, N).astype(np.float64).T @ x.reshape(M, K).astype(np.float64)
+    assert rel_err(from_dev(dw), ref.ravel()) <= TOL
+    assert rel_err(from_dev(dwa), ref.ravel() + dw0) <= TOL
+
+
 def test_unaligned_operands(gpu, orc):
     import torch
     M, N, K, G = 20, 24, 64, 16
