@@ -9,7 +9,8 @@ from .abi import (DGM_ERR_ARG, DGM_ERR_BITS, DGM_ERR_HIP, DGM_ERR_NOT_BEGUN,
                   DGM_ERR_SHAPE, DGM_ERR_UNSUPPORTED, DGM_MATH_BF16,
                   DGM_MATH_FP32, DGM_OK, HEADER, LIB_PATH, PROTOTYPES,
                   DIT_LINEARS, DIT_NORMS, DgmError, DiTCfg, DiTLinear,
-                  DiTWeights, GemmP, QuantP, load_library)
+                  DiTWeights, GemmP, QuantP, AdamP, EmbP, EmbBwdP, PosP, BiasP,
+                  ReduceP, ScaleP, UnaryP, load_library)
 from .gpu import GPU, Buf, RawBuf
 from .dit import DiTBlock, DiTConfig, rope_tables
 
@@ -18,5 +19,6 @@ __all__ = [
     "LIB_PATH", "HEADER", "PROTOTYPES", "DGM_OK", "DGM_ERR_ARG", "DGM_ERR_SHAPE",
     "DGM_ERR_NOT_BEGUN", "DGM_ERR_HIP", "DGM_ERR_BITS", "DGM_ERR_UNSUPPORTED",
     "DGM_MATH_FP32", "DGM_MATH_BF16", "DiTBlock", "DiTConfig", "DiTCfg", "DiTLinear",
-    "DiTWeights", "DIT_LINEARS", "DIT_NORMS", "rope_tables",
+    "DiTWeights", "DIT_LINEARS", "DIT_NORMS", "rope_tables", "AdamP", "EmbP", "EmbBwdP",
+    "PosP", "BiasP", "ReduceP", "ScaleP", "UnaryP",
 ]

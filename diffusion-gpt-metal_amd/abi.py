@@ -1,6 +1,6 @@
 """ctypes binding of include/dgm_quant.h (libdgm_amd.so).
 
-Only plumbing: prototypes, the two parameter-block structs and the status
+Only plumbing: prototypes, the parameter-block structs and the status
 codes. The HIP library is required; there is no fallback of any kind, and a
 missing library raises at load time.
 """
@@ -58,6 +58,55 @@ class DiTWeights(ctypes.Structure):
     """dgm_dit_weights: the block's parameters (src/DiT.swift:242-253)."""
     _fields_ = [(n, DiTLinear) for n in DIT_LINEARS] + [(n, ctypes.c_void_p) for n in DIT_NORMS]
 
+
+def _u32s(*names):
+    return [(n, ctypes.c_uint32) for n in names]
+
+
+class AdamP(ctypes.Structure):
+    """src/Params.swift:138-147 — n (u32) and seven f32; 32 bytes."""
+    _fields_ = [("n", ctypes.c_uint32)] + [(n, ctypes.c_float) for n in
+                                          ("lr", "b1", "b2", "eps", "wd", "invBC1", "invBC2")]
+
+
+class EmbP(ctypes.Structure):
+    """src/Params.swift:78-83."""
+    _fields_ = _u32s("B", "T", "C", "qGroup")
+
+
+class EmbBwdP(ctypes.Structure):
+    """src/Params.swift:85-90."""
+    _fields_ = _u32s("B", "T", "C", "V")
+
+
+class PosP(ctypes.Structure):
+    """src/Params.swift:92-97."""
+    _fields_ = _u32s("B", "T", "C", "pad")
+
+
+class BiasP(ctypes.Structure):
+    """src/Params.swift:46-51."""
+    _fields_ = _u32s("M", "N", "pad0", "pad1")
+
+
+class ReduceP(ctypes.Structure):
+    """src/Params.swift:106-111."""
+    _fields_ = _u32s("n", "slot", "pad0", "pad1")
+
+
+class ScaleP(ctypes.Structure):
+    """src/Params.swift:39-44."""
+    _fields_ = [("n", ctypes.c_uint32), ("s", ctypes.c_float), ("pad0", ctypes.c_uint32), ("pad1", ctypes.c_uint32)]
+
+
+class UnaryP(ctypes.Structure):
+    """src/Params.swift:32-37."""
+    _fields_ = _u32s("n", "pad0", "pad1", "pad2")
+
+
+assert ctypes.sizeof(AdamP) == 32
+assert all(ctypes.sizeof(t) == 16 for t in (EmbP, EmbBwdP, PosP, BiasP, ReduceP, ScaleP, UnaryP))
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
@@ -103,6 +152,25 @@ PROTOTYPES = {
     "dgm_ropeTables": (_I, [_I64, _I64, _F, _P, _P]),
     "dgm_dit_workspace_floats": (_I64, [ctypes.POINTER(DiTCfg)]),
     "dgm_dit_forward": (_I, [_P, ctypes.POINTER(DiTCfg), ctypes.POINTER(DiTWeights), _P, _P, _P, _P, _I64]),
+    "dgm_adamw": (_I, [_P, _P, _P, _P, _P, ctypes.POINTER(AdamP)]),
+    "dgm_adam": (_I, [_P, _P, _P, _P, _P, _I64] + [_F] * 7),
+    "dgm_adam_quantize": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64] + [_F] * 7),
+    "dgm_reduce_sumsq": (_I, [_P, _P, _P, ctypes.POINTER(ReduceP)]),
+    "dgm_reduceSumsq": (_I, [_P, _P, _P, _I64, _I64]),
+    "dgm_zero_f": (_I, [_P, _P, ctypes.POINTER(UnaryP)]),
+    "dgm_scale_f": (_I, [_P, _P, ctypes.POINTER(ScaleP)]),
+    "dgm_zero": (_I, [_P, _P, _I64]),
+    "dgm_scale": (_I, [_P, _P, _I64, _F]),
+    "dgm_embed_f32": (_I, [_P, _P, _P, _P, _P, ctypes.POINTER(EmbP)]),
+    "dgm_embed_i8": (_I, [_P, _P, _P, _P, _P, _P, ctypes.POINTER(EmbP)]),
+    "dgm_embed_i4": (_I, [_P, _P, _P, _P, _P, _P, ctypes.POINTER(EmbP)]),
+    "dgm_embed": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_embed_bwd": (_I, [_P, _P, _P, _P, ctypes.POINTER(EmbBwdP)]),
+    "dgm_embedBwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_pos_bwd": (_I, [_P, _P, _P, ctypes.POINTER(PosP)]),
+    "dgm_posBwd": (_I, [_P, _P, _P, _I64, _I64, _I64]),
+    "dgm_bias_grad": (_I, [_P, _P, _P, ctypes.POINTER(BiasP)]),
+    "dgm_biasGrad": (_I, [_P, _P, _P, _I64, _I64]),
 }
 
 

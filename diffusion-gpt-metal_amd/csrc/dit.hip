@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     // and the table entries at its own index, as rope_fwd computes it.
     const int cpr = D >> 2;                        // float4 chunks per row
     const int hc = cpr >> 1, half = D >> 1;        // chunk pairs per row
-    const int nqp = 16 * hc, np = (16 + T) * hc;   // pairs: q rows first, then k rows
+    const int np = (16 + T) * hc;                  // pairs: 16 q rows first, then T k rows
     const int nv = T * cpr;                        // v chunks
     constexpr int PB = 2, VB = 3;                  // pairs / v chunks per thread per batch
     for (int bp = 0, bv = 0; bp < np || bv < nv; bp += PB * kThreads, bv += VB * kThreads) {

@@ -15,25 +15,14 @@
 // that are not a whole number of groups, take a one-thread-per-group kernel
 // with the same arithmetic.
 #include "common.hpp"
+#include "quant_math.hpp"
 
 namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ int quant_code(float w, float s, int lim) {
-    // rintf is round-half-to-even; the divide is IEEE correctly rounded
-    // (built with -fhip-fp32-correctly-rounded-divide-sqrt, no fast math).
-    float r = rintf(w / s);
-    int q = r > 2147483520.0f ? lim : (r < -2147483520.0f ? -lim : static_cast<int>(r));
-    q = q > lim ? lim : q;
-    q = q < -lim ? -lim : q;
-    return q;
-}
-
-__device__ __forceinline__ float group_scale(float maxAbs, float qmax) {
-    float d = maxAbs / qmax;
-    return 1e-8f >= d ? 1e-8f : d;
-}
+using dgm::group_scale;
+using dgm::quant_code;
 
 // L = G / 8 lanes per group, L in {1, 2, 4, ..., 64}.
 template <int BITS, int L>

@@ -1,8 +1,10 @@
 """Python mirror of the reference's GPU class (src/GPU.swift:91-272) over the C ABI.
 
 Same method names and argument meaning as the Swift wrappers (quantize,
-gemmNT, gemmDX, gemmDW, gemmDWAcc, begin, end, lastKernel) plus the
-kernel-level entries (quant_i8 ... gemm_dw_acc) in the buffer slot order of
+gemmNT, gemmDX, gemmDW, gemmDWAcc, the DiT block's wrappers, the training
+step's adam / reduceSumsq / scale / zero / embed / embedBwd / posBwd /
+biasGrad, begin, end, lastKernel) plus the kernel-level entries (quant_i8 ...
+gemm_dw_acc, adamw, embed_i4 ...) in the buffer slot order of
 metal/kernels.metal. Buffers are device tensors (torch is used only to hold
 device memory) or raw device addresses. A nonzero status raises DgmError,
 where the reference calls fatalError / exit(1).
@@ -12,8 +14,9 @@ from __future__ import annotations
 import ctypes
 from typing import Any, Optional
 
-from .abi import (DGM_MATH_BF16, DGM_MATH_FP32, DgmError, DiTCfg, DiTWeights,
-                  GemmP, QuantP, load_library)
+from .abi import (DGM_MATH_BF16, DGM_MATH_FP32, AdamP, BiasP, DgmError, DiTCfg,
+                  DiTWeights, EmbBwdP, EmbP, GemmP, PosP, QuantP, ReduceP, ScaleP,
+                  UnaryP, load_library)
 
 
 def _ptr(t: Any) -> Optional[int]:
@@ -152,6 +155,41 @@ class GPU:
         self._check(self.lib.dgm_dit_forward(self.h, ctypes.byref(cfg), ctypes.byref(w), _ptr(cos), _ptr(sin),
                                              _ptr(x), _ptr(ws), ws_floats))
 
+    # -- training step (src/GPU.swift:200-210, 274-277, 324-350, 420-429) -----
+    def adam(self, w, g, m, v, n: int, lr: float, b1: float, b2: float, eps: float, wd: float,
+             invBC1: float, invBC2: float) -> None:
+        self._check(self.lib.dgm_adam(self.h, _ptr(w), _ptr(g), _ptr(m), _ptr(v), n, lr, b1, b2, eps, wd,
+                                      invBC1, invBC2))
+
+    def adamQuantize(self, w, g, m, v, q, scale, rows: int, cols: int, bits: int, qGroup: int, lr: float,
+                     b1: float, b2: float, eps: float, wd: float, invBC1: float, invBC2: float) -> None:
+        """adam followed by quantize of the same master, in one pass where the
+        shape allows (dgm_adam_quantize); bit-identical to the two calls."""
+        self._check(self.lib.dgm_adam_quantize(self.h, _ptr(w), _ptr(g), _ptr(m), _ptr(v), _ptr(q), _ptr(scale),
+                                               rows, cols, bits, qGroup, lr, b1, b2, eps, wd, invBC1, invBC2))
+
+    def reduceSumsq(self, x, into, n: int, slot: int) -> None:
+        self._check(self.lib.dgm_reduceSumsq(self.h, _ptr(x), _ptr(into), n, slot))
+
+    def zero(self, b, n: int) -> None:
+        self._check(self.lib.dgm_zero(self.h, _ptr(b), n))
+
+    def scale(self, b, n: int, by: float) -> None:
+        self._check(self.lib.dgm_scale(self.h, _ptr(b), n, by))
+
+    def embed(self, bits: int, tokens, wte, q, scale, wpe, y, B: int, T: int, C: int, qGroup: int) -> None:
+        self._check(self.lib.dgm_embed(self.h, bits, _ptr(tokens), _ptr(wte), _ptr(q), _ptr(scale), _ptr(wpe),
+                                       _ptr(y), B, T, C, qGroup))
+
+    def embedBwd(self, tokens, dx, dwe, B: int, T: int, C: int, V: int) -> None:
+        self._check(self.lib.dgm_embedBwd(self.h, _ptr(tokens), _ptr(dx), _ptr(dwe), B, T, C, V))
+
+    def posBwd(self, dx, dwp, B: int, T: int, C: int) -> None:
+        self._check(self.lib.dgm_posBwd(self.h, _ptr(dx), _ptr(dwp), B, T, C))
+
+    def biasGrad(self, dy, db, M: int, N: int) -> None:
+        self._check(self.lib.dgm_biasGrad(self.h, _ptr(dy), _ptr(db), M, N))
+
     # -- kernel-level entries (metal/kernels.metal slot order) ----------------
     def quant_i8(self, W, Q, scale, p: QuantP) -> None:
         self._check(self.lib.dgm_quant_i8(self.h, _ptr(W), _ptr(Q), _ptr(scale), ctypes.byref(p)))
@@ -184,6 +222,38 @@ class GPU:
 
     def gemm_dw_acc(self, dY, X, dW, p: GemmP) -> None:
         self._check(self.lib.dgm_gemm_dw_acc(self.h, _ptr(dY), _ptr(X), _ptr(dW), ctypes.byref(p)))
+
+    def adamw(self, w, g, m, v, p: AdamP) -> None:
+        self._check(self.lib.dgm_adamw(self.h, _ptr(w), _ptr(g), _ptr(m), _ptr(v), ctypes.byref(p)))
+
+    def reduce_sumsq(self, x, out, p: ReduceP) -> None:
+        self._check(self.lib.dgm_reduce_sumsq(self.h, _ptr(x), _ptr(out), ctypes.byref(p)))
+
+    def zero_f(self, x, p: UnaryP) -> None:
+        self._check(self.lib.dgm_zero_f(self.h, _ptr(x), ctypes.byref(p)))
+
+    def scale_f(self, x, p: ScaleP) -> None:
+        self._check(self.lib.dgm_scale_f(self.h, _ptr(x), ctypes.byref(p)))
+
+    def embed_f32(self, tokens, wte, wpe, y, p: EmbP) -> None:
+        self._check(self.lib.dgm_embed_f32(self.h, _ptr(tokens), _ptr(wte), _ptr(wpe), _ptr(y), ctypes.byref(p)))
+
+    def embed_i8(self, tokens, wte, scale, wpe, y, p: EmbP) -> None:
+        self._check(self.lib.dgm_embed_i8(self.h, _ptr(tokens), _ptr(wte), _ptr(scale), _ptr(wpe), _ptr(y),
+                                          ctypes.byref(p)))
+
+    def embed_i4(self, tokens, wte, scale, wpe, y, p: EmbP) -> None:
+        self._check(self.lib.dgm_embed_i4(self.h, _ptr(tokens), _ptr(wte), _ptr(scale), _ptr(wpe), _ptr(y),
+                                          ctypes.byref(p)))
+
+    def embed_bwd(self, tokens, dx, dwe, p: EmbBwdP) -> None:
+        self._check(self.lib.dgm_embed_bwd(self.h, _ptr(tokens), _ptr(dx), _ptr(dwe), ctypes.byref(p)))
+
+    def pos_bwd(self, dx, dwp, p: PosP) -> None:
+        self._check(self.lib.dgm_pos_bwd(self.h, _ptr(dx), _ptr(dwp), ctypes.byref(p)))
+
+    def bias_grad(self, dY, db, p: BiasP) -> None:
+        self._check(self.lib.dgm_bias_grad(self.h, _ptr(dY), _ptr(db), ctypes.byref(p)))
 
 
 __all__ = ["GPU", "Buf", "RawBuf", "DGM_MATH_FP32", "DGM_MATH_BF16"]

@@ -233,6 +233,94 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w
                     const float* cos_t, const float* sin_t, float* x, float* ws,
                     int64_t ws_floats);
 
+/* ---- training step around the path: optimizer, re-quantize, embedding ----
+ * GPT.step (src/GPT.swift:183-220) zeroes the grads, runs the backward, sums
+ * the squared grads for clipping, scales them, applies AdamW to every master
+ * weight and re-quantizes the quantized ones; the quantized GPT's token
+ * embedding is the other consumer of the codes (src/GPT.swift:332-336,
+ * 371-376, 425-429). Parameter blocks are the reference's (src/Params.swift). */
+
+typedef struct dgm_AdamP {                     /* src/Params.swift:138-147      */
+    uint32_t n;
+    float lr, b1, b2, eps, wd, invBC1, invBC2;
+} dgm_AdamP;                                   /* 32 bytes (src/GPU.swift:469)  */
+typedef struct dgm_EmbP { uint32_t B, T, C, qGroup; } dgm_EmbP;       /* :78-83   */
+typedef struct dgm_EmbBwdP { uint32_t B, T, C, V; } dgm_EmbBwdP;      /* :85-90   */
+typedef struct dgm_PosP { uint32_t B, T, C, pad; } dgm_PosP;          /* :92-97   */
+typedef struct dgm_BiasP { uint32_t M, N, pad0, pad1; } dgm_BiasP;    /* :46-51   */
+typedef struct dgm_ReduceP { uint32_t n, slot, pad0, pad1; } dgm_ReduceP; /* :106-111 */
+typedef struct dgm_ScaleP { uint32_t n; float s; uint32_t pad0, pad1; } dgm_ScaleP; /* :39-44 */
+typedef struct dgm_UnaryP { uint32_t n, pad0, pad1, pad2; } dgm_UnaryP; /* :32-37  */
+
+/* adamw (metal/kernels.metal:786-802), per element i < n:
+ *   m = b1*m + (1-b1)*g;  v = b2*v + (1-b2)*g*g;
+ *   w -= lr * ((m*invBC1) / (sqrt(v*invBC2) + eps) + wd*w)
+ * each operation rounded to fp32 separately (no fused multiply-add). */
+int dgm_adamw(dgm_gpu* g, float* w, const float* grad, float* m, float* v, const dgm_AdamP* p);
+/* GPU.adam (src/GPU.swift:425-429). */
+int dgm_adam(dgm_gpu* g, float* w, const float* grad, float* m, float* v, int64_t n,
+             float lr, float b1, float b2, float eps, float wd, float invBC1, float invBC2);
+/* GPU.adam followed by GPU.quantize of the same master (the quantized
+ * parameters of src/GPT.swift:214-217 then quantizeAll, 441-447), in one pass
+ * over the [rows, cols] master when cols % qGroup == 0 and qGroup is a power
+ * of two in [8, 512]: w, m, v, q and scale come out bit-identical to the two
+ * calls (which run instead for any other shape). No single reference
+ * counterpart; it replaces that pair of dispatches. */
+int dgm_adam_quantize(dgm_gpu* g, float* w, const float* grad, float* m, float* v, void* q,
+                      float* scale, int64_t rows, int64_t cols, int64_t bits, int64_t qGroup,
+                      float lr, float b1, float b2, float eps, float wd, float invBC1,
+                      float invBC2);
+
+/* reduce_sumsq (metal/kernels.metal:749-768): out[slot] = sum of x[i]^2,
+ * i < n. The sum is taken in a fixed order of this library's own (per-block
+ * partial sums over contiguous ranges, then a tree), so repeated calls give
+ * identical bits; it agrees with the reference's 256-lane order to fp32
+ * rounding, not bitwise. */
+int dgm_reduce_sumsq(dgm_gpu* g, const float* x, float* out, const dgm_ReduceP* p);
+/* GPU.reduceSumsq (src/GPU.swift:420-422). */
+int dgm_reduceSumsq(dgm_gpu* g, const float* x, float* into, int64_t n, int64_t slot);
+/* zero_f / scale_f (metal/kernels.metal:770-784); GPU.zero / GPU.scale
+ * (src/GPU.swift:200-209). */
+int dgm_zero_f(dgm_gpu* g, float* x, const dgm_UnaryP* p);
+int dgm_scale_f(dgm_gpu* g, float* x, const dgm_ScaleP* p);
+int dgm_zero(dgm_gpu* g, float* x, int64_t n);
+int dgm_scale(dgm_gpu* g, float* x, int64_t n, float s);
+
+/* embed_f32 / embed_i8 / embed_i4 (metal/kernels.metal:616-663):
+ * y[bt, c] = wte[tok, c] + wpe[bt % T, c], with wte dequantized as
+ * code * scale[tok, c / qGroup] for the quantized forms (rounded, then
+ * added). tokens are uint32 ids < the table's rows (not checked). */
+int dgm_embed_f32(dgm_gpu* g, const uint32_t* tokens, const float* wte, const float* wpe,
+                  float* y, const dgm_EmbP* p);
+int dgm_embed_i8(dgm_gpu* g, const uint32_t* tokens, const int8_t* wte, const float* scale,
+                 const float* wpe, float* y, const dgm_EmbP* p);
+int dgm_embed_i4(dgm_gpu* g, const uint32_t* tokens, const uint8_t* wte, const float* scale,
+                 const float* wpe, float* y, const dgm_EmbP* p);
+/* GPU.embed (src/GPU.swift:324-338): bits selects the kernel; wte is read
+ * for bits 32, q and scale for bits 8 / 4. */
+int dgm_embed(dgm_gpu* g, int64_t bits, const uint32_t* tokens, const float* wte, const void* q,
+              const float* scale, const float* wpe, float* y, int64_t B, int64_t T, int64_t C,
+              int64_t qGroup);
+/* embed_bwd (metal/kernels.metal:665-682): dwe[v, c] += sum over bt with
+ * tokens[bt] == v of dx[bt, c], summed in increasing bt (the reference's
+ * order, so results are bitwise the reference's). Every row v < V is
+ * rewritten. */
+int dgm_embed_bwd(dgm_gpu* g, const uint32_t* tokens, const float* dx, float* dwe,
+                  const dgm_EmbBwdP* p);
+/* GPU.embedBwd (src/GPU.swift:340-344). */
+int dgm_embedBwd(dgm_gpu* g, const uint32_t* tokens, const float* dx, float* dwe, int64_t B,
+                 int64_t T, int64_t C, int64_t V);
+/* pos_bwd (metal/kernels.metal:684-697): dwp[t, c] = sum over b (increasing)
+ * of dx[b*T + t, c]; overwrites. */
+int dgm_pos_bwd(dgm_gpu* g, const float* dx, float* dwp, const dgm_PosP* p);
+/* GPU.posBwd (src/GPU.swift:346-350). */
+int dgm_posBwd(dgm_gpu* g, const float* dx, float* dwp, int64_t B, int64_t T, int64_t C);
+/* bias_grad (metal/kernels.metal:285-295): db[n] = sum over m (increasing) of
+ * dY[m, n]; overwrites. */
+int dgm_bias_grad(dgm_gpu* g, const float* dY, float* db, const dgm_BiasP* p);
+/* GPU.biasGrad (src/GPU.swift:274-277). */
+int dgm_biasGrad(dgm_gpu* g, const float* dy, float* db, int64_t M, int64_t N);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,15 @@
  *                      used by Check.swift:214-241); softmax rows sum to 1;
  *                      swiglu: silu(0) = 0 and float64 formula; block: float64
  *                      numpy restatement on a tiny config.
+ *   orc_adamw          hand-derived exact steps (b1 = 1/2, b2 = 3/4, eps = 0:
+ *                      the first update of a power-of-two gradient is exactly
+ *                      sign(g)), pure decoupled decay at g = 0, and torch.optim
+ *                      AdamW in float64 over several steps.
+ *   orc_reduce_sumsq   exact integer-valued sums and a float64 sum.
+ *   orc_embed*, orc_pos_bwd, orc_bias_grad
+ *                      one-hot token tables that select rows, integer-valued
+ *                      inputs whose sums are exact, and numpy scatter-add /
+ *                      column sums in float64.
  * Nothing here is parity-unpinned.
  */
 #include "oracle.h"
@@ -451,4 +460,93 @@ int orc_dit_forward(const orc_dit_cfg* c,
         memcpy(x, xn, sizeof(float) * (size_t)(M * C));
     }
     return 0;
+}
+
+/* ---- training step ------------------------------------------------------ */
+
+/* adamw, kernels.metal:786-802 (each operation rounded separately). */
+void orc_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1,
+               float b2, float eps, float wd, float invBC1, float invBC2) {
+    for (int64_t i = 0; i < n; ++i) {
+        float gi = g[i];
+        float mi = b1 * m[i] + (1.0f - b1) * gi;
+        float vi = b2 * v[i] + (1.0f - b2) * gi * gi;
+        m[i] = mi;
+        v[i] = vi;
+        float upd = (mi * invBC1) / (sqrtf(vi * invBC2) + eps);
+        w[i] -= lr * (upd + wd * w[i]);
+    }
+}
+
+/* reduce_sumsq, kernels.metal:749-768: 256 lane sums over i = lane (mod 256),
+ * then the halving tree 128, 64, ..., 1. */
+float orc_reduce_sumsq(const float* x, int64_t n) {
+    float sh[256];
+    for (int t = 0; t < 256; ++t) {
+        float v = 0.0f;
+        for (int64_t i = t; i < n; i += 256) {
+            float a = x[i];
+            v += a * a;
+        }
+        sh[t] = v;
+    }
+    for (int s = 128; s > 0; s >>= 1)
+        for (int t = 0; t < s; ++t) sh[t] += sh[t + s];
+    return sh[0];
+}
+
+/* scale_f, kernels.metal:778-784. */
+void orc_scale(float* x, int64_t n, float s) {
+    for (int64_t i = 0; i < n; ++i) x[i] *= s;
+}
+
+/* embed_f32 / embed_i8 / embed_i4, kernels.metal:616-663: the dequantized
+ * table entry code * scale is rounded, then wpe is added. bits 32 reads wte. */
+int orc_embed(const uint32_t* tokens, const float* wte, const void* q, const float* scale,
+              const float* wpe, float* y, int B, int T, int C, int group, int bits) {
+    if (bits != 32 && !shape_ok(1, C, group, bits)) return -1;
+    const int groups = bits == 32 ? 0 : C / group;
+    for (int bt = 0; bt < B * T; ++bt) {
+        const int t = bt % T;
+        const int64_t tok = tokens[bt];
+        for (int c = 0; c < C; ++c) {
+            float e;
+            if (bits == 32) e = wte[tok * C + c];
+            else e = (float)code_at(q, tok, c, C, bits) * scale[tok * groups + c / group];
+            y[(int64_t)bt * C + c] = e + wpe[(int64_t)t * C + c];
+        }
+    }
+    return 0;
+}
+
+/* embed_bwd, kernels.metal:665-682: for each (v, c) a sum from 0 over bt in
+ * increasing order, then added to dwe. */
+void orc_embed_bwd(const uint32_t* tokens, const float* dx, float* dwe, int B, int T, int C, int V) {
+    const int BT = B * T;
+    for (int v = 0; v < V; ++v)
+        for (int c = 0; c < C; ++c) {
+            float sum = 0.0f;
+            for (int bt = 0; bt < BT; ++bt)
+                if (tokens[bt] == (uint32_t)v) sum += dx[(int64_t)bt * C + c];
+            dwe[(int64_t)v * C + c] += sum;
+        }
+}
+
+/* pos_bwd, kernels.metal:684-697. */
+void orc_pos_bwd(const float* dx, float* dwp, int B, int T, int C) {
+    for (int t = 0; t < T; ++t)
+        for (int c = 0; c < C; ++c) {
+            float sum = 0.0f;
+            for (int b = 0; b < B; ++b) sum += dx[((int64_t)b * T + t) * C + c];
+            dwp[(int64_t)t * C + c] = sum;
+        }
+}
+
+/* bias_grad, kernels.metal:285-295. */
+void orc_bias_grad(const float* dy, float* db, int64_t M, int64_t N) {
+    for (int64_t n = 0; n < N; ++n) {
+        float acc = 0.0f;
+        for (int64_t m = 0; m < M; ++m) acc += dy[m * N + n];
+        db[n] = acc;
+    }
 }

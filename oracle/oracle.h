@@ -102,6 +102,17 @@ int orc_dit_forward(const orc_dit_cfg* c,
                     const float* n2b, const float* nf,
                     float* x_io, float* ws);
 
+/* ---- training step: kernels.metal:285-295, 616-697, 749-802 ------------- */
+void orc_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1,
+               float b2, float eps, float wd, float invBC1, float invBC2);
+float orc_reduce_sumsq(const float* x, int64_t n);
+void orc_scale(float* x, int64_t n, float s);
+int orc_embed(const uint32_t* tokens, const float* wte, const void* q, const float* scale,
+              const float* wpe, float* y, int B, int T, int C, int group, int bits);
+void orc_embed_bwd(const uint32_t* tokens, const float* dx, float* dwe, int B, int T, int C, int V);
+void orc_pos_bwd(const float* dx, float* dwp, int B, int T, int C);
+void orc_bias_grad(const float* dy, float* db, int64_t M, int64_t N);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,13 @@ def lib() -> ctypes.CDLL:
             "orc_mix": (None, [_P, _P, _P, _i64, ctypes.c_float, ctypes.c_float]),
             "orc_dit_workspace_floats": (_i64, [_P]),
             "orc_dit_forward": (_i, [_P] + [_P] * 14 + [_P] * 5 + [_P, _P]),
+            "orc_adamw": (None, [_P, _P, _P, _P, _i64] + [ctypes.c_float] * 7),
+            "orc_reduce_sumsq": (ctypes.c_float, [_P, _i64]),
+            "orc_scale": (None, [_P, _i64, ctypes.c_float]),
+            "orc_embed": (_i, [_P, _P, _P, _P, _P, _P, _i, _i, _i, _i, _i]),
+            "orc_embed_bwd": (None, [_P, _P, _P, _i, _i, _i, _i]),
+            "orc_pos_bwd": (None, [_P, _P, _i, _i, _i]),
+            "orc_bias_grad": (None, [_P, _P, _i64, _i64]),
         }
         for name, (res, args) in protos.items():
             fn = getattr(L, name)
@@ -292,3 +299,69 @@ def dit_forward(cfg: DiTCfg, qw: dict, x0: np.ndarray) -> np.ndarray:
     if rc != 0:
         raise ValueError("bad DiT config")
     return x
+
+
+# ---- training step: kernels.metal:285-295, 616-697, 749-802 -----------------
+
+def adamw(w, g, m, v, lr, b1, b2, eps, wd, invBC1, invBC2):
+    """adamw (kernels.metal:786-802). Returns the updated (w, m, v) copies."""
+    w, m, v = (np.array(a, dtype=np.float32, copy=True).reshape(-1) for a in (w, m, v))
+    g = _f32(g).reshape(-1)
+    lib().orc_adamw(_p(w), _p(g), _p(m), _p(v), w.size, lr, b1, b2, eps, wd, invBC1, invBC2)
+    return w, m, v
+
+
+def adam_quantize(w, g, m, v, rows, cols, group, bits, lr, b1, b2, eps, wd, invBC1, invBC2, init=None):
+    """adamw then cpuQuant of the updated master (GPT.swift:214-217, 441-447).
+    Returns (w, m, v, codes, scales)."""
+    w, m, v = adamw(w, g, m, v, lr, b1, b2, eps, wd, invBC1, invBC2)
+    q, s = quant(w, rows, cols, group, bits, init=init)
+    return w, m, v, q, s
+
+
+def reduce_sumsq(x) -> float:
+    """reduce_sumsq (kernels.metal:749-768) in its 256-lane order."""
+    x = _f32(x).reshape(-1)
+    return float(lib().orc_reduce_sumsq(_p(x), x.size))
+
+
+def scale(x, s):
+    x = np.array(x, dtype=np.float32, copy=True).reshape(-1)
+    lib().orc_scale(_p(x), x.size, s)
+    return x
+
+
+def embed(tokens, wte, q, scale_, wpe, B, T, C, group, bits):
+    """embed_f32 / embed_i8 / embed_i4 (kernels.metal:616-663)."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    wte = None if wte is None else _f32(wte)
+    q = None if q is None else np.ascontiguousarray(q)
+    scale_ = None if scale_ is None else _f32(scale_)
+    wpe = _f32(wpe)
+    y = np.zeros(B * T * C, dtype=np.float32)
+    if lib().orc_embed(_p(tokens), _p(wte), _p(q), _p(scale_), _p(wpe), _p(y), B, T, C, group, bits):
+        raise ValueError("bad embed shape")
+    return y
+
+
+def embed_bwd(tokens, dx, dwe, B, T, C, V):
+    """embed_bwd (kernels.metal:665-682): returns dwe + per-token sums."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    dx = _f32(dx)
+    out = np.array(dwe, dtype=np.float32, copy=True).reshape(-1)
+    lib().orc_embed_bwd(_p(tokens), _p(dx), _p(out), B, T, C, V)
+    return out
+
+
+def pos_bwd(dx, B, T, C):
+    dx = _f32(dx)
+    out = np.zeros(T * C, dtype=np.float32)
+    lib().orc_pos_bwd(_p(dx), _p(out), B, T, C)
+    return out
+
+
+def bias_grad(dy, M, N):
+    dy = _f32(dy)
+    out = np.zeros(N, dtype=np.float32)
+    lib().orc_bias_grad(_p(dy), _p(out), M, N)
+    return out
