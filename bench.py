@@ -254,6 +254,47 @@ def bench_quant(b: Bench, reps: int, bits: int) -> dict:
             "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
 
 
+def bench_adam_quant(b: Bench, reps: int, bits: int) -> dict:
+    """AdamW + re-quantization of the c4/c5 weight (W[14336,4096], G=128): the
+    fused pass against adam followed by quantize. Algorithmic bytes per
+    element: w, g, m, v read (16) + w, m, v written (12) + codes (0.5 or 1),
+    plus the scales."""
+    N, K, G = 14336, 4096, 128
+    n = N * K
+    w, g = b.randn(n, 0.02), b.randn(n, 1.0)
+    m, v = b.zeros(n), b.zeros(n)
+    q = b.zeros(n // (2 if bits == 4 else 1), b.torch.uint8)
+    s = b.zeros(N * (K // G))
+    hp = (1e-4, 0.9, 0.95, 1e-8, 0.1, 10.0, 20.0)
+    fused = b.time_launches(lambda i: b.gpu.adamQuantize(w, g, m, v, q, s, N, K, bits, G, *hp), reps)
+
+    def pair(i):
+        b.gpu.adam(w, g, m, v, n, *hp)
+        b.gpu.quantize(w, q, s, N, K, bits, G)
+
+    unfused = b.time_launches(pair, reps)
+    code_b = n // (2 if bits == 4 else 1)
+    nbytes = 28 * n + code_b + 4 * N * (K // G)
+    return {"kernel": "adam_quantize", "shape": f"W[14336,4096] int{bits} G=128", "us": round(fused * 1e3, 3),
+            "GBps": round(nbytes / fused / 1e6, 2), "unfused_us": round(unfused * 1e3, 3),
+            "roofline": roofline(nbytes / fused / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
+
+
+def bench_embed_bwd(b: Bench, reps: int) -> dict:
+    """embed_bwd at the quantized GPT's default shape (src/GPT.swift:374-376;
+    16 x 64 tokens, C 128, a 65-symbol vocabulary) with Zipf-like token counts."""
+    t = b.torch
+    B, T, C, V = 16, 64, 128, 65
+    ranks = t.arange(1, V + 1, dtype=t.float64)
+    probs = (1.0 / ranks) / (1.0 / ranks).sum()
+    toks = t.multinomial(probs, B * T, replacement=True, generator=b.gen).to(t.int32).to("cuda")
+    dx, dwe = b.randn(B * T * C, 1.0), b.zeros(V * C)
+    ms = b.time_launches(lambda i: b.gpu.embedBwd(toks, dx, dwe, B, T, C, V), reps)
+    nbytes = 4 * (B * T * C + 2 * V * C + B * T)
+    return {"kernel": "embed_bwd", "shape": "B=16 T=64 C=128 V=65", "us": round(ms * 1e3, 3),
+            "GBps": round(nbytes / ms / 1e6, 2), "note": "latency-bound: 1 MB of traffic"}
+
+
 def bench_c4(b: Bench, reps: int, M: int, math_mode: int) -> dict:
     """Decode-shaped int4: K=4096, N=14336, G=128. Weight copies are rotated so
     that successive launches never find W in the 256 MB Infinity Cache."""
@@ -535,6 +576,9 @@ def main() -> int:
             ("c3_dit_fwd", lambda: bench_c3(b, 50)),
             ("quant_i4_14336x4096", lambda: bench_quant(b, 20, 4)),
             ("quant_i8_14336x4096", lambda: bench_quant(b, 20, 8)),
+            ("adam_quant_i4_14336x4096", lambda: bench_adam_quant(b, 10, 4)),
+            ("adam_quant_i8_14336x4096", lambda: bench_adam_quant(b, 10, 8)),
+            ("embed_bwd_gpt", lambda: bench_embed_bwd(b, 50)),
             ("c4_int4_m1_fp32", lambda: bench_c4(b, 72, 1, dgm.DGM_MATH_FP32)),
             ("c4_int4_m16_fp32", lambda: bench_c4(b, 72, 16, dgm.DGM_MATH_FP32)),
             ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, dgm.DGM_MATH_BF16)),

@@ -13,6 +13,7 @@ from .abi import (DGM_ERR_ARG, DGM_ERR_BITS, DGM_ERR_HIP, DGM_ERR_NOT_BEGUN,
                   ReduceP, ScaleP, UnaryP, load_library)
 from .gpu import GPU, Buf, RawBuf
 from .dit import DiTBlock, DiTConfig, rope_tables
+from .train import Param, bias_corrections, grad_norm, optimizer_step, zero_grads
 
 __all__ = [
     "GPU", "Buf", "RawBuf", "GemmP", "QuantP", "DgmError", "load_library",
@@ -20,5 +21,6 @@ __all__ = [
     "DGM_ERR_NOT_BEGUN", "DGM_ERR_HIP", "DGM_ERR_BITS", "DGM_ERR_UNSUPPORTED",
     "DGM_MATH_FP32", "DGM_MATH_BF16", "DiTBlock", "DiTConfig", "DiTCfg", "DiTLinear",
     "DiTWeights", "DIT_LINEARS", "DIT_NORMS", "rope_tables", "AdamP", "EmbP", "EmbBwdP",
-    "PosP", "BiasP", "ReduceP", "ScaleP", "UnaryP",
+    "PosP", "BiasP", "ReduceP", "ScaleP", "UnaryP", "Param", "bias_corrections", "grad_norm",
+    "optimizer_step", "zero_grads",
 ]

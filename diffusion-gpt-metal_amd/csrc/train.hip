@@ -23,11 +23,11 @@
 //   adamw + quant_i4 moves 32.5 B per element, the fused pass 28.5 B.
 // * embed_bwd: the reference gives each (v, c) a thread that scans all B*T
 //   tokens (V*B*T*C loads). Here one wave owns one vocabulary row and a strip
-//   of 256 columns: it ballots 64 tokens at a time, and for the matching
-//   positions (in increasing order, 8 rows per batch with all loads issued
-//   first) adds the dx rows into per-lane sums. dx is read once in total and
-//   each sum keeps the reference's order, so results are bitwise the
-//   reference's.
+//   of columns: it ballots 64 tokens at a time (1024 loaded at once) into an
+//   ordered LDS list of the matching positions, then adds those dx rows into
+//   per-lane sums, 16 or 32 rows per batch with all loads issued first. dx is
+//   read once in total and each sum keeps the reference's order, so results
+//   are bitwise the reference's.
 #include "common.hpp"
 #include "quant_math.hpp"
 
@@ -251,61 +251,79 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t* __restr
 }
 
 // ---- embedding backward ------------------------------------------------------
-constexpr int kEbCols = 4;     // columns per lane: a wave covers 256 columns
-constexpr int kEbBatch = 8;    // matching rows whose loads are issued together
+// One wave per vocabulary row v and strip of 64*COLS columns. Per round the
+// wave loads 16 tokens per lane (1024 positions) and, 64 at a time, ballots
+// them and writes the matching positions, in increasing order, into its own
+// LDS list (each matching lane at its rank among the matches below it). It
+// then walks the list BATCH positions at a time: lane b holds position b of
+// the batch, every row's address comes from readlane, all BATCH x COLS loads
+// are issued, and the rows are added into the lane sums in list order. Rows
+// past the end of the list are loaded from a valid position and added as
+// +0.0f, which leaves a sum unchanged (a sum starts at +0.0f and so is never
+// -0.0f).
+constexpr int kEbTok = 16;                 // tokens per lane per round
+constexpr int kEbList = 64 * kEbTok;       // list entries per wave
 
+template <int COLS, int BATCH>
 __global__ __launch_bounds__(kThreads) void embed_bwd_kernel(const uint32_t* __restrict__ tokens,
                                                              const float* __restrict__ dx,
                                                              float* __restrict__ dwe, int BT,
                                                              int C, int V) {
+    static_assert(BATCH <= 64, "one list position per lane");
+    __shared__ int list[kThreads / 64][kEbList];
     const int lane = threadIdx.x & 63;
-    const int v = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    if (v >= V) return;   // whole wave
-    const int c0 = blockIdx.y * (64 * kEbCols) + lane;
-    float sum[kEbCols];
+    const int wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * (kThreads / 64) + wave;
+    if (v >= V) return;   // whole wave; no workgroup barrier below
+    int* L = list[wave];
+    const int c0 = blockIdx.y * (64 * COLS) + lane;
+    float sum[COLS];
 #pragma unroll
-    for (int j = 0; j < kEbCols; ++j) sum[j] = 0.0f;
-    int pend[kEbBatch];   // pending matching positions (wave-uniform values)
-    int np = 0;
-    auto flush = [&](int count) {
-        float r[kEbBatch][kEbCols];
+    for (int j = 0; j < COLS; ++j) sum[j] = 0.0f;
+    for (int base = 0; base < BT; base += kEbList) {
+        uint32_t tok[kEbTok];
 #pragma unroll
-        for (int b = 0; b < kEbBatch; ++b) {
-            if (b >= count) continue;
+        for (int u = 0; u < kEbTok; ++u) {
+            const int bt = base + 64 * u + lane;
+            tok[u] = bt < BT ? tokens[bt] : 0xFFFFFFFFu;
+        }
+        int np = 0;
 #pragma unroll
-            for (int j = 0; j < kEbCols; ++j) {
-                const int c = c0 + 64 * j;
-                r[b][j] = c < C ? dx[int64_t(pend[b]) * C + c] : 0.0f;
+        for (int u = 0; u < kEbTok; ++u) {
+            const bool hit = tok[u] == uint32_t(v);
+            const uint64_t mask = __ballot(hit);
+            const int rank = __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0));
+            if (hit) L[np + rank] = base + 64 * u + lane;
+            np += __popcll(mask);
+        }
+        // The list was written by other lanes of this wave; LDS accesses of one
+        // wave complete in issue order, the fence keeps the compiler's order.
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        for (int i = 0; i < np; i += BATCH) {
+            const int cnt = np - i < BATCH ? np - i : BATCH;
+            const int mine = L[i + (lane < cnt ? lane : 0)];
+            float r[BATCH][COLS];
+#pragma unroll
+            for (int b = 0; b < BATCH; ++b) {
+                const int64_t row = __builtin_amdgcn_readlane(mine, b);
+#pragma unroll
+                for (int j = 0; j < COLS; ++j) {
+                    const int c = c0 + 64 * j;
+                    r[b][j] = c < C ? dx[row * C + c] : 0.0f;
+                }
             }
-        }
 #pragma unroll
-        for (int b = 0; b < kEbBatch; ++b) {
-            if (b >= count) continue;
+            for (int b = 0; b < BATCH; ++b)
 #pragma unroll
-            for (int j = 0; j < kEbCols; ++j) sum[j] += r[b][j];
+                for (int j = 0; j < COLS; ++j) sum[j] += b < cnt ? r[b][j] : 0.0f;
         }
-    };
-    for (int base = 0; base < BT; base += 64) {
-        const int bt = base + lane;
-        const uint32_t tok = bt < BT ? tokens[bt] : 0xFFFFFFFFu;
-        uint64_t mask = __ballot(tok == uint32_t(v));
-        while (mask) {
-            const int j = __builtin_ctzll(mask);
-            mask &= mask - 1;
-            // Static register indexing: the unrolled compare-and-set keeps
-            // pend[] out of scratch memory.
-#pragma unroll
-            for (int b = 0; b < kEbBatch; ++b)
-                if (b == np) pend[b] = base + j;
-            if (++np == kEbBatch) {
-                flush(kEbBatch);
-                np = 0;
-            }
-        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
     }
-    if (np) flush(np);
 #pragma unroll
-    for (int j = 0; j < kEbCols; ++j) {
+    for (int j = 0; j < COLS; ++j) {
         const int c = c0 + 64 * j;
         if (c < C) {
             float* dst = dwe + int64_t(v) * C + c;
@@ -564,9 +582,15 @@ int dgm_embed_bwd(dgm_gpu* g, const uint32_t* tokens, const float* dx, float* dw
     if (BT * C > dgm::kMaxIndex || V * C > dgm::kMaxIndex)
         return dgm::fail(g, DGM_ERR_UNSUPPORTED, "embed_bwd: sizes beyond 2^31");
     if (!dwe || (BT > 0 && (!tokens || !dx))) return dgm::fail(g, DGM_ERR_ARG, "embed_bwd: null buffer");
-    const dim3 grid(dgm::ceil_div(V, kThreads / 64), dgm::ceil_div(C, 64 * kEbCols));
-    hipLaunchKernelGGL(embed_bwd_kernel, grid, dim3(kThreads), 0, g->stream, tokens, dx, dwe, int(BT),
-                       int(C), int(V));
+    if (C <= 128) {
+        const dim3 grid(dgm::ceil_div(V, kThreads / 64), 1);
+        hipLaunchKernelGGL((embed_bwd_kernel<2, 32>), grid, dim3(kThreads), 0, g->stream, tokens, dx, dwe,
+                           int(BT), int(C), int(V));
+    } else {
+        const dim3 grid(dgm::ceil_div(V, kThreads / 64), dgm::ceil_div(C, 256));
+        hipLaunchKernelGGL((embed_bwd_kernel<4, 16>), grid, dim3(kThreads), 0, g->stream, tokens, dx, dwe,
+                           int(BT), int(C), int(V));
+    }
     DGM_LAUNCH_CHECK(g, "embed_bwd");
     return DGM_OK;
 }

@@ -318,3 +318,65 @@ def test_bias_grad_bitexact(gpu, dgm, orc, M, N):
     gpu.bias_grad(to_dev(dy), out2, dgm.BiasP(M, N, 0, 0))
     gpu.end()
     assert _same(from_dev(out2), orc.bias_grad(dy, M, N))
+
+
+def _gpt_like_params(dgm, bits):
+    """A few parameters shaped like the quantized GPT's (src/GPT.swift:118-160):
+    quantized token table and linears, unquantized norms and biases."""
+    G = 8
+    spec = [("wte", 65, 128, True, True), ("wpe", 64, 128, False, True), ("ln1.g", 128, 1, False, False),
+            ("wq", 128, 128, True, True), ("bq", 128, 1, False, False), ("fc", 512, 128, True, True),
+            ("proj", 128, 512, True, True)]
+    return [dgm.Param(n, r, c, q and bits != 32, d, bits, G) for n, r, c, q, d in spec]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_optimizer_step_matches_reference_order(gpu, dgm, orc, bits):
+    """GPT.step's update (src/GPT.swift:193-218): fused adam+quantize equals
+    the literal adam-then-quantizeAll order bit for bit, and each parameter
+    equals the oracle's clip-scale + adamw + quantize given the step's norm."""
+    import torch
+    runs = []
+    for fused in (True, False):
+        params = _gpt_like_params(dgm, bits)
+        gen = torch.Generator(device="cpu").manual_seed(5)
+        for p in params:
+            p.w.copy_((0.02 * torch.randn(p.count, generator=gen)).to("cuda"))
+            p.g.copy_((0.5 * torch.randn(p.count, generator=gen)).to("cuda"))
+        init = [(from_dev(p.w.clone()), from_dev(p.g.clone())) for p in params]
+        norms = [dgm.optimizer_step(gpu, params, 3e-3, 0.1, 1.0, 1, fused=fused)]
+        # a second step from the updated state, without clipping
+        norms.append(dgm.optimizer_step(gpu, params, 3e-3, 0.1, 0.0, 2, fused=fused))
+        runs.append((params, norms, init))
+    (pa, na, init), (pb, nb, _) = runs
+    assert na == nb
+    for a, b in zip(pa, pb):
+        for f in ("w", "m", "v", "q", "scale"):
+            ta, tb = getattr(a, f), getattr(b, f)
+            if ta is not None:
+                assert torch.equal(ta.view(torch.uint8), tb.view(torch.uint8)), (a.name, f)
+    # Oracle check of the first step, with the norm the GPU step measured.
+    norm0 = na[0]
+    assert abs(norm0 - math_sqrt_sum(init)) <= 1e-5 * norm0
+    params = _gpt_like_params(dgm, bits)
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    for p in params:
+        p.w.copy_((0.02 * torch.randn(p.count, generator=gen)).to("cuda"))
+        p.g.copy_((0.5 * torch.randn(p.count, generator=gen)).to("cuda"))
+    dgm.optimizer_step(gpu, params, 3e-3, 0.1, 1.0, 1)
+    s = float(np.float32(1.0) / (np.float32(norm0) + np.float32(1e-6)))
+    bc1, bc2 = dgm.bias_corrections(0.9, 0.95, 1)
+    for p, (w0, g0) in zip(params, init):
+        gs = orc.scale(g0, s)
+        z = np.zeros_like(w0)
+        rw, rm, rv = orc.adamw(w0, gs, z, z, 3e-3, 0.9, 0.95, 1e-8, 0.1 if p.decay else 0.0, bc1, bc2)
+        assert _same(from_dev(p.w), rw) and _same(from_dev(p.m), rm), p.name
+        if p.quantized:
+            rq, rs = orc.quant(rw, p.rows, p.cols, 8, bits)
+            qh = from_dev(p.q)
+            assert np.array_equal(qh.view(np.int8) if bits == 8 else qh, rq), p.name
+            assert _same(from_dev(p.scale), rs), p.name
+
+
+def math_sqrt_sum(init):
+    return float(np.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for _, g in init)))
