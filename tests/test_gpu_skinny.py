@@ -174,21 +174,42 @@ def test_bf16_large_m(gpu, dgm, orc, bits, M, N, K, G):
     ref = _ref(orc, q, s, x, bias, M, N, K, G, bits)
     y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16)
     assert rel_err(y, ref) <= 1e-2
+    if K % 128 == 0:
+        # The bf16 kernel's own arithmetic: float64 products of bf16(X) and
+        # bf16(dequant(W)), fp32 accumulation (max relative error 1e-5).
+        assert rel_err(y, _ref_bf16(orc, q, s, x, bias, M, N, K, G, bits)) <= 1e-5
 
 
-def test_config5_prefill_bf16(gpu, dgm, orc):
-    """c5: X[8192,4096] ~ N(0,1), W[14336,4096] ~ N(0,0.02) int4 G=128, bf16
-    path. The float64 reference is checked on a sample of 96 rows (full-size
-    outputs are compared through the same dequantized weights)."""
+def _bf16_round(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def _ref_bf16(orc, q, s, x, bias, M, N, K, G, bits, rows=None):
+    wd = orc.dequant(from_dev(q), from_dev(s), N, K, G, bits).reshape(N, K)
+    xm = np.asarray(x, np.float32).reshape(M, K)
+    if rows is not None:
+        xm = xm[rows]
+    y = _bf16_round(xm) @ _bf16_round(wd).T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return y.ravel()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_config5_prefill_bf16(gpu, dgm, orc, bits):
+    """c5: X[8192,4096] ~ N(0,1), W[14336,4096] ~ N(0,0.02) int4 / int8 G=128,
+    bf16 path. The float64 references are checked on a sample of 96 rows."""
     import torch
     M, N, K, G = 8192, 14336, 4096, 128
     gen = torch.Generator(device="cpu").manual_seed(1005)
     x = torch.randn(M * K, generator=gen)
     w = torch.randn(N * K, generator=gen) * 0.02
-    q, s = _quantize(gpu, w.to("cuda"), N, K, G, 4)
-    y = _forward(gpu, dgm, 4, q, s, x.numpy(), None, M, N, K, G, dgm.DGM_MATH_BF16).reshape(M, N)
-    wd = orc.dequant(from_dev(q), from_dev(s), N, K, G, 4).reshape(N, K).astype(np.float64)
+    q, s = _quantize(gpu, w.to("cuda"), N, K, G, bits)
+    y = _forward(gpu, dgm, bits, q, s, x.numpy(), None, M, N, K, G, dgm.DGM_MATH_BF16).reshape(M, N)
+    wd = orc.dequant(from_dev(q), from_dev(s), N, K, G, bits).reshape(N, K).astype(np.float64)
     rows = np.random.default_rng(0).choice(M, 96, replace=False)
     ref = x.numpy().reshape(M, K)[rows].astype(np.float64) @ wd.T
     assert rel_err(y[rows], ref) <= 1e-2
+    assert rel_err(y[rows].ravel(), _ref_bf16(orc, q, s, x.numpy(), None, M, N, K, G, bits, rows)) <= 1e-5
     assert np.all(np.isfinite(y))
