@@ -10,7 +10,7 @@ from .abi import (DGM_ERR_ARG, DGM_ERR_BITS, DGM_ERR_HIP, DGM_ERR_NOT_BEGUN,
                   DGM_MATH_FP32, DGM_OK, HEADER, LIB_PATH, PROTOTYPES,
                   DIT_LINEARS, DIT_NORMS, DgmError, DiTCfg, DiTLinear,
                   DiTWeights, GemmP, QuantP, AdamP, EmbP, EmbBwdP, PosP, BiasP,
-                  ReduceP, ScaleP, UnaryP, load_library)
+                  ReduceP, ScaleP, UnaryP, DiTGrads, load_library)
 from .gpu import GPU, Buf, RawBuf
 from .dit import DiTBlock, DiTConfig, rope_tables
 from .train import Param, bias_corrections, grad_norm, optimizer_step, zero_grads
@@ -22,5 +22,5 @@ __all__ = [
     "DGM_MATH_FP32", "DGM_MATH_BF16", "DiTBlock", "DiTConfig", "DiTCfg", "DiTLinear",
     "DiTWeights", "DIT_LINEARS", "DIT_NORMS", "rope_tables", "AdamP", "EmbP", "EmbBwdP",
     "PosP", "BiasP", "ReduceP", "ScaleP", "UnaryP", "Param", "bias_corrections", "grad_norm",
-    "optimizer_step", "zero_grads",
+    "optimizer_step", "zero_grads", "DiTGrads",
 ]

@@ -59,6 +59,12 @@ class DiTWeights(ctypes.Structure):
     _fields_ = [(n, DiTLinear) for n in DIT_LINEARS] + [(n, ctypes.c_void_p) for n in DIT_NORMS]
 
 
+class DiTGrads(ctypes.Structure):
+    """dgm_dit_grads: fp32 gradients (+=) of the seven linears and five norms."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")] + \
+               [(n, ctypes.c_void_p) for n in ("n1", "n1b", "n2", "n2b", "nf")]
+
+
 def _u32s(*names):
     return [(n, ctypes.c_uint32) for n in names]
 
@@ -152,6 +158,18 @@ PROTOTYPES = {
     "dgm_ropeTables": (_I, [_I64, _I64, _F, _P, _P]),
     "dgm_dit_workspace_floats": (_I64, [ctypes.POINTER(DiTCfg)]),
     "dgm_dit_forward": (_I, [_P, ctypes.POINTER(DiTCfg), ctypes.POINTER(DiTWeights), _P, _P, _P, _P, _I64]),
+    "dgm_rmsBwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F]),
+    "dgm_attnBwd": (_I, [_P] * 11 + [_I64] * 4),
+    "dgm_ropeBwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_swigluBwd": (_I, [_P, _P, _P, _P, _P, _P, _I64]),
+    "dgm_sumHeads": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_acc": (_I, [_P, _P, _P, _I64]),
+    "dgm_accScale": (_I, [_P, _P, _P, _I64, _F]),
+    "dgm_dit_acts_floats": (_I64, [ctypes.POINTER(DiTCfg)]),
+    "dgm_dit_backward_ws_floats": (_I64, [ctypes.POINTER(DiTCfg)]),
+    "dgm_dit_forward_train": (_I, [_P, ctypes.POINTER(DiTCfg), ctypes.POINTER(DiTWeights), _P, _P, _P, _P, _I64]),
+    "dgm_dit_backward": (_I, [_P, ctypes.POINTER(DiTCfg), ctypes.POINTER(DiTWeights), ctypes.POINTER(DiTGrads),
+                              _P, _P, _P, _I64, _P, _P, _I64]),
     "dgm_adamw": (_I, [_P, _P, _P, _P, _P, ctypes.POINTER(AdamP)]),
     "dgm_adam": (_I, [_P, _P, _P, _P, _P, _I64] + [_F] * 7),
     "dgm_adam_quantize": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64] + [_F] * 7),

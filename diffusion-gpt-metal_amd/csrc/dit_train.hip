@@ -1,0 +1,608 @@
+// Training step of the looped DiT block (src/DiT.swift:505-626) on gfx950:
+// the backward kernels of the block's non-GEMM pieces, their GPU.swift-style
+// C entry points, a forward that saves every loop's activations, and the
+// block backward that accumulates the weight and norm gradients.
+//
+// Kernels (semantics of metal/kernels.metal, cited per kernel; fp contraction
+// off, each product and sum rounded as in the reference's separate
+// operations):
+//  * rms_bwd_dx: one wave per row; the row's sum(dy*w*x) is a wave reduction
+//    (fp32, a different order than the reference's sequential loop).
+//  * rms_bwd_dw: one workgroup of 16 waves per 64 columns; wave w sums rows
+//    w, w+16, ... and the 16 partial sums are added in wave order, then added
+//    into dweight (the weight is shared by every loop).
+//  * attention backward: the reference's five passes (dV, dP, softmax
+//    backward, dQ, dK) with the reference's summation order, one lane per
+//    output; bitwise the oracle's.
+//  * rope_bwd, swiglu_bwd, sum_heads, acc_f, acc_scale_f: elementwise.
+// The block's GEMMs are the library's: dgm_gemmNT / dgm_gemmDX /
+// dgm_gemmDWAcc on the fp32 masters (bits 32, as the reference's DiT) or on
+// the group-quantized codes (bits 8 / 4: forward on the codes, dX through the
+// dequantized codes, dW into the fp32 master gradient: the straight-through
+// estimator of src/GPT.swift's backward).
+#include <cmath>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float silu_sigmoid(float z) {
+    // metal/kernels.metal:911-918 (sign-split logistic)
+    if (z >= 0.0f) {
+        const float e = expf(-z);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(z);
+    return e / (1.0f + e);
+}
+
+// ---- rmsnorm_bwd_dx (metal/kernels.metal:827-850) ------------------------------
+__global__ __launch_bounds__(kThreads) void rms_bwd_dx_kernel(const float* __restrict__ x,
+                                                              const float* __restrict__ rstd,
+                                                              const float* __restrict__ w,
+                                                              const float* __restrict__ dy,
+                                                              float* __restrict__ dx, int rows, int cols) {
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + size_t(row) * cols;
+    const float* gr = dy + size_t(row) * cols;
+    float part = 0.0f;
+    for (int c = lane; c < cols; c += 64) {
+        const float dyhat = gr[c] * w[c];
+        part += dyhat * xr[c];
+    }
+    const float meanDyX = wave_sum(part) / float(cols);
+    const float rs = rstd[row];
+    const float rs3 = rs * rs * rs;
+    float* o = dx + size_t(row) * cols;
+    for (int c = lane; c < cols; c += 64) {
+        const float dyhat = gr[c] * w[c];
+        o[c] = rs * dyhat - xr[c] * rs3 * meanDyX;
+    }
+}
+
+// ---- rmsnorm_bwd_dw (metal/kernels.metal:852-868): dweight += sum over rows ----
+constexpr int kDwWaves = 16;
+__global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_dw_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ rstd,
+                                                                   const float* __restrict__ dy,
+                                                                   float* __restrict__ dweight, int rows,
+                                                                   int cols) {
+    __shared__ float part[kDwWaves][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
+    float acc = 0.0f;
+    if (c < cols) {
+        int r = wave;
+        for (; r + 7 * kDwWaves < rows; r += 8 * kDwWaves) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int rr = r + u * kDwWaves;
+                v[u] = dy[size_t(rr) * cols + c] * x[size_t(rr) * cols + c] * rstd[rr];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; r < rows; r += kDwWaves) acc += dy[size_t(r) * cols + c] * x[size_t(r) * cols + c] * rstd[r];
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDwWaves; ++w) tot += part[w][lane];
+        dweight[c] += tot;
+    }
+}
+
+// ---- attention backward (metal/kernels.metal:508-612) -----------------------------
+// q, k, v, dout, dq, dk, dv: [B, T, H, D]; probs, dprobs, dscores: [B, H, T, T].
+struct AttnBwdArgs {
+    const float *q, *k, *v, *probs, *dout;
+    float *dq, *dk, *dv, *dprobs, *dscores;
+    int B, T, H, D;
+    float scale;
+};
+
+__global__ __launch_bounds__(kThreads) void attn_bwd_dv_kernel(AttnBwdArgs a) {
+    const int64_t idx = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t total = int64_t(a.B) * a.T * a.H * a.D;
+    if (idx >= total) return;
+    const int d = int(idx % a.D);
+    const int h = int((idx / a.D) % a.H);
+    const int s = int((idx / (int64_t(a.D) * a.H)) % a.T);
+    const int b = int(idx / (int64_t(a.D) * a.H * a.T));
+    const float* pr = a.probs + (int64_t(b) * a.H + h) * a.T * a.T + s;
+    const float* g = a.dout + (int64_t(b) * a.T * a.H + h) * a.D + d;
+    float acc = 0.0f;
+    for (int t = 0; t < a.T; ++t) acc += pr[int64_t(t) * a.T] * g[int64_t(t) * a.H * a.D];
+    a.dv[idx] = acc;
+}
+
+__global__ __launch_bounds__(kThreads) void attn_bwd_dp_kernel(AttnBwdArgs a) {
+    const int64_t idx = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t TT = int64_t(a.T) * a.T;
+    if (idx >= int64_t(a.B) * a.H * TT) return;
+    const int s = int(idx % a.T);
+    const int t = int((idx / a.T) % a.T);
+    const int h = int((idx / TT) % a.H);
+    const int b = int(idx / (TT * a.H));
+    const float* g = a.dout + ((int64_t(b) * a.T + t) * a.H + h) * a.D;
+    const float* vv = a.v + ((int64_t(b) * a.T + s) * a.H + h) * a.D;
+    float acc = 0.0f;
+    for (int d = 0; d < a.D; ++d) acc += g[d] * vv[d];
+    a.dprobs[idx] = acc;
+}
+
+__global__ __launch_bounds__(kThreads) void attn_softmax_bwd_kernel(AttnBwdArgs a) {
+    const int64_t row = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (row >= int64_t(a.B) * a.H * a.T) return;
+    const float* pr = a.probs + row * a.T;
+    const float* g = a.dprobs + row * a.T;
+    float* o = a.dscores + row * a.T;
+    float dot = 0.0f;
+    for (int i = 0; i < a.T; ++i) dot += g[i] * pr[i];
+    for (int i = 0; i < a.T; ++i) o[i] = pr[i] * (g[i] - dot);
+}
+
+template <bool DQ>
+__global__ __launch_bounds__(kThreads) void attn_bwd_dqk_kernel(AttnBwdArgs a) {
+    // DQ: dq[b,t,h,d] = scale * sum_s ds[b,h,t,s] k[b,s,h,d]
+    // else dk[b,s,h,d] = scale * sum_t ds[b,h,t,s] q[b,t,h,d]
+    const int64_t idx = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t total = int64_t(a.B) * a.T * a.H * a.D;
+    if (idx >= total) return;
+    const int d = int(idx % a.D);
+    const int h = int((idx / a.D) % a.H);
+    const int r = int((idx / (int64_t(a.D) * a.H)) % a.T);
+    const int b = int(idx / (int64_t(a.D) * a.H * a.T));
+    const float* ds = a.dscores + (int64_t(b) * a.H + h) * a.T * a.T;
+    const float* src = (DQ ? a.k : a.q) + (int64_t(b) * a.T * a.H + h) * a.D + d;
+    float acc = 0.0f;
+    for (int u = 0; u < a.T; ++u) {
+        const float gval = DQ ? ds[int64_t(r) * a.T + u] : ds[int64_t(u) * a.T + r];
+        acc += gval * src[int64_t(u) * a.H * a.D];
+    }
+    (DQ ? a.dq : a.dk)[idx] = acc * a.scale;
+}
+
+// ---- rope_bwd (metal/kernels.metal:891-909) --------------------------------------
+__global__ __launch_bounds__(kThreads) void rope_bwd_kernel(const float* __restrict__ dy, float* __restrict__ dx,
+                                                            const float* __restrict__ cosv,
+                                                            const float* __restrict__ sinv, int B, int T, int H,
+                                                            int D) {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= int64_t(B) * T * H * D) return;
+    const int d = int(i % D);
+    const int mid = D >> 1;
+    const int t = int((i / (int64_t(H) * D)) % T);
+    const float c = cosv[t * D + d], s = sinv[t * D + d];
+    if (d < mid) dx[i] = dy[i] * c + dy[i + mid] * s;
+    else dx[i] = dy[i] * c - dy[i - mid] * s;
+}
+
+// ---- swiglu_bwd (metal/kernels.metal:932-949) ------------------------------------
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* __restrict__ gate,
+                                                              const float* __restrict__ up,
+                                                              const float* __restrict__ dy,
+                                                              float* __restrict__ dgate, float* __restrict__ dup,
+                                                              int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float z = gate[i];
+    const float s = silu_sigmoid(z);
+    const float silu = z * s;
+    const float siluP = s * (1.0f + z * (1.0f - s));
+    const float g = dy[i];
+    dgate[i] = siluP * up[i] * g;
+    dup[i] = silu * g;
+}
+
+// ---- sum_heads (metal/kernels.metal:995-1010) --------------------------------------
+__global__ __launch_bounds__(kThreads) void sum_heads_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                             int B, int T, int H, int D) {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= int64_t(B) * T * D) return;
+    const int d = int(i % D);
+    const int64_t bt = i / D;
+    const float* p = src + bt * H * D + d;
+    float acc = 0.0f;
+    for (int h = 0; h < H; ++h) acc += p[int64_t(h) * D];
+    dst[i] = acc;
+}
+
+// ---- acc_f / acc_scale_f (metal/kernels.metal:429-436, 970-977) --------------------
+template <bool SCALED>
+__global__ __launch_bounds__(kThreads) void acc_kernel(float* __restrict__ a, const float* __restrict__ b, int64_t n,
+                                                       float s) {
+    const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    if (SCALED) a[i] += s * b[i];
+    else a[i] += b[i];
+}
+
+inline unsigned blocks_for(int64_t n) { return unsigned((n + kThreads - 1) / kThreads); }
+bool bad_count(int64_t n) { return n < 0 || n > dgm::kMaxIndex; }
+
+int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w, const float* dy, float* dx,
+                   float* dweight, int64_t rows, int64_t cols) {
+    if (rows == 0 || cols == 0) return DGM_OK;
+    hipLaunchKernelGGL(rms_bwd_dx_kernel, dim3(unsigned((rows + 3) / 4)), dim3(kThreads), 0, g->stream, x, rstd, w,
+                       dy, dx, int(rows), int(cols));
+    hipLaunchKernelGGL(rms_bwd_dw_kernel, dim3(unsigned((cols + 63) / 64)), dim3(64 * kDwWaves), 0, g->stream, x,
+                       rstd, dy, dweight, int(rows), int(cols));
+    return dgm::check_launch(g, "rms_bwd");
+}
+
+int launch_attn_bwd(dgm_gpu* g, const AttnBwdArgs& a) {
+    const int64_t n = int64_t(a.B) * a.T * a.H * a.D, tt = int64_t(a.B) * a.H * a.T * a.T;
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(attn_bwd_dv_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a);
+    hipLaunchKernelGGL(attn_bwd_dp_kernel, dim3(blocks_for(tt)), dim3(kThreads), 0, g->stream, a);
+    hipLaunchKernelGGL(attn_softmax_bwd_kernel, dim3(blocks_for(int64_t(a.B) * a.H * a.T)), dim3(kThreads), 0,
+                       g->stream, a);
+    hipLaunchKernelGGL(attn_bwd_dqk_kernel<true>, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a);
+    hipLaunchKernelGGL(attn_bwd_dqk_kernel<false>, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a);
+    return dgm::check_launch(g, "attn_bwd");
+}
+
+int launch_rope_bwd(dgm_gpu* g, const float* dy, float* dx, const float* c, const float* s, int B, int T, int H,
+                    int D) {
+    const int64_t n = int64_t(B) * T * H * D;
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(rope_bwd_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, dy, dx, c, s, B, T, H, D);
+    return dgm::check_launch(g, "rope_bwd");
+}
+
+int launch_swiglu_bwd(dgm_gpu* g, const float* gate, const float* up, const float* dy, float* dgate, float* dup,
+                      int64_t n) {
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, gate, up, dy, dgate,
+                       dup, n);
+    return dgm::check_launch(g, "swiglu_bwd");
+}
+
+int launch_sum_heads(dgm_gpu* g, const float* src, float* dst, int B, int T, int H, int D) {
+    const int64_t n = int64_t(B) * T * D;
+    if (n == 0) return DGM_OK;
+    hipLaunchKernelGGL(sum_heads_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, src, dst, B, T, H, D);
+    return dgm::check_launch(g, "sum_heads");
+}
+
+int launch_acc(dgm_gpu* g, float* a, const float* b, int64_t n, float s, bool scaled) {
+    if (n == 0) return DGM_OK;
+    if (scaled)
+        hipLaunchKernelGGL(acc_kernel<true>, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a, b, n, s);
+    else
+        hipLaunchKernelGGL(acc_kernel<false>, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a, b, n, s);
+    return dgm::check_launch(g, scaled ? "acc_scale_f" : "acc_f");
+}
+
+int check_bthd(dgm_gpu* g, const char* name, int64_t B, int64_t T, int64_t H, int64_t D) {
+    if (B < 0 || T < 0 || H < 0 || D < 0) return dgm::fail(g, DGM_ERR_ARG, "%s: negative size", name);
+    if (bad_count(B * T * H * D) || bad_count(B * H * T * T))
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "%s: sizes beyond 2^31 elements", name);
+    return DGM_OK;
+}
+
+// ---- block layout ----------------------------------------------------------------
+// Saved activations of one loop (the reference's Acts, src/DiT.swift:260-300),
+// then the forward's shared scratch.
+enum { A_X, A_LN1, A_R1, A_Q, A_K, A_V, A_PROBS, A_AV, A_ATTN, A_R1B, A_MID, A_LN2, A_R2, A_GATE, A_UP, A_SW,
+       A_MLP, A_R2B, A_PRE, A_RF, A_COUNT };
+enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_COUNT };
+// Backward scratch.
+enum { B_T1, B_T2, B_DLN, B_DSW, B_DG, B_DU, B_DAV, B_DQ, B_DK, B_DV, B_DPROBS, B_DSCORES, B_DK1, B_DV1,
+       B_DVPRE, B_DFIRST, B_QPRE, B_KPRE, B_COUNT };
+
+inline int64_t pad64(int64_t n) { return (n + 63) & ~int64_t(63); }
+
+void act_sizes(const dgm_dit_cfg* c, int64_t* a, int64_t* f) {
+    const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
+    const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
+    const int64_t av[A_COUNT] = {M * C, M * C, M, M * C, M * C, M * C, att, M * C, M * C, M,
+                                 M * C, M * C, M, M * F, M * F, M * F, M * C, M, M * C, M};
+    const int64_t fv[F_COUNT] = {M * C, M * KV, M * KV, M * KV, M * KV, M * KV, att, M * C};
+    for (int i = 0; i < A_COUNT; ++i) a[i] = pad64(av[i]);
+    for (int i = 0; i < F_COUNT; ++i) f[i] = pad64(fv[i]);
+}
+
+void bwd_sizes(const dgm_dit_cfg* c, int64_t* b) {
+    const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
+    const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
+    const int64_t bv[B_COUNT] = {M * C, M * C, M * C, M * F, M * F, M * F, M * C, M * C, M * C, M * C,
+                                 att,   att,   M * KV, M * KV, M * KV, M * KV, M * C, M * KV};
+    for (int i = 0; i < B_COUNT; ++i) b[i] = pad64(bv[i]);
+}
+
+int64_t acts_floats(const dgm_dit_cfg* c) {
+    int64_t a[A_COUNT], f[F_COUNT], per = 0, tot = 0;
+    act_sizes(c, a, f);
+    for (int i = 0; i < A_COUNT; ++i) per += a[i];
+    for (int i = 0; i < F_COUNT; ++i) tot += f[i];
+    return per * c->loops + tot;
+}
+
+int64_t bwd_floats(const dgm_dit_cfg* c) {
+    int64_t b[B_COUNT], tot = 0;
+    bwd_sizes(c, b);
+    for (int i = 0; i < B_COUNT; ++i) tot += b[i];
+    return tot;
+}
+
+// Shared validation of the block entry points.
+int check_cfg(dgm_gpu* g, const char* name, const dgm_dit_cfg* c, const dgm_dit_weights* w, bool need_master) {
+    if (!c || !w) return dgm::fail(g, DGM_ERR_ARG, "%s: null argument", name);
+    if (c->bits != 4 && c->bits != 8 && c->bits != 32)
+        return dgm::fail(g, DGM_ERR_BITS, "%s: unsupported bits %d", name, c->bits);
+    if (c->B <= 0 || c->T <= 0 || c->C <= 0 || c->F <= 0 || c->H <= 0 || c->D <= 0 || c->loops < 0 ||
+        c->loops > 64 || c->H * c->D != c->C || c->D % 2 != 0)
+        return dgm::fail(g, DGM_ERR_SHAPE, "%s: bad config (C must be H*D, D even, loops <= 64)", name);
+    if (c->bits != 32 && (c->group <= 0 || c->C % c->group != 0 || c->F % c->group != 0 ||
+                          (c->bits == 4 && c->group % 2 != 0)))
+        return dgm::fail(g, DGM_ERR_SHAPE, "%s: C and F must be multiples of an (even for int4) group", name);
+    if (bad_count(int64_t(c->B) * c->T * (c->C + 2 * c->F)) || bad_count(int64_t(c->B) * c->H * c->T * c->T))
+        return dgm::fail(g, DGM_ERR_UNSUPPORTED, "%s: activations beyond 2^31 elements", name);
+    const dgm_dit_linear* lins[7] = {&w->wq, &w->wk, &w->wv, &w->wo, &w->wgate, &w->wup, &w->wdown};
+    for (const dgm_dit_linear* L : lins) {
+        if (c->bits == 32 ? !L->w : (!L->q || !L->scale)) return dgm::fail(g, DGM_ERR_ARG, "%s: null weight", name);
+        (void)need_master;
+    }
+    if (!w->n1 || !w->n1b || !w->n2 || !w->n2b || !w->nf) return dgm::fail(g, DGM_ERR_ARG, "%s: null norm", name);
+    return DGM_OK;
+}
+
+}  // namespace
+
+#define DGM_TRY(expr)                \
+    do {                             \
+        int _r = (expr);             \
+        if (_r != DGM_OK) return _r; \
+    } while (0)
+
+extern "C" {
+
+int dgm_rmsBwd(dgm_gpu* g, const float* x, const float* rstd, const float* weight, const float* dy, float* dx,
+               float* dweight, int64_t rows, int64_t cols, float eps) {
+    (void)eps;   // GPU.rmsBwd passes eps; the backward uses the saved rstd
+    int rc = dgm::enter(g, "rmsnorm_bwd");
+    if (rc) return rc;
+    if (rows < 0 || cols < 0 || bad_count(rows * cols)) return dgm::fail(g, DGM_ERR_ARG, "rmsBwd: bad sizes");
+    if (rows * cols && (!x || !rstd || !weight || !dy || !dx || !dweight))
+        return dgm::fail(g, DGM_ERR_ARG, "rmsBwd: null buffer");
+    return launch_rms_bwd(g, x, rstd, weight, dy, dx, dweight, rows, cols);
+}
+
+int dgm_attnBwd(dgm_gpu* g, const float* q, const float* k, const float* v, const float* probs, const float* dout,
+                float* dq, float* dk, float* dv, float* dprobs, float* dscores, int64_t B, int64_t T, int64_t H,
+                int64_t D) {
+    int rc = dgm::enter(g, "attn_bwd");
+    if (rc) return rc;
+    DGM_TRY(check_bthd(g, "attnBwd", B, T, H, D));
+    if (B * T * H * D && (!q || !k || !v || !probs || !dout || !dq || !dk || !dv || !dprobs || !dscores))
+        return dgm::fail(g, DGM_ERR_ARG, "attnBwd: null buffer");
+    AttnBwdArgs a{q, k, v, probs, dout, dq, dk, dv, dprobs, dscores, int(B), int(T), int(H), int(D),
+                  D > 0 ? 1.0f / sqrtf(float(D)) : 0.0f};
+    return launch_attn_bwd(g, a);
+}
+
+int dgm_ropeBwd(dgm_gpu* g, const float* dy, float* dx, const float* cos_t, const float* sin_t, int64_t B,
+                int64_t T, int64_t H, int64_t D) {
+    int rc = dgm::enter(g, "rope_bwd");
+    if (rc) return rc;
+    DGM_TRY(check_bthd(g, "ropeBwd", B, T, H, D));
+    if (D % 2) return dgm::fail(g, DGM_ERR_SHAPE, "ropeBwd: head dim must be even");
+    if (B * T * H * D && (!dy || !dx || !cos_t || !sin_t)) return dgm::fail(g, DGM_ERR_ARG, "ropeBwd: null buffer");
+    return launch_rope_bwd(g, dy, dx, cos_t, sin_t, int(B), int(T), int(H), int(D));
+}
+
+int dgm_swigluBwd(dgm_gpu* g, const float* gate, const float* up, const float* dy, float* dgate, float* dup,
+                  int64_t n) {
+    int rc = dgm::enter(g, "swiglu_bwd");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "swigluBwd: bad count");
+    if (n && (!gate || !up || !dy || !dgate || !dup)) return dgm::fail(g, DGM_ERR_ARG, "swigluBwd: null buffer");
+    return launch_swiglu_bwd(g, gate, up, dy, dgate, dup, n);
+}
+
+int dgm_sumHeads(dgm_gpu* g, const float* src, float* dst, int64_t B, int64_t T, int64_t H, int64_t D) {
+    int rc = dgm::enter(g, "sum_heads");
+    if (rc) return rc;
+    DGM_TRY(check_bthd(g, "sumHeads", B, T, H, D));
+    if (B * T * D && (!src || !dst)) return dgm::fail(g, DGM_ERR_ARG, "sumHeads: null buffer");
+    return launch_sum_heads(g, src, dst, int(B), int(T), int(H), int(D));
+}
+
+int dgm_acc(dgm_gpu* g, float* a, const float* b, int64_t n) {
+    int rc = dgm::enter(g, "acc_f");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "acc: bad count");
+    if (n && (!a || !b)) return dgm::fail(g, DGM_ERR_ARG, "acc: null buffer");
+    return launch_acc(g, a, b, n, 1.0f, false);
+}
+
+int dgm_accScale(dgm_gpu* g, float* a, const float* b, int64_t n, float s) {
+    int rc = dgm::enter(g, "acc_scale_f");
+    if (rc) return rc;
+    if (bad_count(n)) return dgm::fail(g, DGM_ERR_ARG, "accScale: bad count");
+    if (n && (!a || !b)) return dgm::fail(g, DGM_ERR_ARG, "accScale: null buffer");
+    return launch_acc(g, a, b, n, s, true);
+}
+
+int64_t dgm_dit_acts_floats(const dgm_dit_cfg* c) {
+    if (!c || c->loops < 0 || c->B <= 0 || c->T <= 0) return -1;
+    return acts_floats(c);
+}
+
+int64_t dgm_dit_backward_ws_floats(const dgm_dit_cfg* c) {
+    if (!c || c->B <= 0 || c->T <= 0) return -1;
+    return bwd_floats(c);
+}
+
+int dgm_dit_forward_train(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
+                          const float* sinv, float* x, float* acts, int64_t acts_n) {
+    int rc = dgm::enter(g, "dit_forward_train");
+    if (rc) return rc;
+    DGM_TRY(check_cfg(g, "dit_forward_train", c, w, false));
+    if (!x || !acts || !cosv || !sinv) return dgm::fail(g, DGM_ERR_ARG, "dit_forward_train: null buffer");
+    if (acts_n < acts_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_forward_train: activation buffer too small");
+    int64_t asz[A_COUNT], fsz[F_COUNT];
+    act_sizes(c, asz, fsz);
+    const int L = c->loops;
+    float* cur = acts;
+    auto A = [&](int l, int i) {
+        float* p = acts;
+        for (int j = 0; j < l; ++j)
+            for (int k = 0; k < A_COUNT; ++k) p += asz[k];
+        for (int k = 0; k < i; ++k) p += asz[k];
+        return p;
+    };
+    for (int l = 0; l < L; ++l)
+        for (int k = 0; k < A_COUNT; ++k) cur += asz[k];
+    float* S[F_COUNT];
+    for (int i = 0; i < F_COUNT; ++i) {
+        S[i] = cur;
+        cur += fsz[i];
+    }
+    const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
+    const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, nC = M * C, nKV = M * KV;
+    const float mix = c->mix;
+    auto lin = [&](const dgm_dit_linear& Lw, const float* in, float* out, int64_t N, int64_t K) {
+        return dgm_gemmNT(g, bits, Lw.w, Lw.q, Lw.scale, in, nullptr, out, M, N, K, bits == 32 ? 8 : G);
+    };
+    for (int l = 0; l < L; ++l) {
+        float* X = A(l, A_X);
+        if (l == 0) DGM_TRY(dgm_copy(g, x, X, nC));
+        DGM_TRY(dgm_rmsFwd(g, X, A(l, A_LN1), A(l, A_R1), w->n1, M, C, c->eps));
+        DGM_TRY(lin(w->wq, A(l, A_LN1), S[F_QPRE], C, C));
+        DGM_TRY(lin(w->wk, A(l, A_LN1), S[F_KPRE], KV, C));
+        DGM_TRY(lin(w->wv, A(l, A_LN1), S[F_VPRE], KV, C));
+        if (l == 0) {
+            DGM_TRY(dgm_copy(g, S[F_VPRE], S[F_VFIRST], nKV));
+            DGM_TRY(dgm_repeatHeads(g, S[F_VPRE], A(l, A_V), B, T, H, D));
+        } else {
+            DGM_TRY(dgm_mix(g, S[F_VPRE], S[F_VFIRST], S[F_VMIX], nKV, 1.0f - mix, mix));
+            DGM_TRY(dgm_repeatHeads(g, S[F_VMIX], A(l, A_V), B, T, H, D));
+        }
+        DGM_TRY(dgm_ropeFwd(g, S[F_QPRE], A(l, A_Q), cosv, sinv, B, T, H, D));
+        DGM_TRY(dgm_ropeFwd(g, S[F_KPRE], S[F_KROT], cosv, sinv, B, T, 1, D));
+        DGM_TRY(dgm_repeatHeads(g, S[F_KROT], A(l, A_K), B, T, H, D));
+        DGM_TRY(dgm_attnFwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), S[F_SCORES], A(l, A_PROBS), A(l, A_AV), B, T, H, D,
+                            0));
+        DGM_TRY(lin(w->wo, A(l, A_AV), A(l, A_ATTN), C, C));
+        DGM_TRY(dgm_rmsFwd(g, A(l, A_ATTN), S[F_T1], A(l, A_R1B), w->n1b, M, C, c->eps));
+        DGM_TRY(dgm_add(g, X, S[F_T1], A(l, A_MID), nC));
+        DGM_TRY(dgm_rmsFwd(g, A(l, A_MID), A(l, A_LN2), A(l, A_R2), w->n2, M, C, c->eps));
+        DGM_TRY(lin(w->wgate, A(l, A_LN2), A(l, A_GATE), F, C));
+        DGM_TRY(lin(w->wup, A(l, A_LN2), A(l, A_UP), F, C));
+        DGM_TRY(dgm_swigluFwd(g, A(l, A_GATE), A(l, A_UP), A(l, A_SW), M * F));
+        DGM_TRY(lin(w->wdown, A(l, A_SW), A(l, A_MLP), C, F));
+        DGM_TRY(dgm_rmsFwd(g, A(l, A_MLP), S[F_T1], A(l, A_R2B), w->n2b, M, C, c->eps));
+        DGM_TRY(dgm_add(g, A(l, A_MID), S[F_T1], A(l, A_PRE), nC));
+        DGM_TRY(dgm_rmsFwd(g, A(l, A_PRE), l + 1 < L ? A(l + 1, A_X) : x, A(l, A_RF), w->nf, M, C, c->eps));
+    }
+    return DGM_OK;
+}
+
+int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const dgm_dit_grads* gr,
+                     const float* cosv, const float* sinv, const float* acts, int64_t acts_n, float* gx, float* ws,
+                     int64_t ws_n) {
+    int rc = dgm::enter(g, "dit_backward");
+    if (rc) return rc;
+    DGM_TRY(check_cfg(g, "dit_backward", c, w, true));
+    if (!gr || !acts || !gx || !ws || !cosv || !sinv) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: null buffer");
+    float* const gws[7] = {gr->wq, gr->wk, gr->wv, gr->wo, gr->wgate, gr->wup, gr->wdown};
+    float* const gns[5] = {gr->n1, gr->n1b, gr->n2, gr->n2b, gr->nf};
+    for (float* p : gws)
+        if (!p) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: null weight gradient");
+    for (float* p : gns)
+        if (!p) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: null norm gradient");
+    if (acts_n < acts_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: activation buffer too small");
+    if (ws_n < bwd_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: workspace too small");
+    int64_t asz[A_COUNT], fsz[F_COUNT], bsz[B_COUNT];
+    act_sizes(c, asz, fsz);
+    bwd_sizes(c, bsz);
+    auto A = [&](int l, int i) {
+        const float* p = acts;
+        for (int j = 0; j < l; ++j)
+            for (int k = 0; k < A_COUNT; ++k) p += asz[k];
+        for (int k = 0; k < i; ++k) p += asz[k];
+        return p;
+    };
+    float* S[B_COUNT];
+    float* cur = ws;
+    for (int i = 0; i < B_COUNT; ++i) {
+        S[i] = cur;
+        cur += bsz[i];
+    }
+    const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
+    const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, nC = M * C, nKV = M * KV;
+    const float mix = c->mix;
+    // dX through the linear (fp32 master for bits 32, dequantized codes for
+    // bits 8 / 4) and dW accumulated into its fp32 gradient.
+    auto dx = [&](const dgm_dit_linear& Lw, const float* dy, float* out, int64_t N, int64_t K) {
+        return dgm_gemmDX(g, bits, Lw.w, Lw.q, Lw.scale, dy, out, M, N, K, bits == 32 ? 8 : G);
+    };
+    auto dw = [&](const float* dy, const float* in, float* dW, int64_t N, int64_t K) {
+        return dgm_gemmDWAcc(g, dy, in, dW, M, N, K);
+    };
+    float *t1 = S[B_T1], *t2 = S[B_T2], *dln = S[B_DLN];
+    DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
+    for (int l = c->loops - 1; l >= 0; --l) {
+        DGM_TRY(dgm_rmsBwd(g, A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, M, C, c->eps));
+        DGM_TRY(dgm_rmsBwd(g, A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, M, C, c->eps));
+        DGM_TRY(dw(t2, A(l, A_SW), gr->wdown, C, F));
+        DGM_TRY(dx(w->wdown, t2, S[B_DSW], C, F));
+        DGM_TRY(dgm_swigluBwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
+        DGM_TRY(dw(S[B_DG], A(l, A_LN2), gr->wgate, F, C));
+        DGM_TRY(dx(w->wgate, S[B_DG], t2, F, C));
+        DGM_TRY(dw(S[B_DU], A(l, A_LN2), gr->wup, F, C));
+        DGM_TRY(dx(w->wup, S[B_DU], dln, F, C));
+        DGM_TRY(dgm_acc(g, t2, dln, nC));
+        DGM_TRY(dgm_rmsBwd(g, A(l, A_MID), A(l, A_R2), w->n2, t2, dln, gr->n2, M, C, c->eps));
+        DGM_TRY(dgm_acc(g, t1, dln, nC));
+        DGM_TRY(dgm_rmsBwd(g, A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, M, C, c->eps));
+        DGM_TRY(dw(t2, A(l, A_AV), gr->wo, C, C));
+        DGM_TRY(dx(w->wo, t2, S[B_DAV], C, C));
+        DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK], S[B_DV],
+                            S[B_DPROBS], S[B_DSCORES], B, T, H, D));
+        DGM_TRY(dgm_sumHeads(g, S[B_DK], S[B_DK1], B, T, H, D));
+        DGM_TRY(dgm_sumHeads(g, S[B_DV], S[B_DV1], B, T, H, D));
+        DGM_TRY(dgm_ropeBwd(g, S[B_DQ], S[B_QPRE], cosv, sinv, B, T, H, D));
+        DGM_TRY(dgm_ropeBwd(g, S[B_DK1], S[B_KPRE], cosv, sinv, B, T, 1, D));
+        if (l == 0) {
+            DGM_TRY(dgm_copy(g, S[B_DV1], S[B_DVPRE], nKV));
+            DGM_TRY(dgm_acc(g, S[B_DVPRE], S[B_DFIRST], nKV));
+        } else {
+            DGM_TRY(dgm_mix(g, S[B_DV1], S[B_DV1], S[B_DVPRE], nKV, 1.0f - mix, 0.0f));
+            DGM_TRY(dgm_accScale(g, S[B_DFIRST], S[B_DV1], nKV, mix));
+        }
+        DGM_TRY(dw(S[B_QPRE], A(l, A_LN1), gr->wq, C, C));
+        DGM_TRY(dx(w->wq, S[B_QPRE], t2, C, C));
+        DGM_TRY(dw(S[B_KPRE], A(l, A_LN1), gr->wk, KV, C));
+        DGM_TRY(dx(w->wk, S[B_KPRE], dln, KV, C));
+        DGM_TRY(dgm_acc(g, t2, dln, nC));
+        DGM_TRY(dw(S[B_DVPRE], A(l, A_LN1), gr->wv, KV, C));
+        DGM_TRY(dx(w->wv, S[B_DVPRE], dln, KV, C));
+        DGM_TRY(dgm_acc(g, t2, dln, nC));
+        DGM_TRY(dgm_rmsBwd(g, A(l, A_X), A(l, A_R1), w->n1, t2, dln, gr->n1, M, C, c->eps));
+        DGM_TRY(dgm_acc(g, t1, dln, nC));
+        DGM_TRY(dgm_copy(g, t1, gx, nC));
+    }
+    return DGM_OK;
+}
+
+}  // extern "C"
+#undef DGM_TRY

@@ -15,7 +15,7 @@ from typing import Dict
 
 import numpy as np
 
-from .abi import DIT_LINEARS, DIT_NORMS, DgmError, DiTCfg, DiTLinear, DiTWeights, load_library
+from .abi import DIT_LINEARS, DIT_NORMS, DgmError, DiTCfg, DiTGrads, DiTLinear, DiTWeights, load_library
 from .gpu import GPU, _ptr
 
 
@@ -138,6 +138,42 @@ class DiTBlock:
         if x.numel() != cfg.B * cfg.T * cfg.C or not x.is_contiguous():
             raise ValueError("x must be a contiguous [B*T, C] tensor")
         self.gpu.dit_forward(self.c, self.w, self.cos, self.sin, x, self.ws, self.ws_floats)
+
+    # -- training (src/DiT.swift:520-626) -------------------------------------
+    def zero_grads(self) -> None:
+        """Allocates (first call) or clears the fp32 parameter gradients."""
+        import torch
+        if not hasattr(self, "grads"):
+            shapes = self.cfg.linear_shapes()
+            dev = self.cos.device
+            self.grads = {n: torch.zeros(shapes[n][0] * shapes[n][1], dtype=torch.float32, device=dev)
+                          for n in DIT_LINEARS}
+            self.grads.update({n: torch.zeros(self.cfg.C, dtype=torch.float32, device=dev) for n in DIT_NORMS})
+            self.c_grads = DiTGrads(*[self.grads[n].data_ptr() for n in DIT_LINEARS],
+                                    *[self.grads[n].data_ptr() for n in DIT_NORMS])
+            self.acts_floats = self.gpu.dit_acts_floats(self.c)
+            self.bws_floats = self.gpu.dit_backward_ws_floats(self.c)
+            self.acts = torch.zeros(max(self.acts_floats, 1), dtype=torch.float32, device=dev)
+            self.bws = torch.zeros(max(self.bws_floats, 1), dtype=torch.float32, device=dev)
+        else:
+            for t in self.grads.values():
+                t.zero_()
+
+    def forward_train(self, x) -> None:
+        """xs[0] -> xs[loops] in place, keeping every loop's activations for
+        backward(). Inside begin()/end(); call zero_grads() once first."""
+        cfg = self.cfg
+        if x.numel() != cfg.B * cfg.T * cfg.C or not x.is_contiguous():
+            raise ValueError("x must be a contiguous [B*T, C] tensor")
+        if not hasattr(self, "acts"):
+            self.zero_grads()
+        self.gpu.dit_forward_train(self.c, self.w, self.cos, self.sin, x, self.acts, self.acts_floats)
+
+    def backward(self, gx) -> None:
+        """gx: dL/dxs[loops] -> dL/dxs[0] in place; adds the parameter
+        gradients into self.grads (fp32, keyed like the weights)."""
+        self.gpu.dit_backward(self.c, self.w, self.c_grads, self.cos, self.sin, self.acts, self.acts_floats, gx,
+                              self.bws, self.bws_floats)
 
     def workspace_view(self, name: str):
         """The last loop's intermediate `name` (scores, probs, ...) as a view of

@@ -15,7 +15,7 @@ import ctypes
 from typing import Any, Optional
 
 from .abi import (DGM_MATH_BF16, DGM_MATH_FP32, AdamP, BiasP, DgmError, DiTCfg,
-                  DiTWeights, EmbBwdP, EmbP, GemmP, PosP, QuantP, ReduceP, ScaleP,
+                  DiTGrads, DiTWeights, EmbBwdP, EmbP, GemmP, PosP, QuantP, ReduceP, ScaleP,
                   UnaryP, load_library)
 
 
@@ -147,6 +147,45 @@ class GPU:
 
     def copy(self, x, y, n: int) -> None:
         self._check(self.lib.dgm_copy(self.h, _ptr(x), _ptr(y), n))
+
+    def rmsBwd(self, x, rstd, weight, dy, dx, dweight, rows: int, cols: int, eps: float) -> None:
+        self._check(self.lib.dgm_rmsBwd(self.h, _ptr(x), _ptr(rstd), _ptr(weight), _ptr(dy), _ptr(dx), _ptr(dweight),
+                                        rows, cols, eps))
+
+    def attnBwd(self, q, k, v, probs, dout, dq, dk, dv, dprobs, dscores, B: int, T: int, H: int, D: int) -> None:
+        self._check(self.lib.dgm_attnBwd(self.h, _ptr(q), _ptr(k), _ptr(v), _ptr(probs), _ptr(dout), _ptr(dq),
+                                         _ptr(dk), _ptr(dv), _ptr(dprobs), _ptr(dscores), B, T, H, D))
+
+    def ropeBwd(self, dy, dx, cos, sin, B: int, T: int, H: int, D: int) -> None:
+        self._check(self.lib.dgm_ropeBwd(self.h, _ptr(dy), _ptr(dx), _ptr(cos), _ptr(sin), B, T, H, D))
+
+    def swigluBwd(self, gate, up, dy, dgate, dup, n: int) -> None:
+        self._check(self.lib.dgm_swigluBwd(self.h, _ptr(gate), _ptr(up), _ptr(dy), _ptr(dgate), _ptr(dup), n))
+
+    def sumHeads(self, src, dst, B: int, T: int, H: int, D: int) -> None:
+        self._check(self.lib.dgm_sumHeads(self.h, _ptr(src), _ptr(dst), B, T, H, D))
+
+    def acc(self, a, b, n: int) -> None:
+        self._check(self.lib.dgm_acc(self.h, _ptr(a), _ptr(b), n))
+
+    def accScale(self, a, b, n: int, by: float) -> None:
+        self._check(self.lib.dgm_accScale(self.h, _ptr(a), _ptr(b), n, by))
+
+    def dit_acts_floats(self, cfg: DiTCfg) -> int:
+        return int(self.lib.dgm_dit_acts_floats(ctypes.byref(cfg)))
+
+    def dit_backward_ws_floats(self, cfg: DiTCfg) -> int:
+        return int(self.lib.dgm_dit_backward_ws_floats(ctypes.byref(cfg)))
+
+    def dit_forward_train(self, cfg: DiTCfg, w: DiTWeights, cos, sin, x, acts, acts_floats: int) -> None:
+        self._check(self.lib.dgm_dit_forward_train(self.h, ctypes.byref(cfg), ctypes.byref(w), _ptr(cos), _ptr(sin),
+                                                   _ptr(x), _ptr(acts), acts_floats))
+
+    def dit_backward(self, cfg: DiTCfg, w: DiTWeights, grads: DiTGrads, cos, sin, acts, acts_floats: int, gx, ws,
+                     ws_floats: int) -> None:
+        self._check(self.lib.dgm_dit_backward(self.h, ctypes.byref(cfg), ctypes.byref(w), ctypes.byref(grads),
+                                              _ptr(cos), _ptr(sin), _ptr(acts), acts_floats, _ptr(gx), _ptr(ws),
+                                              ws_floats))
 
     def dit_workspace_floats(self, cfg: DiTCfg) -> int:
         return int(self.lib.dgm_dit_workspace_floats(ctypes.byref(cfg)))

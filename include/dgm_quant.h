@@ -233,6 +233,66 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w
                     const float* cos_t, const float* sin_t, float* x, float* ws,
                     int64_t ws_floats);
 
+/* ---- looped DiT block backward (src/DiT.swift:558-626) ---------------------
+ * The wrappers the backward loop calls, with the Swift names and buffer
+ * order, then a forward that saves every loop's activations and the block
+ * backward. */
+
+/* GPU.rmsBwd (src/GPU.swift:369-373; rmsnorm_bwd_dx / rmsnorm_bwd_dw,
+ * metal/kernels.metal:827-868): dx per row from the saved rstd, and
+ * dweight[c] += sum over rows of dy*x*rstd (the weight is shared by every
+ * loop). eps is accepted for the signature and unused, as in the reference. */
+int dgm_rmsBwd(dgm_gpu* g, const float* x, const float* rstd, const float* weight, const float* dy,
+               float* dx, float* dweight, int64_t rows, int64_t cols, float eps);
+/* GPU.attnBwd (src/GPU.swift:312-322; attn_bwd_dv, attn_bwd_dp,
+ * attn_softmax_bwd, attn_bwd_dq, attn_bwd_dk, metal/kernels.metal:508-612):
+ * q, k, v, dout, dq, dk, dv [B,T,H,D]; probs, dprobs, dscores [B,H,T,T]. */
+int dgm_attnBwd(dgm_gpu* g, const float* q, const float* k, const float* v, const float* probs,
+                const float* dout, float* dq, float* dk, float* dv, float* dprobs, float* dscores,
+                int64_t B, int64_t T, int64_t H, int64_t D);
+/* GPU.ropeBwd (src/GPU.swift:380-383; rope_bwd, metal/kernels.metal:891-909). */
+int dgm_ropeBwd(dgm_gpu* g, const float* dy, float* dx, const float* cos_t, const float* sin_t,
+                int64_t B, int64_t T, int64_t H, int64_t D);
+/* GPU.swigluBwd (src/GPU.swift:389-391; swiglu_bwd, metal/kernels.metal:932-949). */
+int dgm_swigluBwd(dgm_gpu* g, const float* gate, const float* up, const float* dy, float* dgate,
+                  float* dup, int64_t n);
+/* GPU.sumHeads (src/GPU.swift:412-415; sum_heads, metal/kernels.metal:995-1010):
+ * dst[b,t,:] = sum over h of src[b,t,h,:]. */
+int dgm_sumHeads(dgm_gpu* g, const float* src, float* dst, int64_t B, int64_t T, int64_t H, int64_t D);
+/* GPU.acc / GPU.accScale (src/GPU.swift:216-218, 402-405; acc_f, acc_scale_f,
+ * metal/kernels.metal:429-436, 970-977): a += b, a += s*b. */
+int dgm_acc(dgm_gpu* g, float* a, const float* b, int64_t n);
+int dgm_accScale(dgm_gpu* g, float* a, const float* b, int64_t n, float s);
+
+/* Gradients of the block's parameters, fp32, accumulated (+=): the seven
+ * linears [N,K] as in dgm_dit_weights and the five RMSNorm weights [C]. */
+typedef struct dgm_dit_grads {
+    float *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;
+    float *n1, *n1b, *n2, *n2b, *nf;
+} dgm_dit_grads;
+
+/* Floats of the activation buffer dgm_dit_forward_train fills (-1 for NULL). */
+int64_t dgm_dit_acts_floats(const dgm_dit_cfg* cfg);
+/* Floats of workspace dgm_dit_backward needs (-1 for NULL). */
+int64_t dgm_dit_backward_ws_floats(const dgm_dit_cfg* cfg);
+/* The loop body of DiT.forward (src/DiT.swift:520-550) with every loop's
+ * activations saved in acts (the reference's Acts): x holds xs[0] on entry
+ * and xs[loops] on exit. Linears as in dgm_dit_forward (bits 32: fp32
+ * weights; bits 8 / 4: codes + scales). */
+int dgm_dit_forward_train(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w,
+                          const float* cos_t, const float* sin_t, float* x, float* acts,
+                          int64_t acts_floats);
+/* The loop part of DiT.backward (src/DiT.swift:566-626) over the activations
+ * of dgm_dit_forward_train: gx holds dL/dxs[loops] on entry and dL/dxs[0] on
+ * exit; the parameter gradients are added into *grads. bits 32 runs dX on
+ * the fp32 weights, as the reference does; bits 8 / 4 run it through the
+ * dequantized codes (straight-through estimator) and dW into the fp32
+ * gradients. ws: dgm_dit_backward_ws_floats(cfg) floats. */
+int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* cfg, const dgm_dit_weights* w,
+                     const dgm_dit_grads* grads, const float* cos_t, const float* sin_t,
+                     const float* acts, int64_t acts_floats, float* gx, float* ws,
+                     int64_t ws_floats);
+
 /* ---- training step around the path: optimizer, re-quantize, embedding ----
  * GPT.step (src/GPT.swift:183-220) zeroes the grads, runs the backward, sums
  * the squared grads for clipping, scales them, applies AdamW to every master

@@ -550,3 +550,268 @@ void orc_bias_grad(const float* dy, float* db, int64_t M, int64_t N) {
         db[n] = acc;
     }
 }
+
+/* ---- DiT block backward ------------------------------------------------- */
+
+/* rmsnorm_bwd_dx + rmsnorm_bwd_dw, kernels.metal:827-868 (GPU.rmsBwd,
+ * GPU.swift:369-373): dweight accumulates. */
+void orc_rms_bwd(const float* x, const float* rstd, const float* weight, const float* dy, float* dx,
+                 float* dweight, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float rs = rstd[r];
+        float meanDyX = 0.0f;
+        for (int64_t c = 0; c < cols; ++c) {
+            float dyhat = dy[r * cols + c] * weight[c];
+            meanDyX += dyhat * x[r * cols + c];
+        }
+        meanDyX /= (float)cols;
+        float rs3 = rs * rs * rs;
+        for (int64_t c = 0; c < cols; ++c) {
+            float dyhat = dy[r * cols + c] * weight[c];
+            dx[r * cols + c] = rs * dyhat - x[r * cols + c] * rs3 * meanDyX;
+        }
+    }
+    for (int64_t c = 0; c < cols; ++c) {
+        float dg = 0.0f;
+        for (int64_t r = 0; r < rows; ++r) dg += dy[r * cols + c] * x[r * cols + c] * rstd[r];
+        dweight[c] += dg;
+    }
+}
+
+/* attn_bwd_dv / attn_bwd_dp / attn_softmax_bwd / attn_bwd_dq / attn_bwd_dk,
+ * kernels.metal:508-612, in GPU.attnBwd's order (GPU.swift:312-322). */
+void orc_attn_bwd(const float* q, const float* k, const float* v, const float* probs, const float* dout,
+                  float* dq, float* dk, float* dv, float* dprobs, float* dscores, int B, int T, int H, int D) {
+    const float scale = 1.0f / sqrtf((float)D);
+#define QI(b, t, h, d) ((((int64_t)(b) * T + (t)) * H + (h)) * D + (d))
+#define PI(b, h, t, s) ((((int64_t)(b) * H + (h)) * T + (t)) * T + (s))
+    for (int b = 0; b < B; ++b)
+        for (int s = 0; s < T; ++s)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    float acc = 0.0f;
+                    for (int t = 0; t < T; ++t) acc += probs[PI(b, h, t, s)] * dout[QI(b, t, h, d)];
+                    dv[QI(b, s, h, d)] = acc;
+                }
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H; ++h)
+            for (int t = 0; t < T; ++t)
+                for (int s = 0; s < T; ++s) {
+                    float acc = 0.0f;
+                    for (int d = 0; d < D; ++d) acc += dout[QI(b, t, h, d)] * v[QI(b, s, h, d)];
+                    dprobs[PI(b, h, t, s)] = acc;
+                }
+    for (int64_t row = 0; row < (int64_t)B * H * T; ++row) {
+        const float* pr = probs + row * T;
+        const float* g = dprobs + row * T;
+        float* o = dscores + row * T;
+        float dot = 0.0f;
+        for (int i = 0; i < T; ++i) dot += g[i] * pr[i];
+        for (int i = 0; i < T; ++i) o[i] = pr[i] * (g[i] - dot);
+    }
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    float acc = 0.0f;
+                    for (int s = 0; s < T; ++s) acc += dscores[PI(b, h, t, s)] * k[QI(b, s, h, d)];
+                    dq[QI(b, t, h, d)] = acc * scale;
+                }
+    for (int b = 0; b < B; ++b)
+        for (int s = 0; s < T; ++s)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    float acc = 0.0f;
+                    for (int t = 0; t < T; ++t) acc += dscores[PI(b, h, t, s)] * q[QI(b, t, h, d)];
+                    dk[QI(b, s, h, d)] = acc * scale;
+                }
+#undef QI
+#undef PI
+}
+
+/* rope_bwd, kernels.metal:891-909. */
+void orc_rope_bwd(const float* dy, float* dx, const float* cosv, const float* sinv, int B, int T, int H, int D) {
+    const int64_t total = (int64_t)B * T * H * D;
+    const int mid = D >> 1;
+    for (int64_t i = 0; i < total; ++i) {
+        int d = (int)(i % D);
+        int t = (int)((i / ((int64_t)H * D)) % T);
+        float c = cosv[t * D + d], s = sinv[t * D + d];
+        if (d < mid) dx[i] = dy[i] * c + dy[i + mid] * s;
+        else dx[i] = dy[i] * c - dy[i - mid] * s;
+    }
+}
+
+/* swiglu_bwd, kernels.metal:932-949. */
+void orc_swiglu_bwd(const float* gate, const float* up, const float* dy, float* dgate, float* dup, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float z = gate[i];
+        float s = silu_sigmoid(z);
+        float silu = z * s;
+        float siluP = s * (1.0f + z * (1.0f - s));
+        float g = dy[i];
+        dgate[i] = siluP * up[i] * g;
+        dup[i] = silu * g;
+    }
+}
+
+/* sum_heads, kernels.metal:995-1010. */
+void orc_sum_heads(const float* src, float* dst, int B, int T, int H, int D) {
+    for (int64_t i = 0; i < (int64_t)B * T * D; ++i) {
+        int d = (int)(i % D);
+        int t = (int)((i / D) % T);
+        int b = (int)(i / ((int64_t)T * D));
+        float acc = 0.0f;
+        for (int h = 0; h < H; ++h) acc += src[(((int64_t)b * T + t) * H + h) * D + d];
+        dst[i] = acc;
+    }
+}
+
+/* acc_scale_f, kernels.metal:970-977 (acc_f, 429-436, is s = 1 without the
+ * product: see orc_dit_train). */
+void orc_acc_scale(float* a, const float* b, int64_t n, float s) {
+    for (int64_t i = 0; i < n; ++i) a[i] += s * b[i];
+}
+
+static void acc_f(float* a, const float* b, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) a[i] += b[i];
+}
+
+/* Saved activations of one loop (DiT.swift's Acts) and the step's scratch. */
+enum { A_X, A_LN1, A_R1, A_Q, A_K, A_V, A_PROBS, A_AV, A_ATTN, A_R1B, A_MID, A_LN2, A_R2,
+       A_GATE, A_UP, A_SW, A_MLP, A_R2B, A_PRE, A_RF, A_COUNT };
+enum { S_QPRE, S_KPRE, S_VPRE, S_VFIRST, S_VMIX, S_KROT, S_SCORES, S_T1, S_T2, S_DLN, S_DSW, S_DG,
+       S_DU, S_DAV, S_DQ, S_DK, S_DV, S_DPROBS, S_DK1, S_DV1, S_DVPRE, S_DFIRST, S_COS, S_SIN,
+       S_COUNT };
+
+static void train_sizes(const orc_dit_cfg* c, int64_t* a, int64_t* sc) {
+    int64_t M = (int64_t)c->B * c->T, C = c->C, F = c->F, KV = c->D;
+    int64_t att = (int64_t)c->B * c->H * c->T * c->T;
+    int64_t av[A_COUNT] = { M * C, M * C, M, M * C, M * C, M * C, att, M * C, M * C, M, M * C, M * C, M,
+                            M * F, M * F, M * F, M * C, M, M * C, M };
+    int64_t sv[S_COUNT] = { M * C, M * KV, M * KV, M * KV, M * KV, M * KV, att, M * C, M * C, M * C, M * F,
+                            M * F, M * F, M * C, M * C, M * C, M * C, att, M * KV, M * KV, M * KV, M * KV,
+                            (int64_t)c->T * c->D, (int64_t)c->T * c->D };
+    memcpy(a, av, sizeof(av));
+    memcpy(sc, sv, sizeof(sv));
+}
+
+int64_t orc_dit_train_floats(const orc_dit_cfg* c) {
+    int64_t a[A_COUNT], sc[S_COUNT], per = 0, tot = 0;
+    train_sizes(c, a, sc);
+    for (int i = 0; i < A_COUNT; ++i) per += a[i];
+    for (int i = 0; i < S_COUNT; ++i) tot += sc[i];
+    return per * (c->loops > 0 ? c->loops : 1) + tot;
+}
+
+static int lin_fwd(const orc_dit_cfg* c, int i, const float* const* w, const void* const* q,
+                   const float* const* s, const float* x, float* y, int64_t M, int64_t N, int64_t K) {
+    if (c->bits == 32) { orc_gemm_nt(x, w[i], NULL, y, M, N, K); return 0; }
+    return orc_gemm_nt_q(q[i], s[i], x, NULL, y, M, N, K, c->group, c->bits);
+}
+
+static int lin_dx(const orc_dit_cfg* c, int i, const float* const* w, const void* const* q,
+                  const float* const* s, const float* dy, float* dx, int64_t M, int64_t N, int64_t K) {
+    if (c->bits == 32) { orc_gemm_dx(dy, w[i], dx, M, N, K); return 0; }
+    return orc_gemm_dx_q(q[i], s[i], dy, dx, M, N, K, c->group, c->bits);
+}
+
+int orc_dit_train(const orc_dit_cfg* c, const float* const* w, const void* const* q,
+                  const float* const* s, const float* const* norms, float* x_io, float* gy,
+                  float* const* gw, float* const* gn, float* ws) {
+    if (c->H * c->D != c->C || (c->D % 2) != 0) return -1;
+    enum { WQ, WK, WV, WO, WG, WU, WD };
+    const float *n1 = norms[0], *n1b = norms[1], *n2 = norms[2], *n2b = norms[3], *nf = norms[4];
+    int64_t asz[A_COUNT], ssz[S_COUNT];
+    train_sizes(c, asz, ssz);
+    const int L = c->loops;
+    float* cur = ws;
+    float* A[64][A_COUNT];
+    float* S[S_COUNT];
+    if (L > 64) return -1;
+    for (int l = 0; l < L; ++l)
+        for (int i = 0; i < A_COUNT; ++i) { A[l][i] = cur; cur += asz[i]; }
+    for (int i = 0; i < S_COUNT; ++i) { S[i] = cur; cur += ssz[i]; }
+    const int B = c->B, T = c->T, H = c->H, D = c->D;
+    const int64_t M = (int64_t)B * T, C = c->C, F = c->F, KV = D, nC = M * C, nKV = M * KV;
+    const float mix = c->mix;
+    orc_rope_tables(T, D, c->theta, S[S_COS], S[S_SIN]);
+    /* forward, DiT.swift:520-550, saving each loop's activations */
+    for (int l = 0; l < L; ++l) {
+        float** a = A[l];
+        if (l == 0) memcpy(a[A_X], x_io, sizeof(float) * (size_t)nC);
+        orc_rmsnorm_fwd(a[A_X], a[A_LN1], a[A_R1], n1, M, C, c->eps);
+        if (lin_fwd(c, WQ, w, q, s, a[A_LN1], S[S_QPRE], M, C, C)) return -1;
+        if (lin_fwd(c, WK, w, q, s, a[A_LN1], S[S_KPRE], M, KV, C)) return -1;
+        if (lin_fwd(c, WV, w, q, s, a[A_LN1], S[S_VPRE], M, KV, C)) return -1;
+        if (l == 0) {
+            memcpy(S[S_VFIRST], S[S_VPRE], sizeof(float) * (size_t)nKV);
+            orc_repeat_heads(S[S_VPRE], a[A_V], B, T, H, D);
+        } else {
+            orc_mix(S[S_VPRE], S[S_VFIRST], S[S_VMIX], nKV, 1.0f - mix, mix);
+            orc_repeat_heads(S[S_VMIX], a[A_V], B, T, H, D);
+        }
+        orc_rope_fwd(S[S_QPRE], a[A_Q], S[S_COS], S[S_SIN], B, T, H, D);
+        orc_rope_fwd(S[S_KPRE], S[S_KROT], S[S_COS], S[S_SIN], B, T, 1, D);
+        orc_repeat_heads(S[S_KROT], a[A_K], B, T, H, D);
+        orc_attn_fwd(a[A_Q], a[A_K], a[A_V], S[S_SCORES], a[A_PROBS], a[A_AV], B, T, H, D, 0);
+        if (lin_fwd(c, WO, w, q, s, a[A_AV], a[A_ATTN], M, C, C)) return -1;
+        orc_rmsnorm_fwd(a[A_ATTN], S[S_T1], a[A_R1B], n1b, M, C, c->eps);
+        orc_add(a[A_X], S[S_T1], a[A_MID], nC);
+        orc_rmsnorm_fwd(a[A_MID], a[A_LN2], a[A_R2], n2, M, C, c->eps);
+        if (lin_fwd(c, WG, w, q, s, a[A_LN2], a[A_GATE], M, F, C)) return -1;
+        if (lin_fwd(c, WU, w, q, s, a[A_LN2], a[A_UP], M, F, C)) return -1;
+        orc_swiglu_fwd(a[A_GATE], a[A_UP], a[A_SW], M * F);
+        if (lin_fwd(c, WD, w, q, s, a[A_SW], a[A_MLP], M, C, F)) return -1;
+        orc_rmsnorm_fwd(a[A_MLP], S[S_T1], a[A_R2B], n2b, M, C, c->eps);
+        orc_add(a[A_MID], S[S_T1], a[A_PRE], nC);
+        float* xn = l + 1 < L ? A[l + 1][A_X] : x_io;
+        orc_rmsnorm_fwd(a[A_PRE], xn, a[A_RF], nf, M, C, c->eps);
+    }
+    /* backward, DiT.swift:566-626 (the loop part; gy plays gx) */
+    float *t1 = S[S_T1], *t2 = S[S_T2], *dln = S[S_DLN];
+    memset(S[S_DFIRST], 0, sizeof(float) * (size_t)nKV);
+    for (int l = L - 1; l >= 0; --l) {
+        float** a = A[l];
+        orc_rms_bwd(a[A_PRE], a[A_RF], nf, gy, t1, gn[4], M, C);
+        orc_rms_bwd(a[A_MLP], a[A_R2B], n2b, t1, t2, gn[3], M, C);
+        orc_gemm_dw(t2, a[A_SW], gw[WD], M, C, F, 1);
+        if (lin_dx(c, WD, w, q, s, t2, S[S_DSW], M, C, F)) return -1;
+        orc_swiglu_bwd(a[A_GATE], a[A_UP], S[S_DSW], S[S_DG], S[S_DU], M * F);
+        orc_gemm_dw(S[S_DG], a[A_LN2], gw[WG], M, F, C, 1);
+        if (lin_dx(c, WG, w, q, s, S[S_DG], t2, M, F, C)) return -1;
+        orc_gemm_dw(S[S_DU], a[A_LN2], gw[WU], M, F, C, 1);
+        if (lin_dx(c, WU, w, q, s, S[S_DU], dln, M, F, C)) return -1;
+        acc_f(t2, dln, nC);
+        orc_rms_bwd(a[A_MID], a[A_R2], n2, t2, dln, gn[2], M, C);
+        acc_f(t1, dln, nC);
+        orc_rms_bwd(a[A_ATTN], a[A_R1B], n1b, t1, t2, gn[1], M, C);
+        orc_gemm_dw(t2, a[A_AV], gw[WO], M, C, C, 1);
+        if (lin_dx(c, WO, w, q, s, t2, S[S_DAV], M, C, C)) return -1;
+        orc_attn_bwd(a[A_Q], a[A_K], a[A_V], a[A_PROBS], S[S_DAV], S[S_DQ], S[S_DK], S[S_DV],
+                     S[S_DPROBS], S[S_SCORES], B, T, H, D);
+        orc_sum_heads(S[S_DK], S[S_DK1], B, T, H, D);
+        orc_sum_heads(S[S_DV], S[S_DV1], B, T, H, D);
+        orc_rope_bwd(S[S_DQ], S[S_QPRE], S[S_COS], S[S_SIN], B, T, H, D);
+        orc_rope_bwd(S[S_DK1], S[S_KPRE], S[S_COS], S[S_SIN], B, T, 1, D);
+        if (l == 0) {
+            memcpy(S[S_DVPRE], S[S_DV1], sizeof(float) * (size_t)nKV);
+            acc_f(S[S_DVPRE], S[S_DFIRST], nKV);
+        } else {
+            orc_mix(S[S_DV1], S[S_DV1], S[S_DVPRE], nKV, 1.0f - mix, 0.0f);
+            orc_acc_scale(S[S_DFIRST], S[S_DV1], nKV, mix);
+        }
+        orc_gemm_dw(S[S_QPRE], a[A_LN1], gw[WQ], M, C, C, 1);
+        if (lin_dx(c, WQ, w, q, s, S[S_QPRE], t2, M, C, C)) return -1;
+        orc_gemm_dw(S[S_KPRE], a[A_LN1], gw[WK], M, KV, C, 1);
+        if (lin_dx(c, WK, w, q, s, S[S_KPRE], dln, M, KV, C)) return -1;
+        acc_f(t2, dln, nC);
+        orc_gemm_dw(S[S_DVPRE], a[A_LN1], gw[WV], M, KV, C, 1);
+        if (lin_dx(c, WV, w, q, s, S[S_DVPRE], dln, M, KV, C)) return -1;
+        acc_f(t2, dln, nC);
+        orc_rms_bwd(a[A_X], a[A_R1], n1, t2, dln, gn[0], M, C);
+        acc_f(t1, dln, nC);
+        memcpy(gy, t1, sizeof(float) * (size_t)nC);
+    }
+    return 0;
+}

@@ -113,6 +113,28 @@ void orc_embed_bwd(const uint32_t* tokens, const float* dx, float* dwe, int B, i
 void orc_pos_bwd(const float* dx, float* dwp, int B, int T, int C);
 void orc_bias_grad(const float* dy, float* db, int64_t M, int64_t N);
 
+/* ---- DiT block backward: kernels.metal:429-437, 508-612, 827-868, 891-949,
+ * 970-1010; DiT.swift:558-626 ------------------------------------------- */
+void orc_rms_bwd(const float* x, const float* rstd, const float* weight, const float* dy, float* dx,
+                 float* dweight, int64_t rows, int64_t cols);
+void orc_attn_bwd(const float* q, const float* k, const float* v, const float* probs, const float* dout,
+                  float* dq, float* dk, float* dv, float* dprobs, float* dscores, int B, int T, int H, int D);
+void orc_rope_bwd(const float* dy, float* dx, const float* cosv, const float* sinv, int B, int T, int H, int D);
+void orc_swiglu_bwd(const float* gate, const float* up, const float* dy, float* dgate, float* dup, int64_t n);
+void orc_sum_heads(const float* src, float* dst, int B, int T, int H, int D);
+void orc_acc_scale(float* a, const float* b, int64_t n, float s);
+/* One training step of the looped block: forward over cfg->loops loops saving
+ * every loop's activations, then the backward of DiT.swift:566-626 (the loop
+ * part). Linears: bits 32 uses w[i] (fp32 [N,K]); bits 8/4 run the forward on
+ * the codes (Metal kernel order) and the STE dX through the dequantized codes.
+ * x_io: xs[0] in, xs[loops] out. gy: dL/dxs[loops] in, dL/dxs[0] out.
+ * gw[7] (+=, fp32 [N,K]) and gn[5] (+=, [C]) receive the weight gradients.
+ * ws: orc_dit_train_floats(c) floats. */
+int64_t orc_dit_train_floats(const orc_dit_cfg* c);
+int orc_dit_train(const orc_dit_cfg* c, const float* const* w, const void* const* q,
+                  const float* const* s, const float* const* norms, float* x_io, float* gy,
+                  float* const* gw, float* const* gn, float* ws);
+
 #ifdef __cplusplus
 }
 #endif

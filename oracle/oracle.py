@@ -69,6 +69,14 @@ def lib() -> ctypes.CDLL:
             "orc_embed_bwd": (None, [_P, _P, _P, _i, _i, _i, _i]),
             "orc_pos_bwd": (None, [_P, _P, _i, _i, _i]),
             "orc_bias_grad": (None, [_P, _P, _i64, _i64]),
+            "orc_rms_bwd": (None, [_P, _P, _P, _P, _P, _P, _i64, _i64]),
+            "orc_attn_bwd": (None, [_P] * 10 + [_i, _i, _i, _i]),
+            "orc_rope_bwd": (None, [_P, _P, _P, _P, _i, _i, _i, _i]),
+            "orc_swiglu_bwd": (None, [_P, _P, _P, _P, _P, _i64]),
+            "orc_sum_heads": (None, [_P, _P, _i, _i, _i, _i]),
+            "orc_acc_scale": (None, [_P, _P, _i64, ctypes.c_float]),
+            "orc_dit_train_floats": (_i64, [_P]),
+            "orc_dit_train": (_i, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
         }
         for name, (res, args) in protos.items():
             fn = getattr(L, name)
@@ -365,3 +373,98 @@ def bias_grad(dy, M, N):
     out = np.zeros(N, dtype=np.float32)
     lib().orc_bias_grad(_p(dy), _p(out), M, N)
     return out
+
+
+# ---- DiT block backward: kernels.metal:508-612, 827-868, 891-1010; DiT.swift:558-626
+
+def rms_bwd(x, rstd, weight, dy, dweight, rows, cols):
+    """rmsnorm_bwd_dx / rmsnorm_bwd_dw. Returns (dx, dweight + sum)."""
+    x, rstd, weight, dy = _f32(x), _f32(rstd), _f32(weight), _f32(dy)
+    dx = np.zeros(rows * cols, np.float32)
+    dw = np.array(dweight, dtype=np.float32, copy=True).reshape(-1)
+    lib().orc_rms_bwd(_p(x), _p(rstd), _p(weight), _p(dy), _p(dx), _p(dw), rows, cols)
+    return dx, dw
+
+
+def attn_bwd(q, k, v, probs, dout, B, T, H, D):
+    """GPU.attnBwd (GPU.swift:312-322). Returns dq, dk, dv, dprobs, dscores."""
+    q, k, v, probs, dout = (_f32(a) for a in (q, k, v, probs, dout))
+    n, tt = B * T * H * D, B * H * T * T
+    dq, dk, dv = (np.zeros(n, np.float32) for _ in range(3))
+    dp, ds = np.zeros(tt, np.float32), np.zeros(tt, np.float32)
+    lib().orc_attn_bwd(_p(q), _p(k), _p(v), _p(probs), _p(dout), _p(dq), _p(dk), _p(dv), _p(dp), _p(ds),
+                       B, T, H, D)
+    return dq, dk, dv, dp, ds
+
+
+def rope_bwd(dy, cosv, sinv, B, T, H, D):
+    dy, cosv, sinv = _f32(dy), _f32(cosv), _f32(sinv)
+    dx = np.zeros_like(dy)
+    lib().orc_rope_bwd(_p(dy), _p(dx), _p(cosv), _p(sinv), B, T, H, D)
+    return dx
+
+
+def swiglu_bwd(gate, up, dy):
+    gate, up, dy = _f32(gate), _f32(up), _f32(dy)
+    dg, du = np.zeros_like(gate), np.zeros_like(gate)
+    lib().orc_swiglu_bwd(_p(gate), _p(up), _p(dy), _p(dg), _p(du), gate.size)
+    return dg, du
+
+
+def sum_heads(src, B, T, H, D):
+    src = _f32(src)
+    dst = np.zeros(B * T * D, np.float32)
+    lib().orc_sum_heads(_p(src), _p(dst), B, T, H, D)
+    return dst
+
+
+def acc_scale(a, b, s):
+    a = np.array(a, dtype=np.float32, copy=True).reshape(-1)
+    lib().orc_acc_scale(_p(a), _p(_f32(b)), a.size, s)
+    return a
+
+
+def dit_train(cfg: DiTCfg, lin: dict, norms: dict, x0, gy):
+    """One training step of the looped block (forward with saved activations,
+    then DiT.swift:566-626). lin maps each of DIT_LINEARS to an fp32 weight
+    (bits 32) or (codes, scales) (bits 8/4). Returns (xs[loops], dL/dxs[0],
+    weight grads {name: [N*K]}, norm grads {name: [C]})."""
+    c = _CCfg(cfg.B, cfg.T, cfg.C, cfg.F, cfg.H, cfg.D, cfg.loops, cfg.group, cfg.bits,
+              cfg.eps, cfg.theta, cfg.mix)
+    shapes = {"wq": (cfg.C, cfg.C), "wk": (cfg.D, cfg.C), "wv": (cfg.D, cfg.C), "wo": (cfg.C, cfg.C),
+              "wgate": (cfg.F, cfg.C), "wup": (cfg.F, cfg.C), "wdown": (cfg.C, cfg.F)}
+    keep = []
+    W = (ctypes.c_void_p * 7)()
+    Q = (ctypes.c_void_p * 7)()
+    S = (ctypes.c_void_p * 7)()
+    GW = (ctypes.c_void_p * 7)()
+    gw = {}
+    for i, name in enumerate(DIT_LINEARS):
+        if cfg.bits == 32:
+            w = _f32(lin[name]).reshape(-1)
+            keep.append(w)
+            W[i] = w.ctypes.data
+        else:
+            q, s = lin[name]
+            q, s = np.ascontiguousarray(q), _f32(s)
+            keep += [q, s]
+            Q[i], S[i] = q.ctypes.data, s.ctypes.data
+        gw[name] = np.zeros(shapes[name][0] * shapes[name][1], np.float32)
+        GW[i] = gw[name].ctypes.data
+    NR = (ctypes.c_void_p * 5)()
+    GN = (ctypes.c_void_p * 5)()
+    gn = {}
+    for i, name in enumerate(DIT_NORMS):
+        nw = _f32(norms[name])
+        keep.append(nw)
+        NR[i] = nw.ctypes.data
+        gn[name] = np.zeros(cfg.C, np.float32)
+        GN[i] = gn[name].ctypes.data
+    x = np.array(x0, dtype=np.float32, copy=True).reshape(-1)
+    g = np.array(gy, dtype=np.float32, copy=True).reshape(-1)
+    ws = np.zeros(lib().orc_dit_train_floats(ctypes.byref(c)), np.float32)
+    rc = lib().orc_dit_train(ctypes.byref(c), ctypes.cast(W, _P), ctypes.cast(Q, _P), ctypes.cast(S, _P),
+                             ctypes.cast(NR, _P), _p(x), _p(g), ctypes.cast(GW, _P), ctypes.cast(GN, _P), _p(ws))
+    if rc != 0:
+        raise ValueError("bad DiT config")
+    return x, g, gw, gn
