@@ -356,6 +356,39 @@ def bench_c3(b: Bench, reps: int) -> dict:
             "note": "launch/latency-bound: ~2.3 GFLOP and ~0.6 MB of weights per forward"}
 
 
+def bench_c3_train(b: Bench, reps: int) -> dict:
+    """One training step of the c3 block (weights as in bench_c3): the forward
+    that saves every loop's activations, then the block backward (int8 STE:
+    dX through the codes, dW into fp32 gradients) from dL/dxs[4] ~N(0,1e-2).
+    Flop: the forward's, plus dX and dW of every linear and the four
+    attention backward products (3x the forward)."""
+    dgm = b.dgm
+    cfg = dgm.DiTConfig()
+    w = {n: b.randn(N * K, 0.02) for n, (N, K) in cfg.linear_shapes().items()}
+    for n in dgm.DIT_NORMS:
+        w[n] = b.torch.ones(cfg.C, dtype=b.torch.float32, device="cuda")
+    b.sync()
+    with b.torch.cuda.stream(b.stream):
+        blk = dgm.DiTBlock(b.gpu, cfg, w)
+        blk.zero_grads()
+    x0 = b.randn(cfg.B * cfg.T * cfg.C, 1.0)
+    g0 = b.randn(cfg.B * cfg.T * cfg.C, 1e-2)
+    x, g = x0.clone(), g0.clone()
+
+    def step(i):
+        blk.forward_train(x)
+        blk.backward(g)
+
+    ms = b.time_launches(step, reps)
+    flops = 3 * c3_flops(cfg)
+    tokens = cfg.B * cfg.T
+    return {"kernel": "dit_forward_train + dit_backward (4 loops)", "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
+            "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
+            "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
+            "note": "launch/latency-bound; x and dL/dx are reused in place across the timed steps"}
+
+
 def bench_c5(b: Bench, reps: int, bits: int, math_mode: int) -> dict:
     M, N, K, G = 8192, 14336, 4096, 128
     w = b.randn(N * K, 0.02)
@@ -574,6 +607,7 @@ def main() -> int:
         jobs = [
             ("c1_int8_fwd", lambda: bench_c1(b, args.reps)),
             ("c3_dit_fwd", lambda: bench_c3(b, 50)),
+            ("c3_dit_train_step", lambda: bench_c3_train(b, 10)),
             ("quant_i4_14336x4096", lambda: bench_quant(b, 20, 4)),
             ("quant_i8_14336x4096", lambda: bench_quant(b, 20, 8)),
             ("adam_quant_i4_14336x4096", lambda: bench_adam_quant(b, 10, 4)),

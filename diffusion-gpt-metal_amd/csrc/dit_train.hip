@@ -11,9 +11,10 @@
 //  * rms_bwd_dw: one workgroup of 16 waves per 64 columns; wave w sums rows
 //    w, w+16, ... and the 16 partial sums are added in wave order, then added
 //    into dweight (the weight is shared by every loop).
-//  * attention backward: the reference's five passes (dV, dP, softmax
-//    backward, dQ, dK) with the reference's summation order, one lane per
-//    output; bitwise the oracle's.
+//  * attention backward: one workgroup per (batch, head) with the head in
+//    LDS (T and D multiples of 4, (4TD + 2T^2) floats of LDS), or the
+//    reference's five passes with one lane per output; both sum in the
+//    reference's order and are bitwise the oracle's.
 //  * rope_bwd, swiglu_bwd, sum_heads, acc_f, acc_scale_f: elementwise.
 // The block's GEMMs are the library's: dgm_gemmNT / dgm_gemmDX /
 // dgm_gemmDWAcc on the fp32 masters (bits 32, as the reference's DiT) or on
@@ -178,6 +179,111 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dqk_kernel(AttnBwdArgs a) {
     (DQ ? a.dq : a.dk)[idx] = acc * a.scale;
 }
 
+// ---- fused attention backward: one workgroup per (batch, head) -------------------
+// The head's Q, K, V, dO rows and its probability matrix P are staged in LDS
+// once; dV = P^T dO and dP = dO V^T, the softmax backward dS = P (dP - rowdot),
+// then dQ = scale dS K and dK = scale dS^T Q, each as a register-tiled product
+// (4 x 4 outputs per lane) whose sums run over the contraction index in
+// increasing order from +0.0f, the reference kernels' order: bitwise the five
+// separate passes. LDS: (4 T D + 2 T T) floats.
+constexpr int kAbTile = 4;
+
+template <typename FA, typename FB, typename FO>
+__device__ __forceinline__ void tiled_product(int rows, int cols, int kdim, FA A, FB B, FO out) {
+    const int tc = cols / kAbTile;
+    const int ntiles = (rows / kAbTile) * tc;
+    for (int tile = threadIdx.x; tile < ntiles; tile += kThreads) {
+        const int r0 = (tile / tc) * kAbTile, c0 = (tile % tc) * kAbTile;
+        float acc[kAbTile][kAbTile];
+#pragma unroll
+        for (int i = 0; i < kAbTile; ++i)
+#pragma unroll
+            for (int j = 0; j < kAbTile; ++j) acc[i][j] = 0.0f;
+        for (int k = 0; k < kdim; ++k) {
+            float a[kAbTile], b[kAbTile];
+#pragma unroll
+            for (int i = 0; i < kAbTile; ++i) a[i] = A(r0 + i, k);
+#pragma unroll
+            for (int j = 0; j < kAbTile; ++j) b[j] = B(k, c0 + j);
+#pragma unroll
+            for (int i = 0; i < kAbTile; ++i)
+#pragma unroll
+                for (int j = 0; j < kAbTile; ++j) acc[i][j] += a[i] * b[j];
+        }
+#pragma unroll
+        for (int i = 0; i < kAbTile; ++i)
+#pragma unroll
+            for (int j = 0; j < kAbTile; ++j) out(r0 + i, c0 + j, acc[i][j]);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void attn_bwd_fused_kernel(AttnBwdArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int T = a.T, D = a.D, H = a.H;
+    const int b = blockIdx.x / H, h = blockIdx.x % H;
+    float* Q = lds;
+    float* K = Q + T * D;
+    float* V = K + T * D;
+    float* G = V + T * D;     // dO
+    float* P = G + T * D;
+    float* S = P + T * T;     // dP, then dS
+    const int64_t row_stride = int64_t(H) * D;
+    const int64_t head0 = (int64_t(b) * T * H + h) * D;     // [b, 0, h, 0]
+    const int64_t pm0 = (int64_t(b) * H + h) * T * T;         // [b, h, 0, 0]
+    // Stage the head's rows (D % 4 == 0: 16-byte loads) and P.
+    const int d4 = D / 4;
+    for (int i = threadIdx.x; i < T * d4; i += kThreads) {
+        const int t = i / d4, c = (i % d4) * 4;
+        const int64_t off = head0 + t * row_stride + c;
+        *reinterpret_cast<float4*>(Q + t * D + c) = *reinterpret_cast<const float4*>(a.q + off);
+        *reinterpret_cast<float4*>(K + t * D + c) = *reinterpret_cast<const float4*>(a.k + off);
+        *reinterpret_cast<float4*>(V + t * D + c) = *reinterpret_cast<const float4*>(a.v + off);
+        *reinterpret_cast<float4*>(G + t * D + c) = *reinterpret_cast<const float4*>(a.dout + off);
+    }
+    for (int i = threadIdx.x; i < T * T / 4; i += kThreads)
+        reinterpret_cast<float4*>(P)[i] = reinterpret_cast<const float4*>(a.probs + pm0)[i];
+    __syncthreads();
+    // dV[s][d] = sum_t P[t][s] dO[t][d]  (attn_bwd_dv)
+    tiled_product(
+        T, D, T, [&](int s, int t) { return P[t * T + s]; }, [&](int t, int d) { return G[t * D + d]; },
+        [&](int s, int d, float v) { a.dv[head0 + s * row_stride + d] = v; });
+    // dP[t][s] = sum_d dO[t][d] V[s][d]  (attn_bwd_dp)
+    tiled_product(
+        T, T, D, [&](int t, int d) { return G[t * D + d]; }, [&](int d, int s) { return V[s * D + d]; },
+        [&](int t, int s, float v) {
+            S[t * T + s] = v;
+            a.dprobs[pm0 + t * T + s] = v;
+        });
+    __syncthreads();
+    // dS[t][i] = P[t][i] (dP[t][i] - sum_i dP[t][i] P[t][i])  (attn_softmax_bwd)
+    for (int t = threadIdx.x; t < T; t += kThreads) {
+        float dot = 0.0f;
+        for (int i = 0; i < T; ++i) dot += S[t * T + i] * P[t * T + i];
+        for (int i = 0; i < T; ++i) {
+            const float ds = P[t * T + i] * (S[t * T + i] - dot);
+            S[t * T + i] = ds;
+            a.dscores[pm0 + t * T + i] = ds;
+        }
+    }
+    __syncthreads();
+    // dQ[t][d] = scale * sum_s dS[t][s] K[s][d]  (attn_bwd_dq)
+    tiled_product(
+        T, D, T, [&](int t, int s) { return S[t * T + s]; }, [&](int s, int d) { return K[s * D + d]; },
+        [&](int t, int d, float v) { a.dq[head0 + t * row_stride + d] = v * a.scale; });
+    // dK[s][d] = scale * sum_t dS[t][s] Q[t][d]  (attn_bwd_dk)
+    tiled_product(
+        T, D, T, [&](int s, int t) { return S[t * T + s]; }, [&](int t, int d) { return Q[t * D + d]; },
+        [&](int s, int d, float v) { a.dk[head0 + s * row_stride + d] = v * a.scale; });
+}
+
+size_t attn_bwd_fused_lds(int T, int D) { return (size_t(4) * T * D + size_t(2) * T * T) * sizeof(float); }
+
+bool attn_bwd_fused_ok(const AttnBwdArgs& a) {
+    return a.T % 4 == 0 && a.D % 4 == 0 && attn_bwd_fused_lds(a.T, a.D) <= 160 * 1024 &&
+           dgm::aligned(a.q, 16) && dgm::aligned(a.k, 16) && dgm::aligned(a.v, 16) && dgm::aligned(a.dout, 16) &&
+           dgm::aligned(a.probs, 16);
+}
+
 // ---- rope_bwd (metal/kernels.metal:891-909) --------------------------------------
 __global__ __launch_bounds__(kThreads) void rope_bwd_kernel(const float* __restrict__ dy, float* __restrict__ dx,
                                                             const float* __restrict__ cosv,
@@ -249,6 +355,16 @@ int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w
 int launch_attn_bwd(dgm_gpu* g, const AttnBwdArgs& a) {
     const int64_t n = int64_t(a.B) * a.T * a.H * a.D, tt = int64_t(a.B) * a.H * a.T * a.T;
     if (n == 0) return DGM_OK;
+    if (attn_bwd_fused_ok(a)) {
+        const size_t lds = attn_bwd_fused_lds(a.T, a.D);
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_bwd_fused_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "attn_bwd: cannot reserve %zu bytes of LDS: %s", lds,
+                             hipGetErrorString(e));
+        hipLaunchKernelGGL(attn_bwd_fused_kernel, dim3(unsigned(a.B * a.H)), dim3(kThreads), lds, g->stream, a);
+        return dgm::check_launch(g, "attn_bwd");
+    }
     hipLaunchKernelGGL(attn_bwd_dv_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a);
     hipLaunchKernelGGL(attn_bwd_dp_kernel, dim3(blocks_for(tt)), dim3(kThreads), 0, g->stream, a);
     hipLaunchKernelGGL(attn_softmax_bwd_kernel, dim3(blocks_for(int64_t(a.B) * a.H * a.T)), dim3(kThreads), 0,
