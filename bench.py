@@ -3,11 +3,13 @@
 Headline ("c2"): one step = the int4 group-quant
 linear forward plus its STE backward on the DiT down-projection shape,
 X[512,768] ~ N(0,1), W[192,768] ~ N(0,0.02) int4 G=32, dY ~ N(0,1e-3):
-    Y  = X deq(W)^T   (gemm_nt_i4)
-    dX = dY deq(W)    (gemm_dx_i4)
-    dW = dY^T X       (gemm_dw)
+    Y  = X deq(W)^T   (gemmNT, gemm_nt_i4)
+    dW = dY^T X       (gemmBwd: the reference's gemmDW + gemmDX pair,
+    dX = dY deq(W)     one launch, bitwise the two calls)
 Inputs are resident in HBM before timing; the weights are quantized once
 before the timed region. value = algorithmic flop of the step / step time.
+The per-kernel times of the separate gemm_dx_i4 and gemm_dw calls are
+reported beside it.
 
 Every GPU timing replays a captured HIP graph of the launches (through
 torch.cuda.CUDAGraph), so host-side call overhead never leaks into kernel
@@ -168,6 +170,7 @@ def c2_setup(b: Bench):
     g = b.gpu
     return {
         "gemm_nt_i4": lambda i: g.gemmNT(4, None, q, s, x, None, y, M, N, K, G),
+        "gemm_bwd_i4": lambda i: g.gemmBwd(4, None, q, s, dy, x, dx, dw, M, N, K, G),
         "gemm_dx_i4": lambda i: g.gemmDX(4, None, q, s, dy, dx, M, N, K, G),
         "gemm_dw": lambda i: g.gemmDW(dy, x, dw, M, N, K),
     }
@@ -181,7 +184,8 @@ def c2_bytes() -> dict:
     M, N, K, G = C2["M"], C2["N"], C2["K"], C2["G"]
     q, s = N * K // 2, N * (K // G) * 4
     return {"gemm_nt_i4": q + s + 4 * (M * K + M * N), "gemm_dx_i4": q + s + 4 * (M * N + M * K),
-            "gemm_dw": 4 * (M * K + M * N + N * K)}
+            "gemm_dw": 4 * (M * K + M * N + N * K),
+            "gemm_bwd_i4": q + s + 4 * (M * N + M * K + M * K + N * K)}
 
 
 def cpu_baseline_c2(budget_s: float = 12.0) -> dict:
@@ -544,7 +548,7 @@ def main() -> int:
     # -- headline step ----------------------------------------------------------
     log("[bench] c2 step setup")
     kern = c2_setup(b)
-    order = ["gemm_nt_i4", "gemm_dx_i4", "gemm_dw"]
+    order = ["gemm_nt_i4", "gemm_bwd_i4"]
 
     def step(i):
         for k in order:
@@ -564,12 +568,13 @@ def main() -> int:
     del steps, warm
     log(f"[bench] c2 step {ms_step * 1e3:.2f} us wall, {gpu_ms_step * 1e3:.2f} us on the stream")
 
-    per_kernel = {k: b.time_launches(kern[k], args.reps) for k in order}
-    dom = max(per_kernel, key=per_kernel.get)
-    flops_k = 2 * C2["M"] * C2["N"] * C2["K"]
+    per_kernel = {k: b.time_launches(kern[k], args.reps) for k in order + ["gemm_dx_i4", "gemm_dw"]}
+    dom = max(order, key=per_kernel.get)
+    gemm_flop = 2 * C2["M"] * C2["N"] * C2["K"]
+    flops_k = 2 * gemm_flop if dom == "gemm_bwd_i4" else gemm_flop
     # HIP kernel behind each entry point at the c2 shape (names as rocprofv3 prints them).
     device_kernel = {"gemm_nt_i4": "gemm_fwd_lds_kernel<4, 4>", "gemm_dx_i4": "gemm_dx_lds_kernel<4>",
-                     "gemm_dw": "gemm_dw_pair_kernel"}
+                     "gemm_dw": "gemm_dw_pair_kernel", "gemm_bwd_i4": "gemm_bwd_pair_kernel<4>"}
     roof = roofline(flops_k / per_kernel[dom] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
                     traffic_for("c2", device_kernel[dom]))
     roof["kernel"] = dom
@@ -593,7 +598,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (torch CPU generator, seed 1234: X~N(0,1), W~N(0,0.02), dY~N(0,1e-3))",
-        "config": {"workload": "c2: int4 group-quant linear fwd + STE bwd (gemm_nt_i4, gemm_dx_i4, gemm_dw)",
+        "config": {"workload": "c2: int4 group-quant linear fwd + STE bwd (gemmNT; gemmBwd = gemmDW + gemmDX "
+                               "in one launch)",
                    "M": C2["M"], "K": C2["K"], "N": C2["N"], "group": C2["G"], "bits": 4,
                    "parallelism": "single GPU", "timing": "one HIP graph of the timed steps"},
         "GBps": round(sum(c2_bytes().values()) / (ms_step * 1e-3) / 1e9, 2),

@@ -147,6 +147,7 @@ PROTOTYPES = {
     "dgm_gemmDX": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmDW": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
     "dgm_gemmDWAcc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "dgm_gemmBwd": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I]),
     "dgm_rmsFwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _F]),
     "dgm_ropeFwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_repeatHeads": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64]),

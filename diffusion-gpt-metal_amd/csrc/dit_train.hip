@@ -16,8 +16,8 @@
 //    reference's five passes with one lane per output; both sum in the
 //    reference's order and are bitwise the oracle's.
 //  * rope_bwd, swiglu_bwd, sum_heads, acc_f, acc_scale_f: elementwise.
-// The block's GEMMs are the library's: dgm_gemmNT / dgm_gemmDX /
-// dgm_gemmDWAcc on the fp32 masters (bits 32, as the reference's DiT) or on
+// The block's GEMMs are the library's: dgm_gemmNT and dgm_gemmBwd (gemmDWAcc +
+// gemmDX in one launch) on the fp32 masters (bits 32, as the reference's DiT) or on
 // the group-quantized codes (bits 8 / 4: forward on the codes, dX through the
 // dequantized codes, dW into the fp32 master gradient: the straight-through
 // estimator of src/GPT.swift's backward).
@@ -666,32 +666,27 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
     const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, nC = M * C, nKV = M * KV;
     const float mix = c->mix;
-    // dX through the linear (fp32 master for bits 32, dequantized codes for
-    // bits 8 / 4) and dW accumulated into its fp32 gradient.
-    auto dx = [&](const dgm_dit_linear& Lw, const float* dy, float* out, int64_t N, int64_t K) {
-        return dgm_gemmDX(g, bits, Lw.w, Lw.q, Lw.scale, dy, out, M, N, K, bits == 32 ? 8 : G);
-    };
-    auto dw = [&](const float* dy, const float* in, float* dW, int64_t N, int64_t K) {
-        return dgm_gemmDWAcc(g, dy, in, dW, M, N, K);
+    // dW accumulated into the fp32 gradient and dX through the linear (fp32
+    // master for bits 32, dequantized codes for bits 8 / 4): the reference's
+    // gemmDWAcc + gemmDX pair, one launch where the shapes allow.
+    auto bwd = [&](const dgm_dit_linear& Lw, const float* dy, const float* in, float* out, float* dW, int64_t N,
+                   int64_t K) {
+        return dgm_gemmBwd(g, bits, Lw.w, Lw.q, Lw.scale, dy, in, out, dW, M, N, K, bits == 32 ? 8 : G, 1);
     };
     float *t1 = S[B_T1], *t2 = S[B_T2], *dln = S[B_DLN];
     DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
     for (int l = c->loops - 1; l >= 0; --l) {
         DGM_TRY(dgm_rmsBwd(g, A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, M, C, c->eps));
         DGM_TRY(dgm_rmsBwd(g, A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, M, C, c->eps));
-        DGM_TRY(dw(t2, A(l, A_SW), gr->wdown, C, F));
-        DGM_TRY(dx(w->wdown, t2, S[B_DSW], C, F));
+        DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
         DGM_TRY(dgm_swigluBwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
-        DGM_TRY(dw(S[B_DG], A(l, A_LN2), gr->wgate, F, C));
-        DGM_TRY(dx(w->wgate, S[B_DG], t2, F, C));
-        DGM_TRY(dw(S[B_DU], A(l, A_LN2), gr->wup, F, C));
-        DGM_TRY(dx(w->wup, S[B_DU], dln, F, C));
+        DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, F, C));
+        DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));
         DGM_TRY(dgm_acc(g, t2, dln, nC));
         DGM_TRY(dgm_rmsBwd(g, A(l, A_MID), A(l, A_R2), w->n2, t2, dln, gr->n2, M, C, c->eps));
         DGM_TRY(dgm_acc(g, t1, dln, nC));
         DGM_TRY(dgm_rmsBwd(g, A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, M, C, c->eps));
-        DGM_TRY(dw(t2, A(l, A_AV), gr->wo, C, C));
-        DGM_TRY(dx(w->wo, t2, S[B_DAV], C, C));
+        DGM_TRY(bwd(w->wo, t2, A(l, A_AV), S[B_DAV], gr->wo, C, C));
         DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK], S[B_DV],
                             S[B_DPROBS], S[B_DSCORES], B, T, H, D));
         DGM_TRY(dgm_sumHeads(g, S[B_DK], S[B_DK1], B, T, H, D));
@@ -705,13 +700,10 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(dgm_mix(g, S[B_DV1], S[B_DV1], S[B_DVPRE], nKV, 1.0f - mix, 0.0f));
             DGM_TRY(dgm_accScale(g, S[B_DFIRST], S[B_DV1], nKV, mix));
         }
-        DGM_TRY(dw(S[B_QPRE], A(l, A_LN1), gr->wq, C, C));
-        DGM_TRY(dx(w->wq, S[B_QPRE], t2, C, C));
-        DGM_TRY(dw(S[B_KPRE], A(l, A_LN1), gr->wk, KV, C));
-        DGM_TRY(dx(w->wk, S[B_KPRE], dln, KV, C));
+        DGM_TRY(bwd(w->wq, S[B_QPRE], A(l, A_LN1), t2, gr->wq, C, C));
+        DGM_TRY(bwd(w->wk, S[B_KPRE], A(l, A_LN1), dln, gr->wk, KV, C));
         DGM_TRY(dgm_acc(g, t2, dln, nC));
-        DGM_TRY(dw(S[B_DVPRE], A(l, A_LN1), gr->wv, KV, C));
-        DGM_TRY(dx(w->wv, S[B_DVPRE], dln, KV, C));
+        DGM_TRY(bwd(w->wv, S[B_DVPRE], A(l, A_LN1), dln, gr->wv, KV, C));
         DGM_TRY(dgm_acc(g, t2, dln, nC));
         DGM_TRY(dgm_rmsBwd(g, A(l, A_X), A(l, A_R1), w->n1, t2, dln, gr->n1, M, C, c->eps));
         DGM_TRY(dgm_acc(g, t1, dln, nC));

@@ -12,6 +12,8 @@ int gemm_f32_dx(dgm_gpu* g, int bits, const void* W, const float* scale, const f
                 float* dX, const dgm_GemmP* p);
 int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dgm_GemmP* p,
                 bool accumulate);
+int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, const float* dY, const float* X,
+                      float* dX, float* dW, const dgm_GemmP* p, bool accumulate, bool* fused);
 }  // namespace dgm
 
 namespace {
@@ -150,6 +152,43 @@ int dgm_gemmDWAcc(dgm_gpu* g, const float* dy, const float* x, float* dw, int64_
     int rc = make_p(g, "gemmDWAcc", M, N, K, 0, 8, &p);
     if (rc) return rc;
     return dgm_gemm_dw_acc(g, dy, x, dw, &p);
+}
+
+int dgm_gemmBwd(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale, const float* dy,
+                const float* x, float* dx, float* dw, int64_t M, int64_t N, int64_t K, int64_t qGroup,
+                int accumulate) {
+    // GPU.gemmDW (or gemmDWAcc) then GPU.gemmDX on the same dY, as the
+    // reference's backward issues them (src/GPT.swift:374-376, 384-420).
+    if (!g) return DGM_ERR_ARG;
+    if (bits != 32 && bits != 8 && bits != 4)
+        return dgm::fail(g, DGM_ERR_BITS, "gemmBwd: unsupported bits %lld", (long long)bits);
+    dgm_GemmP p;
+    int rc = make_p(g, "gemmBwd", M, N, K, 0, qGroup, &p);
+    if (rc) return rc;
+    const char* name = bits == 32 ? "gemm_bwd_f32" : (bits == 8 ? "gemm_bwd_i8" : "gemm_bwd_i4");
+    rc = dgm::enter(g, name);
+    if (rc) return rc;
+    rc = dgm::gemm_check_sizes(g, name, &p, int(bits));
+    if (rc) return rc;
+    const void* wt = bits == 32 ? static_cast<const void*>(w) : q;
+    if (p.M > 0 && p.N > 0 && p.K > 0) {
+        if (!dx || !dw || !dy || !x || !wt || (bits != 32 && !scale))
+            return dgm::fail(g, DGM_ERR_ARG, "gemmBwd: null buffer");
+        bool fused = false;
+        rc = dgm::gemm_f32_bwd_pair(g, int(bits), wt, scale, dy, x, dx, dw, &p, accumulate != 0, &fused);
+        if (rc) return rc;
+        if (fused) {
+            DGM_LAUNCH_CHECK(g, name);
+            return DGM_OK;
+        }
+    }
+    rc = accumulate ? dgm_gemm_dw_acc(g, dy, x, dw, &p) : dgm_gemm_dw(g, dy, x, dw, &p);
+    if (rc) return rc;
+    switch (bits) {
+        case 32: return dgm_gemm_dx_f32(g, w, dy, dx, &p);
+        case 8: return dgm_gemm_dx_i8(g, static_cast<const int8_t*>(q), scale, dy, dx, &p);
+        default: return dgm_gemm_dx_i4(g, static_cast<const uint8_t*>(q), scale, dy, dx, &p);
+    }
 }
 
 }  // extern "C"

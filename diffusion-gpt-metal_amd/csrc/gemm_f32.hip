@@ -636,10 +636,12 @@ void launch_fwd_lds(const GemmArgs& a, int num_cus, hipStream_t st) {
 // contraction indices are one 16-byte LDS read and the 16 rows an MFMA operand
 // touches fall in distinct banks. Contraction order inside a 64-wide stage is
 // the same permutation for both operands (lane q takes 16q .. 16q+15).
+// Body of one dX tile; `blk` is the workgroup's index within its own grid
+// (dealt round-robin to the 8 XCDs), sm4 its LDS (dx_lds_bytes(N)).
 template <int BITS>
-__global__ __launch_bounds__(kThreads) void gemm_dx_lds_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
-    extern __shared__ __align__(16) float4 sm4[];
-    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+__device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int tiles_j, int per_xcd, int blk,
+                                            float4* sm4) {
+    const int t = (blk & 7) * per_xcd + (blk >> 3);
     if (t >= tiles_i * tiles_j) return;
     const int ti = t / tiles_j, tj = t - ti * tiles_j;
     const int i0 = ti * 16, k0 = tj * 64;
@@ -730,6 +732,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dx_lds_kernel(GemmArgs a, int t
     }
 }
 
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void gemm_dx_lds_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    extern __shared__ __align__(16) float4 sm4[];
+    dx_lds_tile<BITS>(a, tiles_i, tiles_j, per_xcd, int(blockIdx.x), sm4);
+}
+
 size_t dx_lds_bytes(int N) { return size_t(16) * N * 4 + size_t(64) * (N + 4) * 4; }
 
 // N % 64 == 0 and N <= 448 (dY block and the transposed strip stay in LDS),
@@ -769,9 +777,10 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
 // m = m0 + q + 4 s. Wave partials are reduced through LDS in a fixed order.
 constexpr int DWP_CH = 8;   // 16-row chunks per wave and round
 
-__global__ __launch_bounds__(kThreads) void gemm_dw_pair_kernel(GemmArgs a, int tiles_n, int tiles_k, int per_xcd) {
-    __shared__ float part[4][2][16][16];
-    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+// Body of one dW tile; `blk` as in dx_lds_tile, part: 8 KB of LDS.
+__device__ __forceinline__ void dw_pair_tile(const GemmArgs& a, int tiles_n, int tiles_k, int per_xcd, int blk,
+                                             float (*part)[2][16][16]) {
+    const int t = (blk & 7) * per_xcd + (blk >> 3);
     if (t >= tiles_n * tiles_k) return;
     const int tk = t / tiles_n, tn = t - tk * tiles_n;
     const int n0 = tn * 32, k0 = tk * 16;
@@ -828,6 +837,28 @@ __global__ __launch_bounds__(kThreads) void gemm_dw_pair_kernel(GemmArgs a, int 
         float* o = a.out + size_t(i) * K + k;
         if (a.accumulate) *o += v;
         else *o = v;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void gemm_dw_pair_kernel(GemmArgs a, int tiles_n, int tiles_k, int per_xcd) {
+    __shared__ float part[4][2][16][16];
+    dw_pair_tile(a, tiles_n, tiles_k, per_xcd, int(blockIdx.x), part);
+}
+
+// ---- the STE backward pair in one launch ------------------------------------------
+// Workgroups [0, 8*per_x) compute dX tiles (dx_lds_tile), the rest dW tiles
+// (dw_pair_tile): the two GEMMs share no output and only read dY, so they run
+// side by side instead of back to back. Each tile is computed exactly as by
+// its own kernel.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void gemm_bwd_pair_kernel(GemmArgs ax, int ti, int tj, int per_x, GemmArgs aw,
+                                                                 int tn, int tk, int per_w) {
+    extern __shared__ __align__(16) float4 sm4[];
+    const int nx = 8 * per_x;
+    if (int(blockIdx.x) < nx) {
+        dx_lds_tile<BITS>(ax, ti, tj, per_x, int(blockIdx.x), sm4);
+    } else {
+        dw_pair_tile(aw, tn, tk, per_w, int(blockIdx.x) - nx, reinterpret_cast<float (*)[2][16][16]>(sm4));
     }
 }
 
@@ -968,6 +999,53 @@ int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dg
     }
     if (deep_ok<MODE_DW>(a, 32, false)) launch_deep<MODE_DW, 32>(a, g->num_cus, g->stream);
     else launch_gemm<MODE_DW, 32>(a, false, g->num_cus, g->stream);
+    return DGM_OK;
+}
+
+// dX and dW of one linear as a single launch (gemm_bwd_pair_kernel) when both
+// shapes take the LDS dX kernel and the paired-column dW kernel; *fused tells
+// the caller whether it ran (else it runs gemm_f32_dx and gemm_f32_dw).
+int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, const float* dY, const float* X,
+                      float* dX, float* dW, const dgm_GemmP* p, bool accumulate, bool* fused) {
+    *fused = false;
+    GemmArgs ax{};
+    ax.A = dY; ax.B = W; ax.scale = scale; ax.out = dX;
+    ax.M = p->M; ax.N = p->N; ax.K = p->K;
+    ax.rows = p->M; ax.cols = p->K; ax.red = p->N;
+    ax.G = bits == 32 ? 1 : int(p->qGroup);
+    ax.groups = bits == 32 ? 0 : int(p->K / p->qGroup);
+    GemmArgs aw{};
+    aw.A = dY; aw.B = X; aw.out = dW;
+    aw.M = p->M; aw.N = p->N; aw.K = p->K;
+    aw.rows = p->N; aw.cols = p->K; aw.red = p->M;
+    aw.G = 1; aw.groups = 0;
+    aw.accumulate = accumulate;
+    if (!dx_lds_ok(ax, bits, dY, W) || !dw_pair_ok(aw, dY)) return DGM_OK;
+    const size_t lds = dx_lds_bytes(ax.N);   // >= the 8 KB the dW tiles use (N >= 64)
+    const void* kern = bits == 32 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<32>)
+                       : bits == 8 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<8>)
+                                   : reinterpret_cast<const void*>(gemm_bwd_pair_kernel<4>);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "gemm_bwd: cannot reserve %zu bytes of LDS: %s", lds,
+                             hipGetErrorString(e));
+    }
+    const int ti = int(dgm::ceil_div(ax.rows, 16)), tj = int(dgm::ceil_div(ax.K, 64));
+    const int per_x = int((int64_t(ti) * tj + 7) / 8);
+    const int tn = int(dgm::ceil_div(aw.N, 32)), tk = int(dgm::ceil_div(aw.K, 16));
+    const int per_w = int((int64_t(tn) * tk + 7) / 8);
+    const dim3 grid(unsigned(per_x + per_w) * 8u);
+    if (bits == 32)
+        hipLaunchKernelGGL(gemm_bwd_pair_kernel<32>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk,
+                           per_w);
+    else if (bits == 8)
+        hipLaunchKernelGGL(gemm_bwd_pair_kernel<8>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk,
+                           per_w);
+    else
+        hipLaunchKernelGGL(gemm_bwd_pair_kernel<4>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk,
+                           per_w);
+    *fused = true;
     return DGM_OK;
 }
 

@@ -121,6 +121,13 @@ class GPU:
     def gemmDWAcc(self, dy, x, dw, M: int, N: int, K: int) -> None:
         self._check(self.lib.dgm_gemmDWAcc(self.h, _ptr(dy), _ptr(x), _ptr(dw), M, N, K))
 
+    def gemmBwd(self, bits: int, w, q, scale, dy, x, dx, dw, M: int, N: int, K: int, qGroup: int,
+                accumulate: bool = False) -> None:
+        """gemmDW (or gemmDWAcc) then gemmDX on the same dY, in one launch
+        where the shapes allow (bitwise the two calls)."""
+        self._check(self.lib.dgm_gemmBwd(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(dy), _ptr(x), _ptr(dx),
+                                         _ptr(dw), M, N, K, qGroup, 1 if accumulate else 0))
+
     # -- DiT block wrappers (src/GPU.swift:211-410) ---------------------------
     def rmsFwd(self, x, y, rstd, weight, rows: int, cols: int, eps: float) -> None:
         self._check(self.lib.dgm_rmsFwd(self.h, _ptr(x), _ptr(y), _ptr(rstd), _ptr(weight), rows, cols, eps))

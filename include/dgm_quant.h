@@ -150,6 +150,15 @@ int dgm_gemmDW(dgm_gpu* g, const float* dy, const float* x, float* dw,
 int dgm_gemmDWAcc(dgm_gpu* g, const float* dy, const float* x, float* dw,
                   int64_t M, int64_t N, int64_t K);
 
+/* GPU.gemmDW (accumulate = 0) or GPU.gemmDWAcc (accumulate != 0) followed by
+ * GPU.gemmDX with the same dY: the pair the reference's backward issues back
+ * to back for every linear (src/GPT.swift:374-376, 384-420). One launch when
+ * the shapes allow (the dX and dW tiles run side by side), else the two
+ * calls; either way dx and dw are bitwise what the two calls produce. */
+int dgm_gemmBwd(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale,
+                const float* dy, const float* x, float* dx, float* dw, int64_t M, int64_t N,
+                int64_t K, int64_t qGroup, int accumulate);
+
 /* ---- looped DiT block forward: the non-GEMM wrappers it calls -------------
  * Same names, buffer order and sizes as the Swift wrappers; fp32 buffers in
  * device memory. Layouts: activations [B,T,H,D] (rows of H*D), scores/probs

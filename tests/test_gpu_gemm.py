@@ -261,3 +261,47 @@ def test_gemm_error_paths(gpu, dgm):
     gpu.gemmDW(t, t, t, 0, 4, 16)                           # M = 0: dW = 0
     gpu.end()
     assert float(t[:64].abs().sum()) == 0.0
+
+
+# ---- gemmBwd: the gemmDW(+Acc) / gemmDX pair in one launch ---------------------
+
+BWD_SHAPES = [(512, 192, 768, 32), (512, 768, 192, 32), (512, 48, 192, 32), (512, 192, 192, 32),
+              (64, 64, 128, 16), (128, 448, 64, 32),      # fused (N % 64 == 0, N <= 448, M % 64 == 0)
+              (512, 768, 768, 32), (100, 192, 768, 32), (64, 62, 128, 16)]   # the two calls
+
+
+@pytest.mark.parametrize("bits", [32, 8, 4])
+@pytest.mark.parametrize("M,N,K,G", BWD_SHAPES)
+@pytest.mark.parametrize("acc", [False, True])
+def test_gemm_bwd_is_the_pair(gpu, orc, bits, M, N, K, G, acc):
+    import torch
+    rng = np.random.default_rng(M + N + K + bits)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (0.02 * rng.standard_normal(N * K)).astype(np.float32)
+    dy = (1e-3 * rng.standard_normal(M * N)).astype(np.float32)
+    dw0 = rng.standard_normal(N * K).astype(np.float32)
+    xd, wd, dyd = to_dev(x), to_dev(w), to_dev(dy)
+    q = s = None
+    if bits != 32:
+        q, s = quantize_dev(gpu, wd, N, K, G, bits)
+    dx1, dx2 = (torch.zeros(M * K, device="cuda") for _ in range(2))
+    dw1, dw2 = to_dev(dw0), to_dev(dw0)
+    gpu.begin()
+    gpu.gemmBwd(bits, wd, q, s, dyd, xd, dx1, dw1, M, N, K, G, accumulate=acc)
+    name = gpu.lastKernel
+    (gpu.gemmDWAcc if acc else gpu.gemmDW)(dyd, xd, dw2, M, N, K)
+    gpu.gemmDX(bits, wd, q, s, dyd, dx2, M, N, K, G)
+    gpu.end()
+    assert np.array_equal(from_dev(dx1).view(np.uint32), from_dev(dx2).view(np.uint32))
+    assert np.array_equal(from_dev(dw1).view(np.uint32), from_dev(dw2).view(np.uint32))
+    cpu = 32 if bits == 4 else 16 if bits == 8 else 4    # codes per 16-byte unit of the LDS dX tile
+    fused = N % 64 == 0 and N <= 448 and M % 64 == 0 and K % cpu == 0 and (bits == 32 or G % cpu == 0)
+    assert (name == {32: "gemm_bwd_f32", 8: "gemm_bwd_i8", 4: "gemm_bwd_i4"}[bits]) == fused, name
+    # and against float64 products of the dequantized weights
+    wq = w if bits == 32 else orc.dequant(host_codes(q), from_dev(s), N, K, G, bits)
+    wq = wq.reshape(N, K).astype(np.float64)
+    ref_dx = dy.reshape(M, N).astype(np.float64) @ wq
+    ref_dw = dy.reshape(M, N).astype(np.float64).T @ x.reshape(M, K).astype(np.float64)
+    assert rel_err(from_dev(dx1), ref_dx.ravel()) <= TOL
+    got_dw = from_dev(dw1).astype(np.float64) - (dw0 if acc else 0.0)
+    assert rel_err(got_dw, ref_dw.ravel()) <= (1e-4 if acc else TOL)
