@@ -180,86 +180,107 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dqk_kernel(AttnBwdArgs a) {
 }
 
 // ---- fused attention backward: one workgroup per (batch, head) -------------------
-// The head's Q, K, V, dO rows and its probability matrix P are staged in LDS
-// once; dV = P^T dO and dP = dO V^T, the softmax backward dS = P (dP - rowdot),
-// then dQ = scale dS K and dK = scale dS^T Q, each as a register-tiled product
-// (4 x 4 outputs per lane) whose sums run over the contraction index in
-// increasing order from +0.0f, the reference kernels' order: bitwise the five
-// separate passes. LDS: (4 T D + 2 T T) floats.
-constexpr int kAbTile = 4;
+// The head's Q, K, dO rows, V transposed and its probability matrix P are
+// staged in LDS once; dV = P^T dO and dP = dO V^T, the softmax backward
+// dS = P (dP - rowdot), then dQ = scale dS K and dK = scale dS^T Q. 16 waves
+// (four per SIMD, so one wave's LDS latency hides behind the others' work);
+// each product gives a lane 2 x 2 outputs and runs its contraction loop
+// unrolled by 4. Every sum runs over the contraction index in increasing
+// order from +0.0f, the reference kernels' order, including the softmax
+// row dot (lanes form the products, one lane adds them in order): bitwise
+// the five separate passes. LDS: (4 T D + 2 T T) floats.
+constexpr int kAbThreads = 1024;
 
+// out(r0, c0, acc) receives rows r0, r0+1 x columns c0, c0+1; A2(r, k) the
+// A values of rows r, r+1 at k; B2(k, c) the B values of columns c, c+1.
 template <typename FA, typename FB, typename FO>
-__device__ __forceinline__ void tiled_product(int rows, int cols, int kdim, FA A, FB B, FO out) {
-    const int tc = cols / kAbTile;
-    const int ntiles = (rows / kAbTile) * tc;
-    for (int tile = threadIdx.x; tile < ntiles; tile += kThreads) {
-        const int r0 = (tile / tc) * kAbTile, c0 = (tile % tc) * kAbTile;
-        float acc[kAbTile][kAbTile];
+__device__ __forceinline__ void tiled_product(int rows, int cols, int kdim, FA A2, FB B2, FO out) {
+    const int tc = cols / 2;
+    const int ntiles = (rows / 2) * tc;
+    for (int tile = threadIdx.x; tile < ntiles; tile += kAbThreads) {
+        const int r0 = (tile / tc) * 2, c0 = (tile % tc) * 2;
+        float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
+        for (int k = 0; k < kdim; k += 4) {
+            float2 a[4], b[4];
 #pragma unroll
-        for (int i = 0; i < kAbTile; ++i)
+            for (int u = 0; u < 4; ++u) {
+                a[u] = A2(r0, k + u);
+                b[u] = B2(k + u, c0);
+            }
 #pragma unroll
-            for (int j = 0; j < kAbTile; ++j) acc[i][j] = 0.0f;
-        for (int k = 0; k < kdim; ++k) {
-            float a[kAbTile], b[kAbTile];
-#pragma unroll
-            for (int i = 0; i < kAbTile; ++i) a[i] = A(r0 + i, k);
-#pragma unroll
-            for (int j = 0; j < kAbTile; ++j) b[j] = B(k, c0 + j);
-#pragma unroll
-            for (int i = 0; i < kAbTile; ++i)
-#pragma unroll
-                for (int j = 0; j < kAbTile; ++j) acc[i][j] += a[i] * b[j];
+            for (int u = 0; u < 4; ++u) {
+                a00 += a[u].x * b[u].x;
+                a01 += a[u].x * b[u].y;
+                a10 += a[u].y * b[u].x;
+                a11 += a[u].y * b[u].y;
+            }
         }
-#pragma unroll
-        for (int i = 0; i < kAbTile; ++i)
-#pragma unroll
-            for (int j = 0; j < kAbTile; ++j) out(r0 + i, c0 + j, acc[i][j]);
+        out(r0, c0, a00, a01, a10, a11);
     }
 }
 
-__global__ __launch_bounds__(kThreads) void attn_bwd_fused_kernel(AttnBwdArgs a) {
+__global__ __launch_bounds__(kAbThreads) void attn_bwd_fused_kernel(AttnBwdArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int T = a.T, D = a.D, H = a.H;
     const int b = blockIdx.x / H, h = blockIdx.x % H;
-    float* Q = lds;
-    float* K = Q + T * D;
-    float* V = K + T * D;
-    float* G = V + T * D;     // dO
-    float* P = G + T * D;
-    float* S = P + T * T;     // dP, then dS
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* Q = lds;            // [T][D]
+    float* K = Q + T * D;      // [T][D]
+    float* Vt = K + T * D;     // [D][T]
+    float* G = Vt + T * D;     // dO [T][D]
+    float* P = G + T * D;      // [T][T]
+    float* S = P + T * T;      // dP, then dS [T][T]
     const int64_t row_stride = int64_t(H) * D;
     const int64_t head0 = (int64_t(b) * T * H + h) * D;     // [b, 0, h, 0]
     const int64_t pm0 = (int64_t(b) * H + h) * T * T;         // [b, h, 0, 0]
-    // Stage the head's rows (D % 4 == 0: 16-byte loads) and P.
+    // Stage the head's rows (D % 4 == 0: 16-byte loads), V transposed, and P.
     const int d4 = D / 4;
-    for (int i = threadIdx.x; i < T * d4; i += kThreads) {
+    for (int i = threadIdx.x; i < T * d4; i += kAbThreads) {
         const int t = i / d4, c = (i % d4) * 4;
         const int64_t off = head0 + t * row_stride + c;
         *reinterpret_cast<float4*>(Q + t * D + c) = *reinterpret_cast<const float4*>(a.q + off);
         *reinterpret_cast<float4*>(K + t * D + c) = *reinterpret_cast<const float4*>(a.k + off);
-        *reinterpret_cast<float4*>(V + t * D + c) = *reinterpret_cast<const float4*>(a.v + off);
         *reinterpret_cast<float4*>(G + t * D + c) = *reinterpret_cast<const float4*>(a.dout + off);
+        const float4 v = *reinterpret_cast<const float4*>(a.v + off);
+        Vt[(c + 0) * T + t] = v.x;
+        Vt[(c + 1) * T + t] = v.y;
+        Vt[(c + 2) * T + t] = v.z;
+        Vt[(c + 3) * T + t] = v.w;
     }
-    for (int i = threadIdx.x; i < T * T / 4; i += kThreads)
+    for (int i = threadIdx.x; i < T * T / 4; i += kAbThreads)
         reinterpret_cast<float4*>(P)[i] = reinterpret_cast<const float4*>(a.probs + pm0)[i];
     __syncthreads();
+    auto f2 = [](const float* p) { return *reinterpret_cast<const float2*>(p); };
+    auto col2 = [](const float* p, int stride) { return make_float2(p[0], p[stride]); };
+    auto store2 = [&](float* base, int r0, int c0, float a00, float a01, float a10, float a11) {
+        *reinterpret_cast<float2*>(base + head0 + r0 * row_stride + c0) = make_float2(a00, a01);
+        *reinterpret_cast<float2*>(base + head0 + (r0 + 1) * row_stride + c0) = make_float2(a10, a11);
+    };
     // dV[s][d] = sum_t P[t][s] dO[t][d]  (attn_bwd_dv)
     tiled_product(
-        T, D, T, [&](int s, int t) { return P[t * T + s]; }, [&](int t, int d) { return G[t * D + d]; },
-        [&](int s, int d, float v) { a.dv[head0 + s * row_stride + d] = v; });
+        T, D, T, [&](int s0, int t) { return f2(P + t * T + s0); }, [&](int t, int d0) { return f2(G + t * D + d0); },
+        [&](int s0, int d0, float a00, float a01, float a10, float a11) { store2(a.dv, s0, d0, a00, a01, a10, a11); });
     // dP[t][s] = sum_d dO[t][d] V[s][d]  (attn_bwd_dp)
     tiled_product(
-        T, T, D, [&](int t, int d) { return G[t * D + d]; }, [&](int d, int s) { return V[s * D + d]; },
-        [&](int t, int s, float v) {
-            S[t * T + s] = v;
-            a.dprobs[pm0 + t * T + s] = v;
+        T, T, D, [&](int t0, int d) { return col2(G + t0 * D + d, D); }, [&](int d, int s0) { return f2(Vt + d * T + s0); },
+        [&](int t0, int s0, float a00, float a01, float a10, float a11) {
+            *reinterpret_cast<float2*>(S + t0 * T + s0) = make_float2(a00, a01);
+            *reinterpret_cast<float2*>(S + (t0 + 1) * T + s0) = make_float2(a10, a11);
+            *reinterpret_cast<float2*>(a.dprobs + pm0 + t0 * T + s0) = make_float2(a00, a01);
+            *reinterpret_cast<float2*>(a.dprobs + pm0 + (t0 + 1) * T + s0) = make_float2(a10, a11);
         });
     __syncthreads();
-    // dS[t][i] = P[t][i] (dP[t][i] - sum_i dP[t][i] P[t][i])  (attn_softmax_bwd)
-    for (int t = threadIdx.x; t < T; t += kThreads) {
+    // dS[t][i] = P[t][i] (dP[t][i] - sum_i dP[t][i] P[t][i])  (attn_softmax_bwd):
+    // one wave per row; lane l holds i = l, l+64, ...; the dot is added in i order.
+    for (int t = wave; t < T; t += kAbThreads / 64) {
         float dot = 0.0f;
-        for (int i = 0; i < T; ++i) dot += S[t * T + i] * P[t * T + i];
-        for (int i = 0; i < T; ++i) {
+        for (int i0 = 0; i0 < T; i0 += 64) {
+            const int i = i0 + lane;
+            const float prod = i < T ? S[t * T + i] * P[t * T + i] : 0.0f;
+            const int n = T - i0 < 64 ? T - i0 : 64;
+            for (int j = 0; j < n; ++j) dot += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prod), j));
+        }
+        for (int i = lane; i < T; i += 64) {
             const float ds = P[t * T + i] * (S[t * T + i] - dot);
             S[t * T + i] = ds;
             a.dscores[pm0 + t * T + i] = ds;
@@ -268,12 +289,16 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_fused_kernel(AttnBwdArgs a)
     __syncthreads();
     // dQ[t][d] = scale * sum_s dS[t][s] K[s][d]  (attn_bwd_dq)
     tiled_product(
-        T, D, T, [&](int t, int s) { return S[t * T + s]; }, [&](int s, int d) { return K[s * D + d]; },
-        [&](int t, int d, float v) { a.dq[head0 + t * row_stride + d] = v * a.scale; });
+        T, D, T, [&](int t0, int s) { return col2(S + t0 * T + s, T); }, [&](int s, int d0) { return f2(K + s * D + d0); },
+        [&](int t0, int d0, float a00, float a01, float a10, float a11) {
+            store2(a.dq, t0, d0, a00 * a.scale, a01 * a.scale, a10 * a.scale, a11 * a.scale);
+        });
     // dK[s][d] = scale * sum_t dS[t][s] Q[t][d]  (attn_bwd_dk)
     tiled_product(
-        T, D, T, [&](int s, int t) { return S[t * T + s]; }, [&](int t, int d) { return Q[t * D + d]; },
-        [&](int s, int d, float v) { a.dk[head0 + s * row_stride + d] = v * a.scale; });
+        T, D, T, [&](int s0, int t) { return f2(S + t * T + s0); }, [&](int t, int d0) { return f2(Q + t * D + d0); },
+        [&](int s0, int d0, float a00, float a01, float a10, float a11) {
+            store2(a.dk, s0, d0, a00 * a.scale, a01 * a.scale, a10 * a.scale, a11 * a.scale);
+        });
 }
 
 size_t attn_bwd_fused_lds(int T, int D) { return (size_t(4) * T * D + size_t(2) * T * T) * sizeof(float); }
@@ -281,7 +306,8 @@ size_t attn_bwd_fused_lds(int T, int D) { return (size_t(4) * T * D + size_t(2) 
 bool attn_bwd_fused_ok(const AttnBwdArgs& a) {
     return a.T % 4 == 0 && a.D % 4 == 0 && attn_bwd_fused_lds(a.T, a.D) <= 160 * 1024 &&
            dgm::aligned(a.q, 16) && dgm::aligned(a.k, 16) && dgm::aligned(a.v, 16) && dgm::aligned(a.dout, 16) &&
-           dgm::aligned(a.probs, 16);
+           dgm::aligned(a.probs, 16) && dgm::aligned(a.dq, 16) && dgm::aligned(a.dk, 16) && dgm::aligned(a.dv, 16) &&
+           dgm::aligned(a.dprobs, 16);
 }
 
 // ---- rope_bwd (metal/kernels.metal:891-909) --------------------------------------
@@ -362,7 +388,7 @@ int launch_attn_bwd(dgm_gpu* g, const AttnBwdArgs& a) {
         if (e != hipSuccess)
             return dgm::fail(g, DGM_ERR_HIP, "attn_bwd: cannot reserve %zu bytes of LDS: %s", lds,
                              hipGetErrorString(e));
-        hipLaunchKernelGGL(attn_bwd_fused_kernel, dim3(unsigned(a.B * a.H)), dim3(kThreads), lds, g->stream, a);
+        hipLaunchKernelGGL(attn_bwd_fused_kernel, dim3(unsigned(a.B * a.H)), dim3(kAbThreads), lds, g->stream, a);
         return dgm::check_launch(g, "attn_bwd");
     }
     hipLaunchKernelGGL(attn_bwd_dv_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, a);
