@@ -14,6 +14,7 @@ from .abi import (DGM_ERR_ARG, DGM_ERR_BITS, DGM_ERR_HIP, DGM_ERR_NOT_BEGUN,
 from .gpu import GPU, Buf, RawBuf
 from .dit import DiTBlock, DiTConfig, rope_tables
 from .train import Param, bias_corrections, grad_norm, optimizer_step, zero_grads
+from .ckpt import load_dit_block, load_gpt, read_tdit, read_tgmt, save_tdit, save_tgmt
 
 __all__ = [
     "GPU", "Buf", "RawBuf", "GemmP", "QuantP", "DgmError", "load_library",
@@ -22,5 +23,6 @@ __all__ = [
     "DGM_MATH_FP32", "DGM_MATH_BF16", "DiTBlock", "DiTConfig", "DiTCfg", "DiTLinear",
     "DiTWeights", "DIT_LINEARS", "DIT_NORMS", "rope_tables", "AdamP", "EmbP", "EmbBwdP",
     "PosP", "BiasP", "ReduceP", "ScaleP", "UnaryP", "Param", "bias_corrections", "grad_norm",
-    "optimizer_step", "zero_grads", "DiTGrads",
+    "optimizer_step", "zero_grads", "DiTGrads", "load_dit_block", "load_gpt", "read_tdit", "read_tgmt",
+    "save_tdit", "save_tgmt",
 ]

@@ -65,6 +65,25 @@ class DiTGrads(ctypes.Structure):
                [(n, ctypes.c_void_p) for n in ("n1", "n1b", "n2", "n2b", "nf")]
 
 
+class TgmtHeader(ctypes.Structure):
+    """dgm_tgmt_header: GPT.save's header fields (src/GPT.swift:265-281)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("version", "bits", "vocab", "block", "layers", "heads", "embd",
+                                               "qGroup")]
+
+
+class TditHeader(ctypes.Structure):
+    """dgm_tdit_header: DiT.save's header fields (src/DiT.swift:396-411)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("version", "side", "patch", "names", "loops", "heads", "kvHeads",
+                                               "embd", "intermediate", "freqDim", "diffusionSteps")] + \
+               [("lastAlpha", ctypes.c_float), ("valueMix", ctypes.c_float), ("header_bytes", ctypes.c_uint32)]
+
+
+class ParamInfo(ctypes.Structure):
+    """dgm_param_info: one parameter of a checkpoint."""
+    _fields_ = [("name", ctypes.c_char * 32), ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+                ("quantized", ctypes.c_int32), ("decay", ctypes.c_int32), ("offset", ctypes.c_int64)]
+
+
 def _u32s(*names):
     return [(n, ctypes.c_uint32) for n in names]
 
@@ -159,6 +178,10 @@ PROTOTYPES = {
     "dgm_ropeTables": (_I, [_I64, _I64, _F, _P, _P]),
     "dgm_dit_workspace_floats": (_I64, [ctypes.POINTER(DiTCfg)]),
     "dgm_dit_forward": (_I, [_P, ctypes.POINTER(DiTCfg), ctypes.POINTER(DiTWeights), _P, _P, _P, _P, _I64]),
+    "dgm_tgmt_parse": (_I, [_P, _I64, ctypes.POINTER(TgmtHeader), ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "dgm_tgmt_param": (_I, [ctypes.POINTER(TgmtHeader), _I64, ctypes.POINTER(ParamInfo)]),
+    "dgm_tdit_parse": (_I, [_P, _I64, ctypes.POINTER(TditHeader), ctypes.POINTER(_I64)]),
+    "dgm_tdit_param": (_I, [ctypes.POINTER(TditHeader), _I64, ctypes.POINTER(ParamInfo)]),
     "dgm_rmsBwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F]),
     "dgm_attnBwd": (_I, [_P] * 11 + [_I64] * 4),
     "dgm_ropeBwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),

@@ -390,6 +390,41 @@ int dgm_bias_grad(dgm_gpu* g, const float* dY, float* db, const dgm_BiasP* p);
 /* GPU.biasGrad (src/GPU.swift:274-277). */
 int dgm_biasGrad(dgm_gpu* g, const float* dy, float* db, int64_t M, int64_t N);
 
+/* ---- checkpoints (host code, no context) ----------------------------------
+ * The reference's checkpoint files: a little-endian header, then every
+ * parameter's fp32 master in the model's creation order. These validate a
+ * file image in host memory and describe each parameter; the caller uploads
+ * the masters and re-quantizes the quantized ones (GPT.load calls
+ * quantizeAll, src/GPT.swift:318-322). Return DGM_ERR_SHAPE for a wrong magic
+ * or version, an invalid configuration, or a length that does not match the
+ * model (the reference's preconditions). */
+typedef struct dgm_tgmt_header {   /* GPT.save (src/GPT.swift:265-281) */
+    uint32_t version, bits, vocab, block, layers, heads, embd, qGroup;
+} dgm_tgmt_header;
+typedef struct dgm_tdit_header {   /* DiT.save (src/DiT.swift:396-411) */
+    uint32_t version, side, patch, names, loops, heads, kvHeads, embd, intermediate, freqDim,
+        diffusionSteps;
+    float lastAlpha, valueMix;      /* version 1 files carry no lastAlpha: 0.01 */
+    uint32_t header_bytes;          /* where the first parameter starts       */
+} dgm_tdit_header;
+typedef struct dgm_param_info {
+    char name[32];                  /* the reference's parameter name          */
+    int64_t rows, cols;
+    int32_t quantized, decay;       /* Param.quantized / Param.decay           */
+    int64_t offset;                 /* byte offset of its fp32 data in the file */
+} dgm_param_info;
+
+/* GPT.load (src/GPT.swift:283-324): header, itos at *itos_offset (vocab
+ * bytes), then 2 + 16*layers + 2 parameters (wte, wpe, per layer ln1.g ...
+ * proj.b, ln_f.g, ln_f.b; src/GPT.swift:44-64, 118-131). */
+int dgm_tgmt_parse(const void* data, int64_t len, dgm_tgmt_header* hdr, int64_t* itos_offset,
+                   int64_t* nparams);
+int dgm_tgmt_param(const dgm_tgmt_header* hdr, int64_t i, dgm_param_info* out);
+/* DiT.load (src/DiT.swift:413-451): 17 parameters, wpatch ... wdown, n1 ... nf
+ * (src/DiT.swift:233-250). */
+int dgm_tdit_parse(const void* data, int64_t len, dgm_tdit_header* hdr, int64_t* nparams);
+int dgm_tdit_param(const dgm_tdit_header* hdr, int64_t i, dgm_param_info* out);
+
 #ifdef __cplusplus
 }
 #endif
