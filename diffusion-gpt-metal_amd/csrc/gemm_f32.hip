@@ -598,6 +598,370 @@ void launch_fwd_lds_ks(const GemmArgs& a, hipStream_t st) {
                        per);
 }
 
+// The 4-way contraction split (16 x 16 tiles) with X read straight into
+// registers. With one 16-column group per workgroup no two waves read the same
+// X element, so the LDS block and the barrier before the first MFMA are pure
+// latency: here every lane loads, for each of its stages, the 64 contiguous
+// bytes of X row r16 that it multiplies (indices 16q .. 16q+15 of the stage)
+// as four 16-byte loads, right after that stage's weight codes. Stage u's
+// MFMAs wait only for the loads issued up to stage u (in-order vmcnt), so the
+// first products start while later stages are still in flight. SPW = stages
+// per wave = K / 256 exactly: the body is one basic block, so the compiler
+// cannot sink a stage's loads down to its products. The arithmetic, the order
+// of the sums and the fixed-order reduction of the 4 parts are those of
+// gemm_fwd_lds_kernel<BITS, 4>, so the two give bitwise equal results.
+template <int BITS, int SPW>
+__global__ __launch_bounds__(kThreads) void gemm_fwd_reg_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    __shared__ float part[4 * 16 * 16];
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_i * tiles_j) return;
+    const int ti = t / tiles_j, tj = t - ti * tiles_j;
+    const int i0 = ti * 16, j0 = tj * 16;
+    const int K = a.K;   // == 256 * SPW
+    const int lane = threadIdx.x & 63, wk = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int n = min(j0 + r16, a.cols - 1);
+    const float* xr = a.A + size_t(min(i0 + r16, a.rows - 1)) * K + 16 * q4;
+
+    uint32_t wc[SPW][BITS == 4 ? 2 : 4];
+    float4 wf[SPW][BITS == 32 ? 4 : 1];
+    float sc[SPW];
+    float4 xv[SPW][4];
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+        const int st = wk + 4 * u;
+        const int k = st * 64 + 16 * q4;
+        if constexpr (BITS == 32) {
+            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.B) + size_t(n) * K + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wf[u][e] = p[e];
+        } else if constexpr (BITS == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.B) + size_t(n) * K + k);
+            wc[u][0] = v.x; wc[u][1] = v.y; wc[u][2] = v.z; wc[u][3] = v.w;
+            sc[u] = a.scale[size_t(n) * a.groups + k / a.G];
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.B) + ((size_t(n) * K + k) >> 1));
+            wc[u][0] = v.x; wc[u][1] = v.y;
+            sc[u] = a.scale[size_t(n) * a.groups + k / a.G];
+        }
+        const float4* xp = reinterpret_cast<const float4*>(xr + st * 64);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xv[u][c] = xp[c];
+    }
+    // This thread's output element after the reduction, and its bias.
+    const int e = threadIdx.x;   // 256 threads = the 16 x 16 tile
+    const int i = i0 + (e >> 4), j = j0 + (e & 15);
+    const float bb = a.has_bias ? a.bias[min(j, a.cols - 1)] : 0.0f;
+    // Keep every load above the first wait: left alone, the scheduler moves the
+    // later stages' loads between the MFMAs, after the wait for stage 0, which
+    // exposes a second memory latency.
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 x = xv[u][c];
+            float bv[4];
+            if constexpr (BITS == 32) {
+                const float4 w = wf[u][c];
+                bv[0] = w.x; bv[1] = w.y; bv[2] = w.z; bv[3] = w.w;
+            } else if constexpr (BITS == 8) {
+                const uint32_t w = wc[u][c];
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(int8_t((w >> (8 * s2)) & 0xFF))) * sc[u];
+            } else {
+                const uint32_t w = wc[u][c >> 1] >> (16 * (c & 1));
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    const int nib = int((w >> (4 * s2)) & 0xF);
+                    bv[s2] = float(nib >= 8 ? nib - 16 : nib) * sc[u];
+                }
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, bv[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, bv[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, bv[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, bv[3], acc, 0, 0, 0);
+        }
+    }
+
+    // acc: rows 4*q4 + r, column r16. Parts summed in order 0..3, then the bias.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[(wk * 16 + 4 * q4 + r) * 16 + r16] = acc[r];
+    __syncthreads();
+    if (i < a.rows && j < a.cols) {
+        float v = part[e];
+#pragma unroll
+        for (int p2 = 1; p2 < 4; ++p2) v += part[p2 * 256 + e];
+        if (a.has_bias) v += bb;
+        a.out[size_t(i) * a.cols + j] = v;
+    }
+}
+
+template <int BITS, int SPW>
+void launch_fwd_reg_spw(const GemmArgs& a, hipStream_t st) {
+    const int ti = int(dgm::ceil_div(a.rows, 16)), tj = int(dgm::ceil_div(a.cols, 16));
+    const int per = int((int64_t(ti) * tj + 7) / 8);
+    hipLaunchKernelGGL((gemm_fwd_reg_kernel<BITS, SPW>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, ti, tj,
+                       per);
+}
+
+// K % 256 == 0 (checked by the caller); K <= 1024, 512 for fp32 weights.
+template <int BITS>
+void launch_fwd_reg(const GemmArgs& a, hipStream_t st) {
+    const int spw = a.K / 256;
+    if constexpr (BITS == 32) {
+        if (spw == 1) launch_fwd_reg_spw<BITS, 1>(a, st);
+        else launch_fwd_reg_spw<BITS, 2>(a, st);
+    } else {
+        if (spw == 1) launch_fwd_reg_spw<BITS, 1>(a, st);
+        else if (spw == 2) launch_fwd_reg_spw<BITS, 2>(a, st);
+        else if (spw == 3) launch_fwd_reg_spw<BITS, 3>(a, st);
+        else launch_fwd_reg_spw<BITS, 4>(a, st);
+    }
+}
+
+// ---- Pipelined forward for quantized weights: 16 x 32 tiles, 8 waves ----------
+// Measured on these latency-bound shapes, a CU pulls data from L2 at only
+// ~27 B/ns (outstanding misses x L2 latency), so what matters is the bytes each
+// CU must receive and how early the MFMAs can start. A workgroup owns 16 rows x
+// 32 columns of Y; its 8 waves are 4 contraction parts (wk: stages wk, wk+4,
+// ...) x 2 column groups (wn). Everything it reads is moved into LDS by
+// direct-to-LDS loads whose 64 lanes cover whole cache lines: first the W codes
+// of the 32 columns (one contiguous chunk of 32 rows) and their scales (one
+// contiguous chunk of 32 x groups floats), then X stage by stage (16 rows x 64
+// floats = 4 KB per stage, stored stage-major, each of the two waves of a
+// contraction part loading 8 of the rows). Before stage u a wave waits only for
+// its own loads up to that stage (vmcnt in issue order) and meets the others at
+// a barrier, so the MFMAs of early stages overlap the loads of later ones.
+// The LDS reads are inline asm: the compiler cannot tell them apart from the
+// pending direct-to-LDS loads and would otherwise wait for all of them before
+// the first read. Swizzles: X slot p of row r is stored at p ^ r; W slot p of
+// row r at p ^ f(r), f chosen from the row stride so that the 16 rows read by
+// one operand fetch fall in distinct banks. Products, their order and the
+// fixed-order reduction of the 4 parts are those of gemm_fwd_lds_kernel<BITS, 4>:
+// the results are bitwise equal.
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+
+template <int VM>
+__device__ __forceinline__ void wait_own_loads_and_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
+__device__ __forceinline__ void lds_read_x4(float4& x0, float4& x1, float4& x2, float4& x3, uint32_t a0, uint32_t a1,
+                                            uint32_t a2, uint32_t a3) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b128 %2, %6\n\t"
+        "ds_read_b128 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+        : "memory");
+}
+
+// One stage's codes (8 bytes int4 / 16 bytes int8) and scale of a lane.
+template <int BITS>
+__device__ __forceinline__ void lds_read_codes(uint32_t (&w)[BITS == 4 ? 2 : 4], float& s, uint32_t aw, uint32_t as) {
+    if constexpr (BITS == 4) {
+        uint2 v;
+        asm volatile(
+            "ds_read_b64 %0, %2\n\t"
+            "ds_read_b32 %1, %3\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v), "=&v"(s)
+            : "v"(aw), "v"(as)
+            : "memory");
+        w[0] = v.x; w[1] = v.y;
+    } else {
+        uint4 v;
+        asm volatile(
+            "ds_read_b128 %0, %2\n\t"
+            "ds_read_b32 %1, %3\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v), "=&v"(s)
+            : "v"(aw), "v"(as)
+            : "memory");
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    }
+}
+
+// W slot swizzle of local row r (0..31): 16-byte slots per row = K * BITS / 128.
+template <int BITS>
+__device__ __forceinline__ int w_swizzle(int r, bool odd_k256) {
+    if constexpr (BITS == 4) return odd_k256 ? ((r >> 1) & 7) : (r & 15);
+    else return r & 15;
+}
+
+template <int BITS, int SPW>
+__global__ __launch_bounds__(512) void gemm_fwd_pipe_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    extern __shared__ __align__(16) float4 pipe_lds[];
+    __shared__ float part[4 * 16 * 32];
+    const int K = a.K;               // == 256 * SPW
+    const int wspr = K * BITS / 128; // 16-byte W slots per row
+    const bool odd = ((K >> 8) & 1) != 0;
+    float4* xs = pipe_lds;                                    // [K/64 stages][16 rows][16 slots]
+    float4* ws = pipe_lds + (K >> 6) * 256;                   // [32 rows][wspr slots]
+    float* ss = reinterpret_cast<float*>(ws + 32 * wspr);     // [32 rows][groups]
+
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles_i * tiles_j) return;
+    const int ti = t / tiles_j, tj = t - ti * tiles_j;
+    const int i0 = ti * 16, j0 = tj * 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wk = wave & 3, wn = wave >> 2;
+    const int r16 = lane & 15, q4 = lane >> 4;
+
+    // Output element of this thread after the reduction, and its bias.
+    const int e = threadIdx.x;
+    const int oi = i0 + (e >> 5), oj = j0 + (e & 31);
+    const float bb = a.has_bias ? a.bias[min(oj, a.cols - 1)] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+
+    // W codes of columns j0 .. j0+31, then their scales.
+    const size_t row_bytes = size_t(K) * BITS / 8;
+    const int winst = (32 * wspr) >> 6;
+    for (int ii = wave; ii < winst; ii += 8) {
+        const int L = ii * 64 + lane;
+        const int row = L / wspr, pos = L - row * wspr;
+        const uint8_t* src = static_cast<const uint8_t*>(a.B) + size_t(min(j0 + row, a.cols - 1)) * row_bytes +
+                             (size_t(pos ^ w_swizzle<BITS>(row, odd)) << 4);
+        __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(ws + ii * 64), 16, 0, 0);
+    }
+    const int sslots = 8 * a.groups;   // 16-byte slots of the 32 x groups block
+    for (int ii = wave; ii * 64 < sslots; ii += 8) {
+        const int L = ii * 64 + lane;
+        if (L < sslots) {
+            const int f = 4 * L;
+            const int row = f / a.groups, g = f - row * a.groups;
+            const float* src = a.scale + size_t(min(j0 + row, a.cols - 1)) * a.groups + g;
+            __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(reinterpret_cast<float4*>(ss) + ii * 64),
+                                             16, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // X, stage by stage: this wave loads rows 8*wn .. 8*wn+7 of its stages.
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+        const int st = wk + 4 * u;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int c = 2 * wn + cc;
+            const int row = 4 * c + (lane >> 4), p = lane & 15;
+            const float* src = a.A + size_t(min(i0 + row, a.rows - 1)) * K + st * 64 + 4 * (p ^ row);
+            __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)(xs + st * 256 + c * 64), 16, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    const int wrow = wn * 16 + r16;
+    const int wsw = w_swizzle<BITS>(wrow, odd);
+    uint32_t wc[SPW][BITS == 4 ? 2 : 4];
+    float sc[SPW];
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+        // Everything this wave issued up to stage u has landed; the barrier
+        // extends that to the other waves' loads of the same stages.
+        if (u == SPW - 1) wait_own_loads_and_barrier<0>();
+        else if (u == SPW - 2) wait_own_loads_and_barrier<2>();
+        else if (u == SPW - 3) wait_own_loads_and_barrier<4>();
+        else wait_own_loads_and_barrier<6>();
+        if (u == 0) {
+#pragma unroll
+            for (int v = 0; v < SPW; ++v) {
+                const int sv = wk + 4 * v;
+                const int slot = BITS == 4 ? 2 * sv + (q4 >> 1) : 4 * sv + q4;
+                const uint8_t* wp = reinterpret_cast<const uint8_t*>(ws + wrow * wspr + (slot ^ wsw)) +
+                                    (BITS == 4 ? 8 * (q4 & 1) : 0);
+                lds_read_codes<BITS>(wc[v], sc[v], lds_off(wp),
+                                     lds_off(ss + wrow * a.groups + (sv * 64 + 16 * q4) / a.G));
+            }
+        }
+        const int st = wk + 4 * u;
+        const float4* xrow = xs + st * 256 + r16 * 16;
+        float4 xv[4];
+        lds_read_x4(xv[0], xv[1], xv[2], xv[3], lds_off(xrow + ((4 * q4 + 0) ^ r16)), lds_off(xrow + ((4 * q4 + 1) ^ r16)),
+                    lds_off(xrow + ((4 * q4 + 2) ^ r16)), lds_off(xrow + ((4 * q4 + 3) ^ r16)));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 x = xv[c];
+            float bv[4];
+            if constexpr (BITS == 8) {
+                const uint32_t w = wc[u][c];
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(__builtin_amdgcn_sbfe(int(w), 8 * s2, 8))) * sc[u];
+            } else {
+                const uint32_t w = wc[u][c >> 1] >> (16 * (c & 1));
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(__builtin_amdgcn_sbfe(int(w), 4 * s2, 4))) * sc[u];
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, bv[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, bv[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, bv[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, bv[3], acc, 0, 0, 0);
+        }
+        // Keep the next stage's wait below this stage's products.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // acc: rows 4*q4 + r, column wn*16 + r16. Parts summed in order 0..3, then the bias.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[(wk * 16 + 4 * q4 + r) * 32 + wn * 16 + r16] = acc[r];
+    __syncthreads();
+    if (oi < a.rows && oj < a.cols) {
+        float v = part[e];
+#pragma unroll
+        for (int p2 = 1; p2 < 4; ++p2) v += part[p2 * 512 + e];
+        if (a.has_bias) v += bb;
+        a.out[size_t(oi) * a.cols + oj] = v;
+    }
+}
+
+size_t fwd_pipe_lds_bytes(const GemmArgs& a, int bits) {
+    return size_t(16) * a.K * 4 + size_t(32) * a.K * bits / 8 + size_t(32) * a.groups * 4;
+}
+
+// int4 / int8 codes, 256 <= K <= 1024 with K % 256 == 0, groups of a multiple
+// of 16 (one scale per lane per stage) with K / G % 4 == 0 (whole 16-byte scale
+// slots per row), and 16-byte aligned X, codes and scales.
+bool fwd_pipe_ok(const GemmArgs& a, int bits, const void* X, const void* W, const float* S) {
+    if (bits != 4 && bits != 8) return false;
+    if (a.K % 256 != 0 || a.K > 1024 || a.rows == 0 || a.cols == 0) return false;
+    if (a.G % 16 != 0 || a.groups % 4 != 0) return false;
+    return dgm::aligned(X, 16) && dgm::aligned(W, 16) && dgm::aligned(S, 16);
+}
+
+template <int BITS, int SPW>
+int launch_fwd_pipe_spw(dgm_gpu* g, const GemmArgs& a) {
+    const size_t lds = fwd_pipe_lds_bytes(a, BITS);
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fwd_pipe_kernel<BITS, SPW>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "gemm_nt: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(e));
+    }
+    const int ti = int(dgm::ceil_div(a.rows, 16)), tj = int(dgm::ceil_div(a.cols, 32));
+    const int per = int((int64_t(ti) * tj + 7) / 8);
+    hipLaunchKernelGGL((gemm_fwd_pipe_kernel<BITS, SPW>), dim3(unsigned(per) * 8u), dim3(512), lds, g->stream, a, ti,
+                       tj, per);
+    return DGM_OK;
+}
+
+template <int BITS>
+int launch_fwd_pipe(dgm_gpu* g, const GemmArgs& a) {
+    switch (a.K / 256) {
+        case 1: return launch_fwd_pipe_spw<BITS, 1>(g, a);
+        case 2: return launch_fwd_pipe_spw<BITS, 2>(g, a);
+        case 3: return launch_fwd_pipe_spw<BITS, 3>(g, a);
+        default: return launch_fwd_pipe_spw<BITS, 4>(g, a);
+    }
+}
+
 // K % 64 == 0 and K <= 1024 (the X block stays in LDS; 512 with fp32
 // weights, which take 16 registers per stage), a group that is a
 // multiple of 16 (one scale per lane per stage), 16-byte aligned rows.
@@ -616,8 +980,10 @@ void launch_fwd_lds(const GemmArgs& a, int num_cus, hipStream_t st) {
     const int nst = a.K / 64;
     const int64_t ti = dgm::ceil_div(a.rows, 16);
     const int64_t w4 = ti * dgm::ceil_div(a.cols, 16), w2 = ti * dgm::ceil_div(a.cols, 32);
-    if (nst >= 4 && (w2 < int64_t(num_cus) * 3 / 2 || nst >= 8))
-        launch_fwd_lds_ks<BITS, 4>(a, st);
+    if (nst >= 4 && (w2 < int64_t(num_cus) * 3 / 2 || nst >= 8)) {
+        if (nst % 4 == 0) launch_fwd_reg<BITS>(a, st);
+        else launch_fwd_lds_ks<BITS, 4>(a, st);
+    }
     else if (nst >= 2 && w2 < int64_t(num_cus) * 3)
         launch_fwd_lds_ks<BITS, 2>(a, st);
     else
@@ -941,6 +1307,13 @@ int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const 
     a.has_bias = p->hasBias != 0;
     const size_t wal = bits == 32 ? 16 : (bits == 8 ? 4 : 2);
     const bool vec = (p->K % 4) == 0 && aligned(X, 16) && aligned(W, wal);
+    // The pipelined 16 x 32 kernel where the 4-way contraction split applies:
+    // at least 1.5 tiles per CU would otherwise be too few, or K >= 512.
+    if (fwd_pipe_ok(a, bits, X, W, scale)) {
+        const int64_t w2 = int64_t(dgm::ceil_div(a.rows, 16)) * dgm::ceil_div(a.cols, 32);
+        if (w2 < int64_t(g->num_cus) * 3 / 2 || a.K >= 512)
+            return bits == 8 ? launch_fwd_pipe<8>(g, a) : launch_fwd_pipe<4>(g, a);
+    }
     if (fwd_lds_ok(a, bits, X, W)) {
         if (bits == 32) launch_fwd_lds<32>(a, g->num_cus, g->stream);
         else if (bits == 8) launch_fwd_lds<8>(a, g->num_cus, g->stream);

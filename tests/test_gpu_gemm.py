@@ -148,6 +148,26 @@ def test_ragged_shapes(gpu, orc, bits, G, M, N, K_groups):
     assert max(errs.values()) <= TOL, errs
 
 
+@pytest.mark.parametrize("M,N,K,G,bits", [(33, 47, 256, 32, 4), (16, 16, 512, 16, 8), (100, 20, 1024, 128, 4),
+                                          (17, 200, 768, 32, 8), (5, 9, 512, 1, 32), (64, 30, 256, 1, 32),
+                                          (512, 192, 1024, 32, 4), (48, 16, 1024, 16, 8), (80, 24, 256, 128, 4),
+                                          (72, 40, 512, 256, 8), (512, 200, 768, 32, 8)])
+def test_forward_split_contraction(gpu, orc, M, N, K, G, bits):
+    """Forwards with a contraction that is a multiple of 256 and a 4-way
+    contraction split: int4/int8 codes with K / G % 4 == 0 take the pipelined
+    16 x 32 kernel (codes, scales and X staged in LDS), the others and fp32
+    weights the 16 x 16 kernel that reads X straight into registers; rows and
+    columns past the matrix are clamped on load and masked on store."""
+    rng = np.random.default_rng(M + 5 * N + K + bits)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if N % 2 == 0 else None
+    dy = rng.standard_normal(M * N).astype(np.float32)
+    out = run_step(gpu, bits, x, w, bias, dy, M, N, K, G)
+    errs = _check_all(orc, out, x, w, bias, dy, M, N, K, G, bits)
+    assert max(errs.values()) <= TOL, errs
+
+
 @pytest.mark.parametrize("M,N,K,G,bits", [(48, 32, 40, 8, 8), (16, 48, 70, 14, 4), (80, 16, 24, 2, 4),
                                           (32, 64, 100, 10, 8), (64, 16, 27, 1, 32), (17, 32, 48, 16, 4),
                                           (96, 48, 36, 4, 8), (512, 192, 768, 32, 4), (512, 768, 192, 32, 8),
