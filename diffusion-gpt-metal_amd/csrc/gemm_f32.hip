@@ -542,10 +542,7 @@ __global__ __launch_bounds__(kThreads) void gemm_fwd_lds_kernel(GemmArgs a, int 
             } else {
                 const uint32_t w = wc[u][c >> 1] >> (16 * (c & 1));
 #pragma unroll
-                for (int s2 = 0; s2 < 4; ++s2) {
-                    const int nib = int((w >> (4 * s2)) & 0xF);
-                    bv[s2] = float(nib >= 8 ? nib - 16 : nib) * sc[u];
-                }
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(__builtin_amdgcn_sbfe(int(w), 4 * s2, 4))) * sc[u];
             }
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, bv[0], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, bv[1], acc, 0, 0, 0);
@@ -674,10 +671,7 @@ __global__ __launch_bounds__(kThreads) void gemm_fwd_reg_kernel(GemmArgs a, int 
             } else {
                 const uint32_t w = wc[u][c >> 1] >> (16 * (c & 1));
 #pragma unroll
-                for (int s2 = 0; s2 < 4; ++s2) {
-                    const int nib = int((w >> (4 * s2)) & 0xF);
-                    bv[s2] = float(nib >= 8 ? nib - 16 : nib) * sc[u];
-                }
+                for (int s2 = 0; s2 < 4; ++s2) bv[s2] = float(int(__builtin_amdgcn_sbfe(int(w), 4 * s2, 4))) * sc[u];
             }
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, bv[0], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, bv[1], acc, 0, 0, 0);
@@ -1019,7 +1013,11 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     float* wt = reinterpret_cast<float*>(sm4 + 16 * spr);     // [64][N + 4]
     const int wld = N + 4;
 
-    // -- weight strip: 16-byte units, unit u -> row n = u % N, part u / N.
+    // -- weight strip: 16-byte units. 32 consecutive lanes take 32 consecutive
+    // rows n of one part of the strip, the next 32 lanes the next part, so a
+    // wave instruction reads whole 32-byte (int4) row segments and the
+    // transposed LDS writes below stay conflict-free. Units past the strip are
+    // not loaded (units is a multiple of 64: N % 64 == 0).
     constexpr int CPU = BITS == 4 ? 32 : (BITS == 8 ? 16 : 4);   // codes (or floats) per unit
     constexpr int UPR = 64 / CPU;                                // units per row of the strip
     constexpr int MAXU = (448 * UPR + kThreads - 1) / kThreads;
@@ -1028,8 +1026,11 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     float ws[MAXU];
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
-        const int idx = min(int(threadIdx.x) + u * kThreads, units - 1);
-        const int n = idx % N, part = idx / N;
+        if (u * kThreads >= units) break;
+        const int idx = int(threadIdx.x) + u * kThreads;
+        if (idx >= units) continue;   // wave-uniform (units % 64 == 0)
+        const int grp = idx >> 5;
+        const int n = (grp / UPR) * 32 + (idx & 31), part = grp % UPR;
         const int kc = min(k0 + part * CPU, K - CPU);   // strip columns past K: clamped, never stored
         if constexpr (BITS == 32) {
             wv[u] = *reinterpret_cast<const uint4*>(static_cast<const float*>(a.B) + size_t(n) * K + kc);
@@ -1054,7 +1055,8 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     for (int u = 0; u < MAXU; ++u) {
         const int idx = int(threadIdx.x) + u * kThreads;
         if (idx >= units) break;
-        const int n = idx % N, part = idx / N;
+        const int grp = idx >> 5;
+        const int n = (grp / UPR) * 32 + (idx & 31), part = grp % UPR;
         float* dst = wt + (part * CPU) * wld + n;
         const uint32_t w4[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
         if constexpr (BITS == 32) {
@@ -1062,13 +1064,12 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
             for (int e = 0; e < 4; ++e) dst[e * wld] = __uint_as_float(w4[e]);
         } else if constexpr (BITS == 8) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) dst[e * wld] = float(int(int8_t((w4[e >> 2] >> (8 * (e & 3))) & 0xFF))) * ws[u];
+            for (int e = 0; e < 16; ++e)
+                dst[e * wld] = float(int(__builtin_amdgcn_sbfe(int(w4[e >> 2]), 8 * (e & 3), 8))) * ws[u];
         } else {
 #pragma unroll
-            for (int e = 0; e < 32; ++e) {
-                const int nib = int((w4[e >> 3] >> (4 * (e & 7))) & 0xF);
-                dst[e * wld] = float(nib >= 8 ? nib - 16 : nib) * ws[u];
-            }
+            for (int e = 0; e < 32; ++e)
+                dst[e * wld] = float(int(__builtin_amdgcn_sbfe(int(w4[e >> 3]), 4 * (e & 7), 4))) * ws[u];
         }
     }
     __syncthreads();
