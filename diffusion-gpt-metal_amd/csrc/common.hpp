@@ -46,6 +46,25 @@ void* workspace(dgm_gpu* g, size_t bytes);
 
 constexpr int64_t kMaxIndex = (int64_t(1) << 31) - 1;
 
+// Where the DiT block's training forward stores one loop's activations (the
+// reference's Acts, src/DiT.swift:260-300): x, ln1 and its rstd, q / k / v
+// as the attention consumed them ([B*T, C], k and v repeated to every head),
+// probs, av, attn, rstd of rms(attn), mid, ln2 and its rstd, gate, up, sw,
+// mlp, rstd of rms(mlp), pre, rstd of rms(pre).
+struct DitSaves {
+    float *x, *ln1, *r1, *q, *k, *v, *probs, *av, *attn, *r1b, *mid, *ln2, *r2, *gate, *up, *sw, *mlp, *r2b, *pre,
+        *rf;
+};
+// The training forward on the fused loop-body kernels (dit.hip), storing the
+// activations of every loop into saves[0 .. loops-1]. Returns kNotFused
+// (recording nothing) when the weights or sizes do not fit the fused kernels,
+// so the caller runs the kernel-per-wrapper sequence instead.
+constexpr int kNotFused = -1;
+int64_t dit_train_scratch_floats(const dgm_dit_cfg* c);
+int dit_forward_train_fused(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
+                            const float* sinv, float* x, const DitSaves* saves, float* scratch,
+                            int64_t scratch_floats);
+
 inline bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }

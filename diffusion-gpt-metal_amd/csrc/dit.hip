@@ -223,6 +223,11 @@ struct AttnArgs {
     int kv_heads;                    // 1 (shared head) or H
     float scale, ca, cb;
     int causal, rope, vmix;
+    // Optional saves for the training forward ([B*T, o_ld] rows, head h at
+    // column h*D): q after RoPE, and k after RoPE and v after the value mix,
+    // each repeated to every query head. Null = not stored.
+    float *qo, *ko, *vo;
+    int o_ld;
 };
 
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
@@ -327,6 +332,18 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
+
+    // -- training saves: this workgroup's 16 query rows of q, and the same 16
+    // token rows of k and v for head h (all workgroups of (b, h) cover T).
+    if (a.qo) {
+        for (int e = threadIdx.x; e < 16 * D; e += kThreads) {
+            const int r = e / D, d = e - r * D;
+            const size_t o = size_t(b * T + t0 + r) * a.o_ld + h * D + d;
+            a.qo[o] = qs[r * qs_ld + d];
+            a.ko[o] = ks[(t0 + r) * qs_ld + d];
+            a.vo[o] = vt[d * vt_ld + t0 + r];
+        }
+    }
 
     // -- scores: wave w takes key tiles w, w+4, ...
     const size_t srow0 = (size_t(b) * H + h) * T + t0;   // row index into [B,H,T,T]
@@ -542,7 +559,8 @@ __global__ __launch_bounds__(kThreads) void row_fuse_kernel(const float* __restr
                                                             float* __restrict__ mid, float* __restrict__ out2,
                                                             float* __restrict__ out3, const float* __restrict__ w1,
                                                             const float* __restrict__ w2, const float* __restrict__ w3,
-                                                            float* __restrict__ rstd, int rows, int cols, float eps) {
+                                                            float* __restrict__ rstd, float* __restrict__ rstd1,
+                                                            int rows, int cols, float eps) {
 #pragma clang fp contract(off)
     const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -552,6 +570,7 @@ __global__ __launch_bounds__(kThreads) void row_fuse_kernel(const float* __restr
 #pragma unroll
     for (int u = 0; u < kRowMax; ++u) v[u] = lane + 64 * u < cols ? a[base + lane + 64 * u] : 0.0f;
     float rs = row_rstd(v, lane, cols, eps);
+    if (lane == 0 && rstd1) rstd1[row] = rs;
 #pragma unroll
     for (int u = 0; u < kRowMax; ++u) {
         const int c = lane + 64 * u;
@@ -619,6 +638,11 @@ struct DitGemmArgs {
     int M, N, K, G, groups, F;
     float eps;
     int pro;
+    // Optional saves for the training forward (stored by the workgroups of
+    // column tile 0; null = not stored): the normalized rows fed to the GEMM,
+    // pro 3's first-stage rows (pre), each stage's rstd per row, and with
+    // PAIR the gate and up projections before SwiGLU ([M, F] each).
+    float *lnout, *side1, *rs1, *rs2, *rs3, *gate_out, *up_out;
 };
 
 __device__ __forceinline__ float sum16(float v) {
@@ -707,29 +731,34 @@ __global__ __launch_bounds__(kThreads) void dit_gemm_kernel(DitGemmArgs a, int t
             }
             if (a.pro == 3) w3[j] = *reinterpret_cast<const float4*>(a.w3 + c);
         }
+        const bool saver = tj == 0 && gi < a.M;   // this row's saves
+        auto save_rows = [&](float* dst) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) *reinterpret_cast<float4*>(dst + base + 4 * (r16 + 16 * j)) = v[j];
+        };
+        if (a.pro == 1 && a.side && saver) save_rows(a.side);   // the input rows
         float rs = rstd16<J>(v, K, a.eps);
+        if (a.rs1 && saver && r16 == 0) a.rs1[gi] = rs;
 #pragma unroll
         for (int j = 0; j < J; ++j) v[j] = norm4(v[j], rs, w1[j]);
         if (a.pro >= 2) {
 #pragma unroll
             for (int j = 0; j < J; ++j) v[j] = add4(rr[j], v[j]);
-            if (a.pro == 2 && tj == 0 && gi < a.M) {
-#pragma unroll
-                for (int j = 0; j < J; ++j) *reinterpret_cast<float4*>(a.side + base + 4 * (r16 + 16 * j)) = v[j];
-            }
+            if (a.pro == 2 && saver) save_rows(a.side);
+            if (a.pro == 3 && a.side1 && saver) save_rows(a.side1);
             rs = rstd16<J>(v, K, a.eps);
+            if (a.rs2 && saver && r16 == 0) a.rs2[gi] = rs;
 #pragma unroll
             for (int j = 0; j < J; ++j) v[j] = norm4(v[j], rs, w2[j]);
             if (a.pro == 3) {
-                if (tj == 0 && gi < a.M) {
-#pragma unroll
-                    for (int j = 0; j < J; ++j) *reinterpret_cast<float4*>(a.side + base + 4 * (r16 + 16 * j)) = v[j];
-                }
+                if (saver) save_rows(a.side);
                 rs = rstd16<J>(v, K, a.eps);
+                if (a.rs3 && saver && r16 == 0) a.rs3[gi] = rs;
 #pragma unroll
                 for (int j = 0; j < J; ++j) v[j] = norm4(v[j], rs, w3[j]);
             }
         }
+        if (a.lnout && saver) save_rows(a.lnout);
         const int spr = K >> 2;
 #pragma unroll
         for (int j = 0; j < J; ++j) xs4[row * spr + ((r16 + 16 * j) ^ (row & 15))] = v[j];
@@ -783,6 +812,17 @@ __global__ __launch_bounds__(kThreads) void dit_gemm_kernel(DitGemmArgs a, int t
         if (wave >= 2) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) up[(4 * q4 + r) * 32 + (wave - 2) * 16 + r16] = acc[r];
+        }
+        float* proj = wave < 2 ? a.gate_out : a.up_out;
+        if (proj) {
+            const int j = j0 + (wave & 1) * 16 + r16;
+            if (j < a.F) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = i0 + 4 * q4 + r;
+                    if (i < a.M) proj[size_t(i) * a.F + j] = acc[r];
+                }
+            }
         }
         __syncthreads();
         if (wave < 2) {
@@ -871,10 +911,10 @@ int64_t dit_workspace_floats(const dgm_dit_cfg* c) {
 
 int launch_row_fuse(dgm_gpu* g, const float* a, const float* res, float* mid, float* out2, float* out3,
                     const float* w1, const float* w2, const float* w3, float* rstd, int64_t rows, int64_t cols,
-                    float eps) {
+                    float eps, float* rstd1 = nullptr) {
     if (rows == 0 || cols == 0) return DGM_OK;
     hipLaunchKernelGGL(row_fuse_kernel, dim3(unsigned((rows + 3) / 4)), dim3(kThreads), 0, g->stream, a, res, mid,
-                       out2, out3, w1, w2, w3, rstd, int(rows), int(cols), eps);
+                       out2, out3, w1, w2, w3, rstd, rstd1, int(rows), int(cols), eps);
     return dgm::check_launch(g, "dit_forward row_fuse");
 }
 
@@ -896,6 +936,102 @@ bool follows(const dgm_dit_linear& first, const dgm_dit_linear& next, int64_t ro
 }
 
 }  // namespace
+
+namespace dgm {
+
+// Scratch of the fused training forward: loop 0's and the current loop's
+// [q | k | v] rows and the scores the attention kernel writes.
+int64_t dit_train_scratch_floats(const dgm_dit_cfg* c) {
+    const int64_t M = int64_t(c->B) * c->T, QKV = c->C + 2 * int64_t(c->D);
+    return 2 * ((M * QKV + 63) & ~int64_t(63)) + int64_t(c->B) * c->H * c->T * c->T;
+}
+
+int dit_forward_train_fused(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
+                            const float* sinv, float* x, const DitSaves* saves, float* scratch,
+                            int64_t scratch_floats) {
+    const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
+    const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, QKV = C + 2 * KV;
+    if (!follows(w->wq, w->wk, C, C, bits, G) || !follows(w->wk, w->wv, KV, C, bits, G) ||
+        !follows(w->wgate, w->wup, F, C, bits, G) || !dit_fused_ok(c, w) || !attn_mfma_ok(T, D) ||
+        c->C > 64 * kRowMax || scratch_floats < dit_train_scratch_floats(c) || !aligned(x, 16) ||
+        !aligned(scratch, 16) || !aligned(cosv, 16) || !aligned(sinv, 16))
+        return kNotFused;
+    for (int l = 0; l < c->loops; ++l) {
+        const DitSaves& S = saves[l];
+        for (const float* p : {S.x, S.ln1, S.attn, S.mid, S.ln2, S.mlp, S.pre, S.q, S.k, S.v, S.av})
+            if (!aligned(p, 16)) return kNotFused;
+    }
+    float* qkv0 = scratch;
+    float* qkv1 = qkv0 + ((M * QKV + 63) & ~int64_t(63));
+    float* scores = qkv1 + ((M * QKV + 63) & ~int64_t(63));
+#define DGM_TRY(expr)                \
+    do {                             \
+        int _r = (expr);             \
+        if (_r != DGM_OK) return _r; \
+    } while (0)
+    auto pgemm = [&](const dgm_dit_linear& L, bool pair, int pro, const float* a_in, const float* res,
+                     const float* n_a, const float* n_b, const float* n_c, float* side, float* out, int64_t N,
+                     DitGemmArgs d) -> int {
+        d.a = a_in; d.res = res; d.w1 = n_a; d.w2 = n_b; d.w3 = n_c; d.side = side;
+        d.W = bits == 32 ? static_cast<const void*>(L.w) : L.q;
+        d.S = L.scale;
+        d.out = out;
+        d.M = int(M); d.N = int(N); d.K = int(C); d.G = bits == 32 ? 1 : G;
+        d.groups = bits == 32 ? 0 : int(C / G);
+        d.F = int(F); d.eps = c->eps; d.pro = pro;
+        return launch_dit_gemm(g, bits, pair, d);
+    };
+    auto gemm = [&](const dgm_dit_linear& L, const float* in, float* out, int64_t N, int64_t K) -> int {
+        dgm_GemmP gp{uint32_t(M), uint32_t(N), uint32_t(K), 0u, uint32_t(bits == 32 ? 0 : G), 0, 0, 0};
+        int r = gemm_check_sizes(g, "dit_forward_train", &gp, bits);
+        if (r) return r;
+        const void* wt = bits == 32 ? static_cast<const void*>(L.w) : L.q;
+        r = gemm_f32_fwd(g, bits, wt, L.scale, in, nullptr, out, &gp);
+        if (r) return r;
+        return check_launch(g, "dit_forward_train gemm");
+    };
+    for (int l = 0; l < c->loops; ++l) {
+        const DitSaves& S = saves[l];
+        float* qkv = l == 0 ? qkv0 : qkv1;
+        DitGemmArgs d{};
+        d.lnout = S.ln1;
+        if (l == 0) {   // x (saved as loop 0's input) -> ln1 = rms(x) * n1
+            d.rs1 = S.r1;
+            DGM_TRY(pgemm(w->wq, false, 1, x, nullptr, w->n1, nullptr, nullptr, S.x, qkv, QKV, d));
+        } else {        // pre = mid + rms(mlp) * n2b; x = rms(pre) * nf; ln1 = rms(x) * n1
+            const DitSaves& P = saves[l - 1];
+            d.side1 = P.pre; d.rs1 = P.r2b; d.rs2 = P.rf; d.rs3 = S.r1;
+            DGM_TRY(pgemm(w->wq, false, 3, P.mlp, P.mid, w->n2b, w->nf, w->n1, S.x, qkv, QKV, d));
+        }
+        AttnArgs aa{};
+        aa.q = qkv; aa.k = qkv + C; aa.v = qkv + C + KV; aa.vfirst = qkv0 + C + KV;
+        aa.cosv = cosv; aa.sinv = sinv;
+        aa.scores = scores; aa.probs = S.probs; aa.av = S.av;
+        aa.B = B; aa.T = T; aa.H = H; aa.D = D;
+        aa.q_ld = aa.kv_ld = aa.vf_ld = int(QKV); aa.av_ld = int(C);
+        aa.kv_heads = 1;
+        aa.scale = 1.0f / sqrtf(float(D));
+        aa.ca = 1.0f - c->mix; aa.cb = c->mix;
+        aa.causal = 0; aa.rope = 1; aa.vmix = l > 0;
+        aa.qo = S.q; aa.ko = S.k; aa.vo = S.v; aa.o_ld = int(C);
+        DGM_TRY(launch_attn_mfma(g, aa));
+        DGM_TRY(gemm(w->wo, S.av, S.attn, C, C));
+        // mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2; gate, up; sw = swiglu(gate, up)
+        DitGemmArgs d2{};
+        d2.lnout = S.ln2; d2.rs1 = S.r1b; d2.rs2 = S.r2; d2.gate_out = S.gate; d2.up_out = S.up;
+        DGM_TRY(pgemm(w->wgate, true, 2, S.attn, S.x, w->n1b, w->n2, nullptr, S.mid, S.sw, 2 * F, d2));
+        DGM_TRY(gemm(w->wdown, S.sw, S.mlp, C, F));
+    }
+    if (c->loops > 0) {   // pre = mid + rms(mlp) * n2b; x = rms(pre) * nf
+        const DitSaves& P = saves[c->loops - 1];
+        DGM_TRY(launch_row_fuse(g, P.mlp, P.mid, P.pre, x, nullptr, w->n2b, w->nf, nullptr, P.rf, M, C, c->eps,
+                                P.r2b));
+    }
+#undef DGM_TRY
+    return DGM_OK;
+}
+
+}  // namespace dgm
 
 extern "C" {
 

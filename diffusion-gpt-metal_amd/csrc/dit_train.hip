@@ -618,6 +618,22 @@ int dgm_dit_forward_train(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weight
         S[i] = cur;
         cur += fsz[i];
     }
+    // Fused loop-body kernels (five launches per loop, as the inference
+    // forward) storing every activation the backward reads, when the weights
+    // are laid out back to back; otherwise one kernel per wrapper below.
+    {
+        dgm::DitSaves sv[64];
+        for (int l = 0; l < L; ++l) {
+            sv[l] = dgm::DitSaves{A(l, A_X),   A(l, A_LN1), A(l, A_R1),   A(l, A_Q),   A(l, A_K),
+                                  A(l, A_V),   A(l, A_PROBS), A(l, A_AV), A(l, A_ATTN), A(l, A_R1B),
+                                  A(l, A_MID), A(l, A_LN2), A(l, A_R2),   A(l, A_GATE), A(l, A_UP),
+                                  A(l, A_SW),  A(l, A_MLP), A(l, A_R2B),  A(l, A_PRE), A(l, A_RF)};
+        }
+        int64_t fn = 0;
+        for (int i = 0; i < F_COUNT; ++i) fn += fsz[i];
+        const int r = dgm::dit_forward_train_fused(g, c, w, cosv, sinv, x, sv, S[0], fn);
+        if (r != dgm::kNotFused) return r;
+    }
     const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
     const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, nC = M * C, nKV = M * KV;
     const float mix = c->mix;
