@@ -6,11 +6,11 @@
 // Kernels (semantics of metal/kernels.metal, cited per kernel; fp contraction
 // off, each product and sum rounded as in the reference's separate
 // operations):
-//  * rms_bwd_dx: one wave per row; the row's sum(dy*w*x) is a wave reduction
-//    (fp32, a different order than the reference's sequential loop).
-//  * rms_bwd_dw: one workgroup of 16 waves per 64 columns; wave w sums rows
-//    w, w+16, ... and the 16 partial sums are added in wave order, then added
-//    into dweight (the weight is shared by every loop).
+//  * rms_bwd: dx (one wave per row; the row's sum(dy*w*x) is a wave reduction,
+//    fp32, a different order than the reference's sequential loop) and
+//    dweight (16 waves per 64 columns, partial sums added in wave order, then
+//    into dweight: the weight is shared by every loop) in one launch, dx
+//    optionally added to a residual gradient.
 //  * attention backward: one workgroup per (batch, head) with the head in
 //    LDS (T and D multiples of 4, (4TD + 2T^2) floats of LDS), or the
 //    reference's five passes with one lane per output; both sum in the
@@ -47,42 +47,47 @@ __device__ __forceinline__ float silu_sigmoid(float z) {
     return e / (1.0f + e);
 }
 
-// ---- rmsnorm_bwd_dx (metal/kernels.metal:827-850) ------------------------------
-__global__ __launch_bounds__(kThreads) void rms_bwd_dx_kernel(const float* __restrict__ x,
-                                                              const float* __restrict__ rstd,
-                                                              const float* __restrict__ w,
-                                                              const float* __restrict__ dy,
-                                                              float* __restrict__ dx, int rows, int cols) {
-    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float* xr = x + size_t(row) * cols;
-    const float* gr = dy + size_t(row) * cols;
-    float part = 0.0f;
-    for (int c = lane; c < cols; c += 64) {
-        const float dyhat = gr[c] * w[c];
-        part += dyhat * xr[c];
-    }
-    const float meanDyX = wave_sum(part) / float(cols);
-    const float rs = rstd[row];
-    const float rs3 = rs * rs * rs;
-    float* o = dx + size_t(row) * cols;
-    for (int c = lane; c < cols; c += 64) {
-        const float dyhat = gr[c] * w[c];
-        o[c] = rs * dyhat - xr[c] * rs3 * meanDyX;
-    }
-}
-
-// ---- rmsnorm_bwd_dw (metal/kernels.metal:852-868): dweight += sum over rows ----
 constexpr int kDwWaves = 16;
-__global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_dw_kernel(const float* __restrict__ x,
-                                                                   const float* __restrict__ rstd,
-                                                                   const float* __restrict__ dy,
-                                                                   float* __restrict__ dweight, int rows,
-                                                                   int cols) {
+
+// ---- rmsnorm backward (metal/kernels.metal:827-868), dx and dweight in one launch --
+// Workgroups [0, ndx) take 16 rows each for dx: one wave per row, the row's
+// sum(dy*w*x) a wave reduction (fp32, a different order than the reference's
+// sequential loop). The others take 64 columns each for dweight += sum over
+// rows: wave w sums rows w, w+16, ... and the 16 partial sums are added in
+// wave order, then added into dweight (the weight is shared by every loop). With
+// `add`, dx[r, c] = add[r, c] + the row's dx (an acc_f of the result; add may
+// alias dx).
+__global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ rstd,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ dy, float* dx,
+                                                                const float* add, float* __restrict__ dweight,
+                                                                int rows, int cols, int ndx) {
     __shared__ float part[kDwWaves][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + lane;
+    if (int(blockIdx.x) < ndx) {
+        const int row = blockIdx.x * kDwWaves + wave;
+        if (row >= rows) return;
+        const float* xr = x + size_t(row) * cols;
+        const float* gr = dy + size_t(row) * cols;
+        float pt = 0.0f;
+        for (int c = lane; c < cols; c += 64) {
+            const float dyhat = gr[c] * w[c];
+            pt += dyhat * xr[c];
+        }
+        const float meanDyX = wave_sum(pt) / float(cols);
+        const float rs = rstd[row];
+        const float rs3 = rs * rs * rs;
+        float* o = dx + size_t(row) * cols;
+        const float* ad = add ? add + size_t(row) * cols : nullptr;
+        for (int c = lane; c < cols; c += 64) {
+            const float dyhat = gr[c] * w[c];
+            const float v = rs * dyhat - xr[c] * rs3 * meanDyX;
+            o[c] = ad ? ad[c] + v : v;
+        }
+        return;
+    }
+    const int c = (int(blockIdx.x) - ndx) * 64 + lane;
     float acc = 0.0f;
     if (c < cols) {
         int r = wave;
@@ -103,7 +108,7 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_dw_kernel(const float* 
     if (wave == 0 && c < cols) {
         float tot = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kDwWaves; ++w) tot += part[w][lane];
+        for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][lane];
         dweight[c] += tot;
     }
 }
@@ -368,13 +373,13 @@ __global__ __launch_bounds__(kThreads) void acc_kernel(float* __restrict__ a, co
 inline unsigned blocks_for(int64_t n) { return unsigned((n + kThreads - 1) / kThreads); }
 bool bad_count(int64_t n) { return n < 0 || n > dgm::kMaxIndex; }
 
+// dx must not alias x or dy; `add` may alias dx.
 int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w, const float* dy, float* dx,
-                   float* dweight, int64_t rows, int64_t cols) {
+                   float* dweight, int64_t rows, int64_t cols, const float* add = nullptr) {
     if (rows == 0 || cols == 0) return DGM_OK;
-    hipLaunchKernelGGL(rms_bwd_dx_kernel, dim3(unsigned((rows + 3) / 4)), dim3(kThreads), 0, g->stream, x, rstd, w,
-                       dy, dx, int(rows), int(cols));
-    hipLaunchKernelGGL(rms_bwd_dw_kernel, dim3(unsigned((cols + 63) / 64)), dim3(64 * kDwWaves), 0, g->stream, x,
-                       rstd, dy, dweight, int(rows), int(cols));
+    const int ndx = int((rows + kDwWaves - 1) / kDwWaves), ndw = int((cols + 63) / 64);
+    hipLaunchKernelGGL(rms_bwd_kernel, dim3(unsigned(ndx + ndw)), dim3(64 * kDwWaves), 0, g->stream, x, rstd, w, dy,
+                       dx, add, dweight, int(rows), int(cols), ndx);
     return dgm::check_launch(g, "rms_bwd");
 }
 
@@ -716,18 +721,21 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         return dgm_gemmBwd(g, bits, Lw.w, Lw.q, Lw.scale, dy, in, out, dW, M, N, K, bits == 32 ? 8 : G, 1);
     };
     float *t1 = S[B_T1], *t2 = S[B_T2], *dln = S[B_DLN];
+    // RMSNorm backward; with `add`, the residual gradient add (acc_f) that
+    // follows it in the reference is done by the same launch.
+    auto rms_bwd = [&](const float* xin, const float* rstd, const float* wt, const float* dy, float* dx,
+                       float* dwt, const float* add) { return launch_rms_bwd(g, xin, rstd, wt, dy, dx, dwt, M, C, add); };
     DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
     for (int l = c->loops - 1; l >= 0; --l) {
-        DGM_TRY(dgm_rmsBwd(g, A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, M, C, c->eps));
-        DGM_TRY(dgm_rmsBwd(g, A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, M, C, c->eps));
+        DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
+        DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
         DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
         DGM_TRY(dgm_swigluBwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
         DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, F, C));
         DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));
         DGM_TRY(dgm_acc(g, t2, dln, nC));
-        DGM_TRY(dgm_rmsBwd(g, A(l, A_MID), A(l, A_R2), w->n2, t2, dln, gr->n2, M, C, c->eps));
-        DGM_TRY(dgm_acc(g, t1, dln, nC));
-        DGM_TRY(dgm_rmsBwd(g, A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, M, C, c->eps));
+        DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));   // t1 += dx
+        DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
         DGM_TRY(bwd(w->wo, t2, A(l, A_AV), S[B_DAV], gr->wo, C, C));
         DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK], S[B_DV],
                             S[B_DPROBS], S[B_DSCORES], B, T, H, D));
@@ -747,9 +755,7 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         DGM_TRY(dgm_acc(g, t2, dln, nC));
         DGM_TRY(bwd(w->wv, S[B_DVPRE], A(l, A_LN1), dln, gr->wv, KV, C));
         DGM_TRY(dgm_acc(g, t2, dln, nC));
-        DGM_TRY(dgm_rmsBwd(g, A(l, A_X), A(l, A_R1), w->n1, t2, dln, gr->n1, M, C, c->eps));
-        DGM_TRY(dgm_acc(g, t1, dln, nC));
-        DGM_TRY(dgm_copy(g, t1, gx, nC));
+        DGM_TRY(rms_bwd(A(l, A_X), A(l, A_R1), w->n1, t2, gx, gr->n1, t1));   // gx = t1 + dx
     }
     return DGM_OK;
 }
