@@ -64,6 +64,11 @@ int64_t dit_train_scratch_floats(const dgm_dit_cfg* c);
 int dit_forward_train_fused(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
                             const float* sinv, float* x, const DitSaves* saves, float* scratch,
                             int64_t scratch_floats);
+// True when `next`'s weights (fp32 for bits 32, else codes and scales)
+// start where `first`'s `rows` x K end, so the two act as one [2 rows, K]
+// linear.
+bool dit_linear_follows(const dgm_dit_linear& first, const dgm_dit_linear& next, int64_t rows, int64_t K, int bits,
+                        int G);
 
 inline bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;

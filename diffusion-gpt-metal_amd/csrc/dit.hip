@@ -939,6 +939,11 @@ bool follows(const dgm_dit_linear& first, const dgm_dit_linear& next, int64_t ro
 
 namespace dgm {
 
+bool dit_linear_follows(const dgm_dit_linear& first, const dgm_dit_linear& next, int64_t rows, int64_t K, int bits,
+                        int G) {
+    return follows(first, next, rows, K, bits, G);
+}
+
 // Scratch of the fused training forward: loop 0's and the current loop's
 // [q | k | v] rows and the scores the attention kernel writes.
 int64_t dit_train_scratch_floats(const dgm_dit_cfg* c) {

@@ -15,7 +15,11 @@
 //    LDS (T and D multiples of 4, (4TD + 2T^2) floats of LDS), or the
 //    reference's five passes with one lane per output; both sum in the
 //    reference's order and are bitwise the oracle's.
-//  * rope_bwd, swiglu_bwd, sum_heads, acc_f, acc_scale_f: elementwise.
+//  * rope_bwd, swiglu_bwd, sum_heads, acc_f, acc_scale_f: elementwise;
+//    qkv_grad: sum_heads, rope_bwd and the value-residual steps of the q / k /
+//    v gradients in one launch, one wave per token row.
+//  * swiglu_bwd and qkv_grad can write [dgate | dup] and [dq | dk | dv] rows,
+//    the output gradient of the stacked [gate; up] and [q; k; v] linears.
 // The block's GEMMs are the library's: dgm_gemmNT and dgm_gemmBwd (gemmDWAcc +
 // gemmDX in one launch) on the fp32 masters (bits 32, as the reference's DiT) or on
 // the group-quantized codes (bits 8 / 4: forward on the codes, dX through the
@@ -331,11 +335,12 @@ __global__ __launch_bounds__(kThreads) void rope_bwd_kernel(const float* __restr
 }
 
 // ---- swiglu_bwd (metal/kernels.metal:932-949) ------------------------------------
+// Outputs in rows of ldo floats (ldo == F: the contiguous [n] layout; 2F with
+// dup = dgate + F: the [dgate | dup] rows of a fused [gate; up] projection).
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* __restrict__ gate,
                                                               const float* __restrict__ up,
-                                                              const float* __restrict__ dy,
-                                                              float* __restrict__ dgate, float* __restrict__ dup,
-                                                              int64_t n) {
+                                                              const float* __restrict__ dy, float* dgate, float* dup,
+                                                              int64_t n, int64_t F, int64_t ldo) {
     const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
     if (i >= n) return;
     const float z = gate[i];
@@ -343,8 +348,61 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* __res
     const float silu = z * s;
     const float siluP = s * (1.0f + z * (1.0f - s));
     const float g = dy[i];
-    dgate[i] = siluP * up[i] * g;
-    dup[i] = silu * g;
+    const int64_t o = ldo == F ? i : (i / F) * ldo + i % F;
+    dgate[o] = siluP * up[i] * g;
+    dup[o] = silu * g;
+}
+
+// ---- gradients of q / k / v before their projections, one wave per token row ----
+// From the attention's dq, dk, dv ([B*T, H*D]): dq through RoPE (rope_bwd);
+// dk summed over heads (sum_heads) then through RoPE with one head; dv summed
+// over heads, then through the value residual: loop 0 (vmix == 0) dvpre =
+// dv1 + dfirst (copy_f, acc_f), later loops dvpre = mix(dv1, dv1, 1 - mix, 0)
+// and dfirst += mix * dv1 (mix_f, acc_scale_f). Every element is computed
+// with those kernels' formulas in their order, so the outputs equal the
+// sequence bitwise. Each output has its own row stride (the three blocks of
+// [q | k | v] rows, or three separate buffers).
+__global__ __launch_bounds__(kThreads) void qkv_grad_kernel(const float* __restrict__ dq, const float* __restrict__ dk,
+                                                            const float* __restrict__ dv,
+                                                            const float* __restrict__ cosv,
+                                                            const float* __restrict__ sinv, float* oq, int ldq,
+                                                            float* ok, int ldk, float* ov, int ldv,
+                                                            float* __restrict__ dfirst, int rows, int T, int H, int D,
+                                                            int vmix, float ca, float mixc) {
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int t = row % T, C = H * D, mid = D >> 1;
+    const float* q = dq + size_t(row) * C;
+    const float* cr = cosv + size_t(t) * D;
+    const float* sr = sinv + size_t(t) * D;
+    for (int e = lane; e < C; e += 64) {
+        const int d = e % D;
+        const float c = cr[d], s = sr[d];
+        oq[size_t(row) * ldq + e] = d < mid ? q[e] * c + q[e + mid] * s : q[e] * c - q[e - mid] * s;
+    }
+    const float* kr = dk + size_t(row) * C;
+    const float* vr = dv + size_t(row) * C;
+    for (int d = lane; d < D; d += 64) {
+        const int pd = d < mid ? d + mid : d - mid;
+        float a = 0.0f, b = 0.0f, v = 0.0f;
+        for (int h = 0; h < H; ++h) {
+            a += kr[h * D + d];
+            b += kr[h * D + pd];
+            v += vr[h * D + d];
+        }
+        const float c = cr[d], s = sr[d];
+        ok[size_t(row) * ldk + d] = d < mid ? a * c + b * s : a * c - b * s;
+        float* f = dfirst + size_t(row) * D + d;
+        if (vmix == 0) {
+            ov[size_t(row) * ldv + d] = v + *f;
+        } else {
+            const float p = ca * v;
+            const float r = 0.0f * v;
+            ov[size_t(row) * ldv + d] = p + r;
+            *f += mixc * v;
+        }
+    }
 }
 
 // ---- sum_heads (metal/kernels.metal:995-1010) --------------------------------------
@@ -414,11 +472,24 @@ int launch_rope_bwd(dgm_gpu* g, const float* dy, float* dx, const float* c, cons
 }
 
 int launch_swiglu_bwd(dgm_gpu* g, const float* gate, const float* up, const float* dy, float* dgate, float* dup,
-                      int64_t n) {
+                      int64_t n, int64_t F = 0, int64_t ldo = 0) {
     if (n == 0) return DGM_OK;
+    if (ldo == 0) F = ldo = n;
     hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, g->stream, gate, up, dy, dgate,
-                       dup, n);
+                       dup, n, F, ldo);
     return dgm::check_launch(g, "swiglu_bwd");
+}
+
+int launch_qkv_grad(dgm_gpu* g, const float* dq, const float* dk, const float* dv, const float* c, const float* s,
+                    float* oq, int ldq, float* ok, int ldk, float* ov, int ldv, float* dfirst, int B, int T, int H,
+                    int D, bool first_loop, float mix) {
+    const int rows = B * T;
+    if (rows == 0 || H == 0 || D == 0) return DGM_OK;
+    constexpr int per = kThreads / 64;
+    hipLaunchKernelGGL(qkv_grad_kernel, dim3(unsigned((rows + per - 1) / per)), dim3(kThreads), 0, g->stream, dq, dk,
+                       dv, c, s, oq, ldq, ok, ldk, ov, ldv, dfirst, rows, T, H, D, first_loop ? 0 : 1, 1.0f - mix,
+                       mix);
+    return dgm::check_launch(g, "qkv_grad");
 }
 
 int launch_sum_heads(dgm_gpu* g, const float* src, float* dst, int B, int T, int H, int D) {
@@ -451,8 +522,10 @@ enum { A_X, A_LN1, A_R1, A_Q, A_K, A_V, A_PROBS, A_AV, A_ATTN, A_R1B, A_MID, A_L
        A_MLP, A_R2B, A_PRE, A_RF, A_COUNT };
 enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_COUNT };
 // Backward scratch.
+// B_DG, B_DU back to back hold [M, 2F] rows [dgate | dup] and B_QPRE, B_KPRE,
+// B_DVPRE [M, C + 2 KV] rows [dq | dk | dv] when the linears are fused.
 enum { B_T1, B_T2, B_DLN, B_DSW, B_DG, B_DU, B_DAV, B_DQ, B_DK, B_DV, B_DPROBS, B_DSCORES, B_DK1, B_DV1,
-       B_DVPRE, B_DFIRST, B_QPRE, B_KPRE, B_COUNT };
+       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_COUNT };
 
 inline int64_t pad64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
@@ -470,7 +543,7 @@ void bwd_sizes(const dgm_dit_cfg* c, int64_t* b) {
     const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
     const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
     const int64_t bv[B_COUNT] = {M * C, M * C, M * C, M * F, M * F, M * F, M * C, M * C, M * C, M * C,
-                                 att,   att,   M * KV, M * KV, M * KV, M * KV, M * C, M * KV};
+                                 att,   att,   M * KV, M * KV, M * KV, M * C, M * KV, M * KV};
     for (int i = 0; i < B_COUNT; ++i) b[i] = pad64(bv[i]);
 }
 
@@ -725,36 +798,50 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     // follows it in the reference is done by the same launch.
     auto rms_bwd = [&](const float* xin, const float* rstd, const float* wt, const float* dy, float* dx,
                        float* dwt, const float* add) { return launch_rms_bwd(g, xin, rstd, wt, dy, dx, dwt, M, C, add); };
+    // Where q / k / v (gate / up) weights and their gradients lie back to
+    // back, one backward over the stacked [C + 2 KV, C] ([2F, C]) linear
+    // replaces three (two) and the adds of their dX: dW rows are the same
+    // sums, dX sums the same products in one chain.
+    const bool qkv1 = dgm::dit_linear_follows(w->wq, w->wk, C, C, bits, G) &&
+                      dgm::dit_linear_follows(w->wk, w->wv, KV, C, bits, G) && gr->wk == gr->wq + C * C &&
+                      gr->wv == gr->wk + KV * C;
+    const bool gu1 = dgm::dit_linear_follows(w->wgate, w->wup, F, C, bits, G) && gr->wup == gr->wgate + F * C;
+    const int64_t QKV = qkv1 ? C + 2 * KV : 0;
+    float* const qkvrow = S[B_QPRE];   // [M, C + 2 KV] rows when qkv1
     DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
     for (int l = c->loops - 1; l >= 0; --l) {
         DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
         DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
         DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
-        DGM_TRY(dgm_swigluBwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
-        DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, F, C));
-        DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));
-        DGM_TRY(dgm_acc(g, t2, dln, nC));
+        if (gu1) {
+            DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F, 2 * F));
+            DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, 2 * F, C));
+        } else {
+            DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
+            DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, F, C));
+            DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));
+            DGM_TRY(dgm_acc(g, t2, dln, nC));
+        }
         DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));   // t1 += dx
         DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
         DGM_TRY(bwd(w->wo, t2, A(l, A_AV), S[B_DAV], gr->wo, C, C));
         DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK], S[B_DV],
                             S[B_DPROBS], S[B_DSCORES], B, T, H, D));
-        DGM_TRY(dgm_sumHeads(g, S[B_DK], S[B_DK1], B, T, H, D));
-        DGM_TRY(dgm_sumHeads(g, S[B_DV], S[B_DV1], B, T, H, D));
-        DGM_TRY(dgm_ropeBwd(g, S[B_DQ], S[B_QPRE], cosv, sinv, B, T, H, D));
-        DGM_TRY(dgm_ropeBwd(g, S[B_DK1], S[B_KPRE], cosv, sinv, B, T, 1, D));
-        if (l == 0) {
-            DGM_TRY(dgm_copy(g, S[B_DV1], S[B_DVPRE], nKV));
-            DGM_TRY(dgm_acc(g, S[B_DVPRE], S[B_DFIRST], nKV));
+        // sum_heads of dk and dv, rope_bwd of dq and dk, the value-residual
+        // copy + acc (loop 0) or mix + acc_scale in one launch.
+        if (qkv1) {
+            DGM_TRY(launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, qkvrow, int(QKV), qkvrow + C, int(QKV),
+                                    qkvrow + C + KV, int(QKV), S[B_DFIRST], B, T, H, D, l == 0, mix));
+            DGM_TRY(bwd(w->wq, qkvrow, A(l, A_LN1), t2, gr->wq, QKV, C));
         } else {
-            DGM_TRY(dgm_mix(g, S[B_DV1], S[B_DV1], S[B_DVPRE], nKV, 1.0f - mix, 0.0f));
-            DGM_TRY(dgm_accScale(g, S[B_DFIRST], S[B_DV1], nKV, mix));
+            DGM_TRY(launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, S[B_QPRE], int(C), S[B_KPRE], int(KV),
+                                    S[B_DVPRE], int(KV), S[B_DFIRST], B, T, H, D, l == 0, mix));
+            DGM_TRY(bwd(w->wq, S[B_QPRE], A(l, A_LN1), t2, gr->wq, C, C));
+            DGM_TRY(bwd(w->wk, S[B_KPRE], A(l, A_LN1), dln, gr->wk, KV, C));
+            DGM_TRY(dgm_acc(g, t2, dln, nC));
+            DGM_TRY(bwd(w->wv, S[B_DVPRE], A(l, A_LN1), dln, gr->wv, KV, C));
+            DGM_TRY(dgm_acc(g, t2, dln, nC));
         }
-        DGM_TRY(bwd(w->wq, S[B_QPRE], A(l, A_LN1), t2, gr->wq, C, C));
-        DGM_TRY(bwd(w->wk, S[B_KPRE], A(l, A_LN1), dln, gr->wk, KV, C));
-        DGM_TRY(dgm_acc(g, t2, dln, nC));
-        DGM_TRY(bwd(w->wv, S[B_DVPRE], A(l, A_LN1), dln, gr->wv, KV, C));
-        DGM_TRY(dgm_acc(g, t2, dln, nC));
         DGM_TRY(rms_bwd(A(l, A_X), A(l, A_R1), w->n1, t2, gx, gr->n1, t1));   // gx = t1 + dx
     }
     return DGM_OK;

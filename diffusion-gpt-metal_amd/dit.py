@@ -146,8 +146,12 @@ class DiTBlock:
         if not hasattr(self, "grads"):
             shapes = self.cfg.linear_shapes()
             dev = self.cos.device
-            self.grads = {n: torch.zeros(shapes[n][0] * shapes[n][1], dtype=torch.float32, device=dev)
-                          for n in DIT_LINEARS}
+            # One buffer, the linears in order: [wq; wk; wv] and [wgate; wup]
+            # gradients sit back to back like their weights, so the backward
+            # runs each group as one weight-gradient GEMM.
+            sizes = [shapes[n][0] * shapes[n][1] for n in DIT_LINEARS]
+            self._grad_buf = torch.zeros(sum(sizes), dtype=torch.float32, device=dev)
+            self.grads = dict(zip(DIT_LINEARS, torch.split(self._grad_buf, sizes)))
             self.grads.update({n: torch.zeros(self.cfg.C, dtype=torch.float32, device=dev) for n in DIT_NORMS})
             self.c_grads = DiTGrads(*[self.grads[n].data_ptr() for n in DIT_LINEARS],
                                     *[self.grads[n].data_ptr() for n in DIT_NORMS])
@@ -156,8 +160,9 @@ class DiTBlock:
             self.acts = torch.zeros(max(self.acts_floats, 1), dtype=torch.float32, device=dev)
             self.bws = torch.zeros(max(self.bws_floats, 1), dtype=torch.float32, device=dev)
         else:
-            for t in self.grads.values():
-                t.zero_()
+            self._grad_buf.zero_()
+            for n in DIT_NORMS:
+                self.grads[n].zero_()
 
     def forward_train(self, x) -> None:
         """xs[0] -> xs[loops] in place, keeping every loop's activations for
