@@ -11,24 +11,24 @@
 //  * X is converted to bf16 once by a pre-pass (it is re-read by every tile
 //    column, so converting it inside the GEMM would repeat the work N/256
 //    times).
-//  * A workgroup of 8 waves computes a 256 x 256 tile of Y; each wave owns a
-//    64 x 128 block = 4 x 8 v_mfma_f32_16x16x32_bf16 tiles (128 fp32
-//    accumulators), so two waves share each SIMD and one wave's MFMAs overlap
-//    the other's dequantization, LDS and memory instructions. K advances 64
-//    per step.
-//  * The X tile goes global -> LDS with global_load_lds_dwordx4 (no VGPR
-//    staging). A wave instruction
-//    fills 1 KB of LDS in lane order, so rows are unpadded (128 B) and the
-//    16-byte chunks of row r sit at slot c ^ (r & 7): each lane fetches the
-//    global chunk that belongs in its slot. Fragment reads (16 rows, one
-//    chunk) then hit 8 distinct slots per 8-lane group, free of bank
-//    conflicts. The weight tile uses the same swizzle.
-//  * Each weight row is dequantized once per workgroup, by two threads (32 k
-//    each), into the bf16 weight tile in LDS.
-//  * Two stages: the loads of step k+1 are issued before the MFMAs of step k;
-//    the weight codes of step k+1 are dequantized and stored to the other
-//    stage after the MFMAs; one barrier per step. The loop is unrolled by two
-//    so every stage index is a compile-time constant.
+//  * A workgroup computes a 256 x 256 tile of Y with twelve waves in two
+//    roles. Eight MFMA waves each own a 64 x 128 block = 4 x 8
+//    v_mfma_f32_16x16x32_bf16 tiles (128 fp32 accumulators) and only read LDS
+//    and issue MFMAs. Four producer waves load the X tile (global -> LDS with
+//    global_load_lds_dwordx4, no VGPR staging) and the weight codes, and
+//    dequantize the codes into the bf16 weight tile in LDS, one weight row
+//    per lane. Each SIMD holds two MFMA waves and one producer, so the
+//    dequantization's VALU work runs beside the MFMAs. K advances 64 per step.
+//  * A wave instruction of the X load fills 1 KB of LDS in lane order, so rows
+//    are unpadded (128 B) and the 16-byte chunks of row r sit at slot
+//    c ^ (r & 7): each lane fetches the global chunk that belongs in its slot.
+//    Fragment reads (16 rows, one chunk) then hit 8 distinct slots per 8-lane
+//    group, free of bank conflicts. The weight tile uses the same swizzle.
+//  * Stages: three for X, two for the weights (160 KB of LDS). During step k
+//    the MFMA waves read stage k; the producers store the weights of step k+1
+//    (codes loaded during step k-1) and then issue the loads of step k+2, and
+//    enter the step's barrier once everything but those loads has landed, so
+//    every load has a whole step to arrive. One barrier per step.
 //  * Dequant: int4 bytes are flipped to offset binary and masked into the
 //    high nibble, so each byte is 16*(code+8) as an unsigned value and
 //    converts with one v_cvt_f32_ubyte; fma(f, s/16, -8s) then yields
@@ -50,8 +50,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int RS = BK * 2;        // LDS row stride in bytes (chunks swizzled, no pad)
 constexpr int TILE = BM * RS;     // one operand tile (BM == BN)
-constexpr int STAGE = 2 * TILE;
-constexpr size_t LDS_BYTES = 2 * STAGE;
 constexpr int GROUP_M = 4;        // tile rows per group of the XCD-local order
 
 struct Bf16Args {
@@ -86,21 +84,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Byte offset of 16-byte chunk c of row r in a swizzled operand tile.
 __device__ __forceinline__ int swz(int r, int c) { return r * RS + ((c ^ (r & 7)) << 4); }
 
-// ---- eight-wave variant --------------------------------------------------------
-// Same tile, stages, swizzle and dequantization as gemm_bf16_kernel, with 8
-// waves of 64 x 128 (128 accumulators each), so two waves share each SIMD and
-// one wave's MFMAs overlap the other's dequantization, LDS and memory work.
-// X rows: wave w loads 32 rows; weight rows: two threads per row, 32 k each.
-constexpr int NT8 = 512;
+// ---- the kernel ------------------------------------------------------------------
+// Twelve waves: waves 0-7 only read LDS and issue MFMAs (a 64 x 128 block
+// each); waves 8-11 are producers: they issue the X tile's direct-to-LDS loads
+// and load, dequantize and store the weight tile of the next step while the
+// MFMA waves work on the current one. Waves are dealt to the SIMDs round
+// robin, so each SIMD holds two MFMA waves and one producer and the
+// dequantization's VALU work overlaps MFMA issue instead of following it.
+// LDS: three X stages (the X tile of step k+2 is loaded during step k) and two
+// weight stages, 5 x 32 KB.
+constexpr int NTW = 768;
+constexpr int LDS_WS = 5 * TILE;
 
 template <int BITS>
-__global__ __launch_bounds__(NT8) void gemm_bf16_w8_kernel(Bf16Args a) {
-    constexpr int WB = BITS == 4 ? 1 : 2;   // 16-byte code loads per thread per step (32 k)
+__global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
+    constexpr int CB = BITS == 4 ? 2 : 4;   // 16-byte code loads per producer lane per 64-k step
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int l16 = lane & 15, q = lane >> 4;
-    const int wm = wave >> 1, wn = wave & 1;   // rows wm*64, cols wn*128
     const int M = a.M, N = a.N, K = a.K;
 
     const int total = a.tiles_m * a.tiles_n;
@@ -112,126 +114,138 @@ __global__ __launch_bounds__(NT8) void gemm_bf16_w8_kernel(Bf16Args a) {
     const int within = L - group * GROUP_M * a.tiles_n;
     const int m0 = (first_m + within % gm) * BM;
     const int n0 = (within / gm) * BN;
+    const int nk = K / BK;
 
-    // -- X tile: wave w loads rows w*32 .. w*32+31, 8 rows per instruction.
-    const int arl = lane >> 3, aslot = lane & 7;
-    uint32_t aoff[4];
+    if (wave >= 8) {
+        // ---- producer p: X rows 64p .. 64p+63 (8 per instruction), W row 64p + lane.
+        const int p = wave - 8;
+        const int arl = lane >> 3, aslot = lane & 7;
+        uint32_t aoff[8];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int r = wave * 32 + p * 8 + arl;
-        aoff[p] = uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8);
-    }
-    // -- weight tile: thread t -> row t/2, k half (t & 1) of the 64-k step.
-    const int brow = t >> 1, bh = t & 1;
-    const int bn = min(n0 + brow, N - 1);
-    const uint8_t* bptr = a.W + size_t(bn) * (BITS == 4 ? K / 2 : K);
-    const float* sptr = a.S + size_t(bn) * a.groups;
-
-    uint4 breg[WB];
-    float sreg;
-    auto gload = [&](int ks, int st) {
-        const int k0 = ks * BK;
-        uint8_t* As = smem + st * STAGE + wave * 32 * RS;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-            __builtin_amdgcn_global_load_lds((global_cvoid*)(a.Xb + aoff[p] + k0),
-                                             (lds_void*)(As + p * 8 * RS), 16, 0, 0);
-        const int kh = k0 + 32 * bh;
-#pragma unroll
-        for (int j = 0; j < WB; ++j)
-            breg[j] = *reinterpret_cast<const uint4*>(bptr + (BITS == 4 ? kh / 2 : kh) + 16 * j);
-        sreg = sptr[kh / a.G];
-    };
-
-    auto dequant_store = [&](int st) {
-        uint8_t* Bs = smem + st * STAGE + TILE;
-        const float s = sreg;
-        if constexpr (BITS == 4) {
-            const float s16 = s * 0.0625f, off = -8.0f * s;
-            const uint32_t w4[4] = {breg[0].x, breg[0].y, breg[0].z, breg[0].w};
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {   // 8 nibbles = k 8d..8d+7 of the half
-                const uint32_t x = w4[d] ^ 0x88888888u;
-                uint32_t lo = (x << 4) & 0xF0F0F0F0u;
-                uint32_t hi = x & 0xF0F0F0F0u;
-                // Opaque to the optimizer (no instruction): keeps each byte
-                // extraction below a single v_cvt_f32_ubyte{0..3} instead of a
-                // shift and mask folded into every byte.
-                asm("" : "+v"(lo));
-                asm("" : "+v"(hi));
-                const float fe[4] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
-                                     float(lo >> 24)};
-                const float fo[4] = {float(hi & 0xFFu), float((hi >> 8) & 0xFFu), float((hi >> 16) & 0xFFu),
-                                     float(hi >> 24)};
-                uint32_t o[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    o[i] = pack_bf16(__builtin_fmaf(fe[i], s16, off), __builtin_fmaf(fo[i], s16, off));
-                *reinterpret_cast<uint4*>(Bs + swz(brow, bh * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
-            }
-        } else {
-            const float off = -128.0f * s;
-            const uint32_t w8[8] = {breg[0].x, breg[0].y, breg[0].z, breg[0].w,
-                                    breg[1].x, breg[1].y, breg[1].z, breg[1].w};
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                uint32_t o[4];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t x = w8[2 * d + e] ^ 0x80808080u;
-                    const float f0 = float(x & 0xFFu), f1 = float((x >> 8) & 0xFFu);
-                    const float f2 = float((x >> 16) & 0xFFu), f3 = float(x >> 24);
-                    o[2 * e] = pack_bf16(__builtin_fmaf(f0, s, off), __builtin_fmaf(f1, s, off));
-                    o[2 * e + 1] = pack_bf16(__builtin_fmaf(f2, s, off), __builtin_fmaf(f3, s, off));
-                }
-                *reinterpret_cast<uint4*>(Bs + swz(brow, bh * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
-            }
+        for (int j = 0; j < 8; ++j) {
+            const int r = p * 64 + j * 8 + arl;
+            aoff[j] = uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8);
         }
-    };
+        const int brow = p * 64 + lane;
+        const int bn = min(n0 + brow, N - 1);
+        const uint8_t* bptr = a.W + size_t(bn) * (BITS == 4 ? K / 2 : K);
+        const float* sptr = a.S + size_t(bn) * a.groups;
+        auto xdma = [&](int ks, int st) {
+            uint8_t* As = smem + st * TILE + p * 64 * RS;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                __builtin_amdgcn_global_load_lds((global_cvoid*)(a.Xb + aoff[j] + ks * BK),
+                                                 (lds_void*)(As + j * 8 * RS), 16, 0, 0);
+        };
+        auto wload = [&](uint4 (&c)[CB], float (&s)[2], int ks) {
+            const int k0 = ks * BK;
+#pragma unroll
+            for (int j = 0; j < CB; ++j)
+                c[j] = *reinterpret_cast<const uint4*>(bptr + (BITS == 4 ? k0 / 2 : k0) + 16 * j);
+            s[0] = sptr[k0 / a.G];
+            s[1] = sptr[(k0 + 32) / a.G];
+        };
+        // k half h (32 k) of the step: chunks 4h .. 4h+3 of the row.
+        auto dequant_store = [&](const uint4 (&c)[CB], const float (&sc)[2], int st) {
+            uint8_t* Bs = smem + (3 + st) * TILE;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float s = sc[h];
+                if constexpr (BITS == 4) {
+                    const float s16 = s * 0.0625f, off = -8.0f * s;
+                    const uint32_t w4[4] = {c[h].x, c[h].y, c[h].z, c[h].w};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t x = w4[d] ^ 0x88888888u;
+                        uint32_t lo = (x << 4) & 0xF0F0F0F0u;
+                        uint32_t hi = x & 0xF0F0F0F0u;
+                        asm("" : "+v"(lo));
+                        asm("" : "+v"(hi));
+                        const float fe[4] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
+                                             float(lo >> 24)};
+                        const float fo[4] = {float(hi & 0xFFu), float((hi >> 8) & 0xFFu), float((hi >> 16) & 0xFFu),
+                                             float(hi >> 24)};
+                        uint32_t o[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            o[i] = pack_bf16(__builtin_fmaf(fe[i], s16, off), __builtin_fmaf(fo[i], s16, off));
+                        *reinterpret_cast<uint4*>(Bs + swz(brow, h * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
+                    }
+                } else {
+                    const float off = -128.0f * s;
+                    const uint32_t w8[8] = {c[2 * h].x, c[2 * h].y, c[2 * h].z, c[2 * h].w,
+                                            c[2 * h + 1].x, c[2 * h + 1].y, c[2 * h + 1].z, c[2 * h + 1].w};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        uint32_t o[4];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const uint32_t x = w8[2 * d + e] ^ 0x80808080u;
+                            const float f0 = float(x & 0xFFu), f1 = float((x >> 8) & 0xFFu);
+                            const float f2 = float((x >> 16) & 0xFFu), f3 = float(x >> 24);
+                            o[2 * e] = pack_bf16(__builtin_fmaf(f0, s, off), __builtin_fmaf(f1, s, off));
+                            o[2 * e + 1] = pack_bf16(__builtin_fmaf(f2, s, off), __builtin_fmaf(f3, s, off));
+                        }
+                        *reinterpret_cast<uint4*>(Bs + swz(brow, h * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
+                    }
+                }
+            }
+        };
+        uint4 cr[CB];
+        float sr[2];
+        auto clampk = [&](int ks) { return ks < nk ? ks : nk - 1; };
+        // X stage i at i * TILE, weight stage i at (3 + i) * TILE.
+        xdma(0, 0);
+        xdma(clampk(1), 1);
+        wload(cr, sr, 0);
+        dequant_store(cr, sr, 0);
+        wload(cr, sr, clampk(1));
+        __syncthreads();
+        for (int ks = 0; ks < nk; ++ks) {
+            // Weights of step ks+1 (codes loaded during the previous step; the
+            // compiler waits for every outstanding load before the LDS stores,
+            // which also completes X of step ks+1), then the loads of step ks+2.
+            dequant_store(cr, sr, (ks + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            xdma(clampk(ks + 2), (ks + 2) % 3);
+            wload(cr, sr, clampk(ks + 2));
+            __builtin_amdgcn_sched_barrier(0);
+            // Barrier once everything but this step's loads has completed
+            // (a __syncthreads here would also wait for those).
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + CB + 2) : "memory");
+        }
+        return;
+    }
 
+    // ---- MFMA waves
+    const int wm = wave >> 1, wn = wave & 1;
     f32x4 acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
     const int cw0 = ((0 * 4 + q) ^ (l16 & 7)) << 4, cw1 = ((1 * 4 + q) ^ (l16 & 7)) << 4;
-    auto compute = [&](int st) {
-        const uint8_t* As = smem + st * STAGE + (wm * 64 + l16) * RS;
-        const uint8_t* Bs = smem + st * STAGE + TILE + (wn * 128 + l16) * RS;
+    auto compute = [&](int xs, int ws) {
+        const uint8_t* As = smem + xs * TILE + (wm * 64 + l16) * RS;
+        const uint8_t* Bs = smem + (3 + ws) * TILE + (wn * 128 + l16) * RS;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             const int cw = kk ? cw1 : cw0;
-            bf16x8 bf[8], af[2];
+            bf16x8 af[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(Bs + j * 16 * RS + cw);
-            af[0] = *reinterpret_cast<const bf16x8*>(As + cw);
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(As + i * 16 * RS + cw);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (i + 1 < 4) af[(i + 1) & 1] = *reinterpret_cast<const bf16x8*>(As + (i + 1) * 16 * RS + cw);
+            for (int j = 0; j < 8; ++j) {
+                const bf16x8 bfj = *reinterpret_cast<const bf16x8*>(Bs + j * 16 * RS + cw);
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i & 1], bf[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < 4; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfj, acc[i][j], 0, 0, 0);
             }
         }
     };
-
-    const int nk = K / BK;   // even (host)
-    gload(0, 0);
-    dequant_store(0);
     __syncthreads();
-    for (int ks = 0; ks < nk; ks += 2) {
-        gload(ks + 1, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(0);
-        __builtin_amdgcn_sched_barrier(0);
-        dequant_store(1);
-        __syncthreads();
-        gload(ks + 2 < nk ? ks + 2 : ks + 1, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(1);
-        __builtin_amdgcn_sched_barrier(0);
-        dequant_store(0);
+    for (int ks = 0; ks < nk; ++ks) {
+        compute(ks % 3, ks & 1);
         __syncthreads();
     }
 
@@ -257,7 +271,7 @@ namespace dgm {
 // mode: K a multiple of 128, every 32-k half inside one group, aligned operands.
 bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p) {
     if (bits != 4 && bits != 8) return false;
-    if (p->M <= 64 || p->K == 0 || (p->K % (2 * BK)) != 0) return false;   // even step count
+    if (p->M <= 64 || p->K == 0 || (p->K % (2 * BK)) != 0) return false;
     if (p->qGroup == 0 || (p->qGroup % 32) != 0) return false;   // a thread's 32 k share a group
     if (int64_t(p->M) * p->K >= (int64_t(1) << 32)) return false;   // 32-bit element offsets
     (void)S;
@@ -288,16 +302,12 @@ int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const floa
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const unsigned grid = unsigned(a.tiles_m) * unsigned(a.tiles_n);
-    // Eight waves (two per SIMD): one wave's MFMAs overlap the other's
-    // dequantization and LDS traffic (~10% over the four-wave kernel at c5,
-    // identical results).
-    auto kern = bits == 4 ? gemm_bf16_w8_kernel<4> : gemm_bf16_w8_kernel<8>;
+    auto kern = bits == 4 ? gemm_bf16_kernel<4> : gemm_bf16_kernel<8>;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(LDS_BYTES));
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_WS);
     if (e != hipSuccess)
-        return fail(g, DGM_ERR_HIP, "bf16 gemm: cannot reserve %zu bytes of LDS: %s", LDS_BYTES,
-                    hipGetErrorString(e));
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(NT8), LDS_BYTES, st, a);
+        return fail(g, DGM_ERR_HIP, "bf16 gemm: cannot reserve %d bytes of LDS: %s", LDS_WS, hipGetErrorString(e));
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NTW), LDS_WS, st, a);
     return DGM_OK;
 }
 
