@@ -202,11 +202,11 @@ constexpr int kAbThreads = 1024;
 
 // out(r0, c0, acc) receives rows r0, r0+1 x columns c0, c0+1; A2(r, k) the
 // A values of rows r, r+1 at k; B2(k, c) the B values of columns c, c+1.
-template <typename FA, typename FB, typename FO>
+template <int NT = kAbThreads, typename FA, typename FB, typename FO>
 __device__ __forceinline__ void tiled_product(int rows, int cols, int kdim, FA A2, FB B2, FO out) {
     const int tc = cols / 2;
     const int ntiles = (rows / 2) * tc;
-    for (int tile = threadIdx.x; tile < ntiles; tile += kAbThreads) {
+    for (int tile = threadIdx.x; tile < ntiles; tile += NT) {
         const int r0 = (tile / tc) * 2, c0 = (tile % tc) * 2;
         float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
         for (int k = 0; k < kdim; k += 4) {
@@ -308,6 +308,197 @@ __global__ __launch_bounds__(kAbThreads) void attn_bwd_fused_kernel(AttnBwdArgs 
         [&](int s0, int d0, float a00, float a01, float a10, float a11) {
             store2(a.dk, s0, d0, a00 * a.scale, a01 * a.scale, a10 * a.scale, a11 * a.scale);
         });
+}
+
+// ---- split attention backward: 8-row blocks of a head in two launches ------------
+// The fused kernel gives each (batch, head) one workgroup: 32 workgroups at the
+// DiT's shape. Here a head's work is cut into blocks of 8 rows, with the same
+// per-element arithmetic and summation orders (results bitwise those of the
+// fused kernel):
+//  * rows kernel, workgroup (b, h, query block): dP = dO V^T and the softmax
+//    backward dS for its 8 query rows, then dQ = scale dS K; dP and dS go to
+//    dprobs / dscores;
+//  * keys kernel, workgroup (b, h, key block): dV = P^T dO and
+//    dK = scale dS^T Q for its 8 key rows, reading dS from dscores.
+// Both are bound by latency (global loads, then short LDS contractions): every
+// thread issues all of its loads before its first LDS store, so staging is one
+// round trip, and the products give one output per thread (sum over the
+// contraction index in increasing order from +0.0f).
+constexpr int kAsThreads = 1024;
+constexpr int kAsRows = 8;
+
+size_t attn_split_rows_lds(int T, int D) { return size_t(2 * kAsRows * T + kAsRows * D + 2 * T * D) * sizeof(float); }
+size_t attn_split_keys_lds(int T, int D) { return size_t(2 * kAsRows * T + 2 * T * D) * sizeof(float); }
+
+// out(r, c, v) for r < rows, c < cols, v = sum_k A(r, k) * B(k, c); one output per thread.
+template <typename FA, typename FB, typename FO>
+__device__ __forceinline__ void split_product(int rows, int cols, int kdim, FA A, FB B, FO out) {
+    for (int e = threadIdx.x; e < rows * cols; e += kAsThreads) {
+        const int r = e / cols, c = e % cols;
+        float acc = 0.0f;
+        int k = 0;
+        for (; k + 4 <= kdim; k += 4) {
+            float x[4], y[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                x[u] = A(r, k + u);
+                y[u] = B(k + u, c);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += x[u] * y[u];
+        }
+        for (; k < kdim; ++k) acc += A(r, k) * B(k, c);
+        out(r, c, acc);
+    }
+}
+
+__global__ __launch_bounds__(kAsThreads) void attn_bwd_rows_kernel(AttnBwdArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int T = a.T, D = a.D, H = a.H;
+    const int nblk = T / kAsRows;
+    const int bh = blockIdx.x / nblk, t0 = (blockIdx.x % nblk) * kAsRows;
+    const int b = bh / H, h = bh % H;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* Gr = lds;                 // dO rows [kAsRows][D]
+    float* Vt = Gr + kAsRows * D;    // [D][T]
+    float* Kf = Vt + T * D;          // [T][D]
+    float* Pr = Kf + T * D;          // P rows [kAsRows][T]
+    float* S = Pr + kAsRows * T;     // dP, then dS rows [kAsRows][T]
+    const int64_t row_stride = int64_t(H) * D;
+    const int64_t head0 = (int64_t(b) * T * H + h) * D;
+    const int64_t pm0 = (int64_t(b) * H + h) * T * T + int64_t(t0) * T;   // row t0 of P, dP, dS
+    const int d4 = D / 4, nkv = T * d4, ng = kAsRows * d4, np = kAsRows * T / 4;
+    const int nmax = max(nkv, max(ng, np));
+    for (int i = threadIdx.x; i < nmax; i += kAsThreads) {
+        float4 kk{}, vv{}, gg{}, pp{};
+        const int t = i / d4, c = (i % d4) * 4;
+        if (i < nkv) {
+            const int64_t off = head0 + t * row_stride + c;
+            kk = *reinterpret_cast<const float4*>(a.k + off);
+            vv = *reinterpret_cast<const float4*>(a.v + off);
+        }
+        if (i < ng) gg = *reinterpret_cast<const float4*>(a.dout + head0 + (t0 + t) * row_stride + c);
+        if (i < np) pp = reinterpret_cast<const float4*>(a.probs + pm0)[i];
+        if (i < nkv) {
+            *reinterpret_cast<float4*>(Kf + t * D + c) = kk;
+            Vt[(c + 0) * T + t] = vv.x;
+            Vt[(c + 1) * T + t] = vv.y;
+            Vt[(c + 2) * T + t] = vv.z;
+            Vt[(c + 3) * T + t] = vv.w;
+        }
+        if (i < ng) *reinterpret_cast<float4*>(Gr + t * D + c) = gg;
+        if (i < np) reinterpret_cast<float4*>(Pr)[i] = pp;
+    }
+    __syncthreads();
+    // dP[t][s] = sum_d dO[t][d] V[s][d]
+    split_product(
+        kAsRows, T, D, [&](int r, int d) { return Gr[r * D + d]; }, [&](int d, int s) { return Vt[d * T + s]; },
+        [&](int r, int s, float v) {
+            S[r * T + s] = v;
+            a.dprobs[pm0 + r * T + s] = v;
+        });
+    __syncthreads();
+    // dS rows: lane 0 of the row's wave forms the row dot in i order (the
+    // products rounded, then added, as the fused kernel), then the wave
+    // applies it.
+    for (int r = wave; r < kAsRows; r += kAsThreads / 64) {
+        float dot = 0.0f;
+        if (lane == 0) {
+            const float* sr = S + r * T;
+            const float* pr = Pr + r * T;
+            int i = 0;
+            for (; i + 8 <= T; i += 8) {
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) x[u] = sr[i + u] * pr[i + u];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) dot += x[u];
+            }
+            for (; i < T; ++i) dot += sr[i] * pr[i];
+        }
+        dot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(dot)));
+        for (int i = lane; i < T; i += 64) {
+            const float ds = Pr[r * T + i] * (S[r * T + i] - dot);
+            S[r * T + i] = ds;
+            a.dscores[pm0 + r * T + i] = ds;
+        }
+    }
+    __syncthreads();
+    // dQ[t][d] = scale * sum_s dS[t][s] K[s][d]
+    split_product(
+        kAsRows, D, T, [&](int r, int s) { return S[r * T + s]; }, [&](int s, int d) { return Kf[s * D + d]; },
+        [&](int r, int d, float v) { a.dq[head0 + (t0 + r) * row_stride + d] = v * a.scale; });
+}
+
+__global__ __launch_bounds__(kAsThreads) void attn_bwd_keys_kernel(AttnBwdArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int T = a.T, D = a.D, H = a.H;
+    const int nblk = T / kAsRows;
+    const int bh = blockIdx.x / nblk, s0 = (blockIdx.x % nblk) * kAsRows;
+    const int b = bh / H, h = bh % H;
+    float* G = lds;                  // dO [T][D]
+    float* Qf = G + T * D;           // [T][D]
+    float* Pc = Qf + T * D;          // P[:, s0 .. s0+kAsRows) as [T][kAsRows]
+    float* Sc = Pc + T * kAsRows;    // dS[:, s0 .. s0+kAsRows) as [T][kAsRows]
+    const int64_t row_stride = int64_t(H) * D;
+    const int64_t head0 = (int64_t(b) * T * H + h) * D;
+    const int64_t pm0 = (int64_t(b) * H + h) * T * T + s0;
+    const int d4 = D / 4, nq = T * d4, c4 = kAsRows / 4, npc = T * c4;
+    const int nmax = max(nq, npc);
+    for (int i = threadIdx.x; i < nmax; i += kAsThreads) {
+        float4 gg{}, qq{}, pp{}, ss{};
+        const int t = i / d4, c = (i % d4) * 4;
+        const int tp = i / c4, cp = (i % c4) * 4;
+        if (i < nq) {
+            const int64_t off = head0 + t * row_stride + c;
+            gg = *reinterpret_cast<const float4*>(a.dout + off);
+            qq = *reinterpret_cast<const float4*>(a.q + off);
+        }
+        if (i < npc) {
+            pp = *reinterpret_cast<const float4*>(a.probs + pm0 + tp * T + cp);
+            ss = *reinterpret_cast<const float4*>(a.dscores + pm0 + tp * T + cp);
+        }
+        if (i < nq) {
+            *reinterpret_cast<float4*>(G + t * D + c) = gg;
+            *reinterpret_cast<float4*>(Qf + t * D + c) = qq;
+        }
+        if (i < npc) {
+            *reinterpret_cast<float4*>(Pc + tp * kAsRows + cp) = pp;
+            *reinterpret_cast<float4*>(Sc + tp * kAsRows + cp) = ss;
+        }
+    }
+    __syncthreads();
+    // dV[s][d] = sum_t P[t][s] dO[t][d] and dK[s][d] = scale * sum_t dS[t][s] Q[t][d]:
+    // one list of 2 x kAsRows x D outputs, dV first.
+    const int nout = kAsRows * D;
+    for (int e = threadIdx.x; e < 2 * nout; e += kAsThreads) {
+        const bool isk = e >= nout;
+        const int r = (isk ? e - nout : e) / D, d = (isk ? e - nout : e) % D;
+        const float* A = (isk ? Sc : Pc) + r;
+        const float* Bm = (isk ? Qf : G) + d;
+        float acc = 0.0f;
+        int t = 0;
+        for (; t + 4 <= T; t += 4) {
+            float x[4], y[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                x[u] = A[(t + u) * kAsRows];
+                y[u] = Bm[(t + u) * D];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += x[u] * y[u];
+        }
+        for (; t < T; ++t) acc += A[t * kAsRows] * Bm[t * D];
+        float* o = (isk ? a.dk : a.dv) + head0 + (s0 + r) * row_stride + d;
+        *o = isk ? acc * a.scale : acc;
+    }
+}
+
+bool attn_split_ok(const AttnBwdArgs& a) {
+    return a.T % kAsRows == 0 && a.D % 4 == 0 && attn_split_rows_lds(a.T, a.D) <= 64 * 1024 &&
+           attn_split_keys_lds(a.T, a.D) <= 64 * 1024 && dgm::aligned(a.q, 16) && dgm::aligned(a.k, 16) &&
+           dgm::aligned(a.v, 16) && dgm::aligned(a.dout, 16) && dgm::aligned(a.probs, 16) &&
+           dgm::aligned(a.dscores, 16);
 }
 
 size_t attn_bwd_fused_lds(int T, int D) { return (size_t(4) * T * D + size_t(2) * T * T) * sizeof(float); }
@@ -444,6 +635,14 @@ int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w
 int launch_attn_bwd(dgm_gpu* g, const AttnBwdArgs& a) {
     const int64_t n = int64_t(a.B) * a.T * a.H * a.D, tt = int64_t(a.B) * a.H * a.T * a.T;
     if (n == 0) return DGM_OK;
+    if (attn_split_ok(a)) {
+        const unsigned grid = unsigned(a.B * a.H * (a.T / kAsRows));
+        hipLaunchKernelGGL(attn_bwd_rows_kernel, dim3(grid), dim3(kAsThreads), attn_split_rows_lds(a.T, a.D),
+                           g->stream, a);
+        hipLaunchKernelGGL(attn_bwd_keys_kernel, dim3(grid), dim3(kAsThreads), attn_split_keys_lds(a.T, a.D),
+                           g->stream, a);
+        return dgm::check_launch(g, "attn_bwd");
+    }
     if (attn_bwd_fused_ok(a)) {
         const size_t lds = attn_bwd_fused_lds(a.T, a.D);
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_bwd_fused_kernel),

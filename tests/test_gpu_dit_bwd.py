@@ -39,7 +39,9 @@ def test_rms_bwd(gpu, orc, rows, cols):
     assert gpu.lastKernel == "rmsnorm_bwd"
 
 
-@pytest.mark.parametrize("B,T,H,D", [(8, 64, 4, 48), (2, 5, 3, 4), (1, 17, 2, 10)])
+# T % 8 == 0: the two-launch split kernels; T % 4 == 0 (12): the one-workgroup-
+# per-head kernel; others: the five passes.
+@pytest.mark.parametrize("B,T,H,D", [(8, 64, 4, 48), (2, 32, 2, 12), (2, 12, 3, 8), (2, 5, 3, 4), (1, 17, 2, 10)])
 def test_attn_bwd_bitexact(gpu, orc, B, T, H, D):
     import torch
     rng = np.random.default_rng(B * T + H * D)
