@@ -117,6 +117,140 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_kernel(const float* __r
     }
 }
 
+// ---- two chained rmsnorm backwards in one launch (the DiT backward's pairs) -------
+// Stage 1 is rms_bwd above: out1 = [add1 +] dx of (x1, r1, w1, dy), dweight
+// w1's gradient += sum over rows by the direct workgroups. With x2 set, stage 2
+// takes out1 as its dy: out2 = [add2 +] dx of (x2, r2, w2, out1), computed by
+// the same wave from out1 held in registers (so add1 may alias out1). Stage
+// 2's dweight needs out1 of every row, so each dx workgroup writes the sums
+// over its 16 rows (in row order) to part2[block][cols], and a later launch
+// adds the blocks in order into the gradient: pin / dwp / npin name such
+// pending partial sums, reduced here by their own workgroups. Row arithmetic
+// is rms_bwd's; cols <= 256.
+constexpr int kChainCols = 256;
+struct RmsChainArgs {
+    const float *x1, *r1, *w1, *dy;
+    float* out1;
+    const float* add1;
+    float* dw1;
+    const float *x2, *r2, *w2;
+    float* out2;
+    const float* add2;
+    float* part2;
+    const float* pin;
+    float* dwp;
+    int npin;
+    int rows, cols, ndx, ndw;
+};
+
+__global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainArgs a) {
+    __shared__ float part[kDwWaves][kChainCols];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cols = a.cols, rows = a.rows;
+    constexpr int NPL = kChainCols / 64;
+    const int blk = int(blockIdx.x);
+    if (blk < a.ndx) {
+        const int row = blk * kDwWaves + wave;
+        const bool live = row < rows;
+        float o1[NPL];
+        if (live) {
+            const float* xr = a.x1 + size_t(row) * cols;
+            const float* gr = a.dy + size_t(row) * cols;
+            float pt = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c < cols) pt += (gr[c] * a.w1[c]) * xr[c];
+            }
+            const float meanDyX = wave_sum(pt) / float(cols);
+            const float rs = a.r1[row];
+            const float rs3 = rs * rs * rs;
+            float* o = a.out1 + size_t(row) * cols;
+            const float* ad = a.add1 ? a.add1 + size_t(row) * cols : nullptr;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int c = lane + 64 * i;
+                o1[i] = 0.0f;
+                if (c < cols) {
+                    const float dyhat = gr[c] * a.w1[c];
+                    const float v = rs * dyhat - xr[c] * rs3 * meanDyX;
+                    o1[i] = ad ? ad[c] + v : v;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c < cols) o[c] = o1[i];
+            }
+        }
+        if (!a.x2) return;
+        if (live) {
+            const float* xr = a.x2 + size_t(row) * cols;
+            float pt = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c < cols) pt += (o1[i] * a.w2[c]) * xr[c];
+            }
+            const float meanDyX = wave_sum(pt) / float(cols);
+            const float rs = a.r2[row];
+            const float rs3 = rs * rs * rs;
+            float* o = a.out2 + size_t(row) * cols;
+            const float* ad = a.add2 ? a.add2 + size_t(row) * cols : nullptr;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c < cols) {
+                    const float dyhat = o1[i] * a.w2[c];
+                    const float v = rs * dyhat - xr[c] * rs3 * meanDyX;
+                    o[c] = ad ? ad[c] + v : v;
+                    part[wave][c] = o1[i] * xr[c] * rs;
+                }
+            }
+        } else {
+            for (int c = lane; c < cols; c += 64) part[wave][c] = 0.0f;
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < cols; c += 64 * kDwWaves) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][c];
+            a.part2[size_t(blk) * cols + c] = tot;
+        }
+        return;
+    }
+    // direct dweight of stage 1 (as rms_bwd), then the pending partial sums.
+    const bool direct = blk < a.ndx + a.ndw;
+    const int c = (direct ? blk - a.ndx : blk - a.ndx - a.ndw) * 64 + lane;
+    float acc = 0.0f;
+    if (c < cols) {
+        if (direct) {
+            int r = wave;
+            for (; r + 7 * kDwWaves < rows; r += 8 * kDwWaves) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int rr = r + u * kDwWaves;
+                    v[u] = a.dy[size_t(rr) * cols + c] * a.x1[size_t(rr) * cols + c] * a.r1[rr];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc += v[u];
+            }
+            for (; r < rows; r += kDwWaves) acc += a.dy[size_t(r) * cols + c] * a.x1[size_t(r) * cols + c] * a.r1[r];
+        } else {
+            for (int b = wave; b < a.npin; b += kDwWaves) acc += a.pin[size_t(b) * cols + c];
+        }
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][lane];
+        (direct ? a.dw1 : a.dwp)[c] += tot;
+    }
+}
+
 // ---- attention backward (metal/kernels.metal:508-612) -----------------------------
 // q, k, v, dout, dq, dk, dv: [B, T, H, D]; probs, dprobs, dscores: [B, H, T, T].
 struct AttnBwdArgs {
@@ -632,6 +766,17 @@ int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w
     return dgm::check_launch(g, "rms_bwd");
 }
 
+// a.ndx / a.ndw are filled in here; a.pin may be null (no pending sums).
+int launch_rms_chain(dgm_gpu* g, RmsChainArgs a) {
+    if (a.rows == 0 || a.cols == 0) return DGM_OK;
+    a.ndx = (a.rows + kDwWaves - 1) / kDwWaves;
+    a.ndw = (a.cols + 63) / 64;
+    const int npend = a.pin ? a.ndw : 0;
+    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndw + npend)), dim3(64 * kDwWaves), 0,
+                       g->stream, a);
+    return dgm::check_launch(g, "rms_bwd");
+}
+
 int launch_attn_bwd(dgm_gpu* g, const AttnBwdArgs& a) {
     const int64_t n = int64_t(a.B) * a.T * a.H * a.D, tt = int64_t(a.B) * a.H * a.T * a.T;
     if (n == 0) return DGM_OK;
@@ -723,8 +868,10 @@ enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_COUNT
 // Backward scratch.
 // B_DG, B_DU back to back hold [M, 2F] rows [dgate | dup] and B_QPRE, B_KPRE,
 // B_DVPRE [M, C + 2 KV] rows [dq | dk | dv] when the linears are fused.
+// B_RPA / B_RPB: per-16-row-block sums of the chained RMSNorm backwards'
+// second-stage weight gradients (n2b, n1b), reduced by the next chain launch.
 enum { B_T1, B_T2, B_DLN, B_DSW, B_DG, B_DU, B_DAV, B_DQ, B_DK, B_DV, B_DPROBS, B_DSCORES, B_DK1, B_DV1,
-       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_COUNT };
+       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_RPA, B_RPB, B_COUNT };
 
 inline int64_t pad64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
@@ -741,8 +888,9 @@ void act_sizes(const dgm_dit_cfg* c, int64_t* a, int64_t* f) {
 void bwd_sizes(const dgm_dit_cfg* c, int64_t* b) {
     const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
     const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
-    const int64_t bv[B_COUNT] = {M * C, M * C, M * C, M * F, M * F, M * F, M * C, M * C, M * C, M * C,
-                                 att,   att,   M * KV, M * KV, M * KV, M * C, M * KV, M * KV};
+    const int64_t RP = (M + kDwWaves - 1) / kDwWaves * C;
+    const int64_t bv[B_COUNT] = {M * C, M * C, M * C, M * F, M * F, M * F, M * C,  M * C,  M * C, M * C,
+                                 att,   att,   M * KV, M * KV, M * KV, M * C, M * KV, M * KV, RP,    RP};
     for (int i = 0; i < B_COUNT; ++i) b[i] = pad64(bv[i]);
 }
 
@@ -1007,10 +1155,30 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     const bool gu1 = dgm::dit_linear_follows(w->wgate, w->wup, F, C, bits, G) && gr->wup == gr->wgate + F * C;
     const int64_t QKV = qkv1 ? C + 2 * KV : 0;
     float* const qkvrow = S[B_QPRE];   // [M, C + 2 KV] rows when qkv1
+    // The RMSNorm backwards that follow each other (nf then n2b, n2 then n1b)
+    // run as one chained launch when C <= 256; the second stage's weight
+    // gradient is summed per row block and added by the next chain launch.
+    const bool chain = C <= kChainCols;
+    const int nrb = int((M + kDwWaves - 1) / kDwWaves);
+    auto rms_chain = [&](const float* x1, const float* r1, const float* w1, const float* dy, float* out1,
+                         const float* add1, float* dw1, const float* x2, const float* r2, const float* w2,
+                         float* out2, float* part2, const float* pin, float* dwp) {
+        RmsChainArgs ra{};
+        ra.x1 = x1; ra.r1 = r1; ra.w1 = w1; ra.dy = dy; ra.out1 = out1; ra.add1 = add1; ra.dw1 = dw1;
+        ra.x2 = x2; ra.r2 = r2; ra.w2 = w2; ra.out2 = out2; ra.add2 = nullptr; ra.part2 = part2;
+        ra.pin = pin; ra.dwp = dwp; ra.npin = nrb;
+        ra.rows = int(M); ra.cols = int(C);
+        return launch_rms_chain(g, ra);
+    };
     DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
     for (int l = c->loops - 1; l >= 0; --l) {
-        DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
-        DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
+        if (chain) {
+            DGM_TRY(rms_chain(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, nullptr, gr->nf, A(l, A_MLP), A(l, A_R2B),
+                              w->n2b, t2, S[B_RPA], nullptr, nullptr));
+        } else {
+            DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
+            DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
+        }
         DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
         if (gu1) {
             DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F, 2 * F));
@@ -1021,9 +1189,18 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));
             DGM_TRY(dgm_acc(g, t2, dln, nC));
         }
-        DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));   // t1 += dx
-        DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
-        DGM_TRY(bwd(w->wo, t2, A(l, A_AV), S[B_DAV], gr->wo, C, C));
+        // t1 += dx of n2; its n1b backward goes to dln (t2 is still being read
+        // by the direct weight-gradient workgroups of the same launch).
+        float* dattn = t2;
+        if (chain) {
+            DGM_TRY(rms_chain(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, t1, gr->n2, A(l, A_ATTN), A(l, A_R1B), w->n1b,
+                              dln, S[B_RPB], S[B_RPA], gr->n2b));
+            dattn = dln;
+        } else {
+            DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));
+            DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
+        }
+        DGM_TRY(bwd(w->wo, dattn, A(l, A_AV), S[B_DAV], gr->wo, C, C));
         DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK], S[B_DV],
                             S[B_DPROBS], S[B_DSCORES], B, T, H, D));
         // sum_heads of dk and dv, rope_bwd of dq and dk, the value-residual
@@ -1041,7 +1218,11 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(bwd(w->wv, S[B_DVPRE], A(l, A_LN1), dln, gr->wv, KV, C));
             DGM_TRY(dgm_acc(g, t2, dln, nC));
         }
-        DGM_TRY(rms_bwd(A(l, A_X), A(l, A_R1), w->n1, t2, gx, gr->n1, t1));   // gx = t1 + dx
+        if (chain)   // gx = t1 + dx, and the pending n1b sums
+            DGM_TRY(rms_chain(A(l, A_X), A(l, A_R1), w->n1, t2, gx, t1, gr->n1, nullptr, nullptr, nullptr, nullptr,
+                              nullptr, S[B_RPB], gr->n1b));
+        else
+            DGM_TRY(rms_bwd(A(l, A_X), A(l, A_R1), w->n1, t2, gx, gr->n1, t1));   // gx = t1 + dx
     }
     return DGM_OK;
 }
