@@ -70,6 +70,33 @@ int dit_forward_train_fused(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weig
 bool dit_linear_follows(const dgm_dit_linear& first, const dgm_dit_linear& next, int64_t rows, int64_t K, int bits,
                         int G);
 
+// SwiGLU backward of one element (metal/kernels.metal:911-918 for the
+// sign-split logistic, 932-949 for the derivative), fp contraction off:
+// dgate = silu'(z) * u * g, dup = silu(z) * g.
+__device__ inline void swiglu_bwd_value(float z, float u, float g, float& dgate, float& dup) {
+#pragma clang fp contract(off)
+    float s;
+    if (z >= 0.0f) {
+        const float e = expf(-z);
+        s = 1.0f / (1.0f + e);
+    } else {
+        const float e = expf(z);
+        s = e / (1.0f + e);
+    }
+    const float silu = z * s;
+    const float siluP = s * (1.0f + z * (1.0f - s));
+    dgate = siluP * u * g;
+    dup = silu * g;
+}
+
+// gemmBwd (dW += dY^T X, dX = dY W) of a linear whose input was
+// SwiGLU(gate, up) [M, K], with the SwiGLU backward applied to dX in the same
+// launch: dgu gets [M, 2K] rows [dgate | dup]. Returns kNotFused, having
+// launched nothing, when the shapes do not fit the one-launch pair.
+int gemm_bwd_swiglu(dgm_gpu* g, int bits, const float* w, const void* q, const float* scale, const float* dy,
+                    const float* x, const float* gate, const float* up, float* dgu, float* dw, int64_t M, int64_t N,
+                    int64_t K, int64_t qGroup);
+
 inline bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }

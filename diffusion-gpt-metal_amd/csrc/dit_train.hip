@@ -41,16 +41,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float silu_sigmoid(float z) {
-    // metal/kernels.metal:911-918 (sign-split logistic)
-    if (z >= 0.0f) {
-        const float e = expf(-z);
-        return 1.0f / (1.0f + e);
-    }
-    const float e = expf(z);
-    return e / (1.0f + e);
-}
-
 constexpr int kDwWaves = 16;
 
 // ---- rmsnorm backward (metal/kernels.metal:827-868), dx and dweight in one launch --
@@ -668,14 +658,8 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* __res
                                                               int64_t n, int64_t F, int64_t ldo) {
     const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
     if (i >= n) return;
-    const float z = gate[i];
-    const float s = silu_sigmoid(z);
-    const float silu = z * s;
-    const float siluP = s * (1.0f + z * (1.0f - s));
-    const float g = dy[i];
     const int64_t o = ldo == F ? i : (i / F) * ldo + i % F;
-    dgate[o] = siluP * up[i] * g;
-    dup[o] = silu * g;
+    dgm::swiglu_bwd_value(gate[i], up[i], dy[i], dgate[o], dup[o]);
 }
 
 // ---- gradients of q / k / v before their projections, one wave per token row ----
@@ -1179,11 +1163,22 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
             DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
         }
-        DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
         if (gu1) {
-            DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F, 2 * F));
+            // wdown's backward with the SwiGLU backward in its dX epilogue,
+            // else the two launches.
+            const int r = dgm::gemm_bwd_swiglu(g, bits, w->wdown.w, w->wdown.q, w->wdown.scale, t2, A(l, A_SW),
+                                               A(l, A_GATE), A(l, A_UP), S[B_DG], gr->wdown, M, C, F,
+                                               bits == 32 ? 8 : G);
+            if (r == dgm::kNotFused) {
+                DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
+                DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F,
+                                          2 * F));
+            } else {
+                DGM_TRY(r);
+            }
             DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, 2 * F, C));
         } else {
+            DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
             DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
             DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, F, C));
             DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));

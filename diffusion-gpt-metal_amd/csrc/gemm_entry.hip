@@ -13,7 +13,8 @@ int gemm_f32_dx(dgm_gpu* g, int bits, const void* W, const float* scale, const f
 int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dgm_GemmP* p,
                 bool accumulate);
 int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, const float* dY, const float* X,
-                      float* dX, float* dW, const dgm_GemmP* p, bool accumulate, bool* fused);
+                      float* dX, float* dW, const dgm_GemmP* p, bool accumulate, bool* fused,
+                      const float* sg_gate = nullptr, const float* sg_up = nullptr);
 }  // namespace dgm
 
 namespace {
@@ -192,3 +193,33 @@ int dgm_gemmBwd(dgm_gpu* g, int64_t bits, const float* w, const void* q, const f
 }
 
 }  // extern "C"
+
+namespace dgm {
+
+int gemm_bwd_swiglu(dgm_gpu* g, int bits, const float* w, const void* q, const float* scale, const float* dy,
+                    const float* x, const float* gate, const float* up, float* dgu, float* dw, int64_t M, int64_t N,
+                    int64_t K, int64_t qGroup) {
+    if (!g) return DGM_ERR_ARG;
+    if (bits != 32 && bits != 8 && bits != 4)
+        return fail(g, DGM_ERR_BITS, "gemmBwd: unsupported bits %d", bits);
+    dgm_GemmP p;
+    int rc = make_p(g, "gemmBwd", M, N, K, 0, qGroup, &p);
+    if (rc) return rc;
+    const char* name = bits == 32 ? "gemm_bwd_f32" : (bits == 8 ? "gemm_bwd_i8" : "gemm_bwd_i4");
+    rc = gemm_check_sizes(g, name, &p, bits);
+    if (rc) return rc;
+    const void* wt = bits == 32 ? static_cast<const void*>(w) : q;
+    if (p.M == 0 || p.N == 0 || p.K == 0) return kNotFused;
+    if (!dgu || !dw || !dy || !x || !wt || !gate || !up || (bits != 32 && !scale))
+        return fail(g, DGM_ERR_ARG, "gemmBwd: null buffer");
+    rc = enter(g, name);
+    if (rc) return rc;
+    bool fused = false;
+    rc = gemm_f32_bwd_pair(g, bits, wt, scale, dy, x, dgu, dw, &p, true, &fused, gate, up);
+    if (rc) return rc;
+    if (!fused) return kNotFused;
+    DGM_LAUNCH_CHECK(g, name);
+    return DGM_OK;
+}
+
+}  // namespace dgm

@@ -39,6 +39,10 @@ struct GemmArgs {
     int G, groups;
     int has_bias;
     int accumulate;       // DW: += instead of =
+    // DX (LDS kernel) only, when set: out gets [rows, 2K] rows [dgate | dup],
+    // the SwiGLU backward of dX against gate / up [rows, K].
+    const float* sg_gate;
+    const float* sg_up;
 };
 
 template <int BITS>
@@ -1091,10 +1095,22 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     }
     const int k = k0 + wave * 16 + r16;
     if (k < K) {
+        if (a.sg_gate) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = i0 + 4 * q4 + r;
-            if (i < a.rows) a.out[size_t(i) * K + k] = acc[r];
+            for (int r = 0; r < 4; ++r) {
+                const int i = i0 + 4 * q4 + r;
+                if (i < a.rows) {
+                    const size_t e = size_t(i) * K + k;
+                    float* o = a.out + size_t(i) * 2 * K + k;
+                    dgm::swiglu_bwd_value(a.sg_gate[e], a.sg_up[e], acc[r], o[0], o[K]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = i0 + 4 * q4 + r;
+                if (i < a.rows) a.out[size_t(i) * K + k] = acc[r];
+            }
         }
     }
 }
@@ -1378,12 +1394,15 @@ int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dg
 
 // dX and dW of one linear as a single launch (gemm_bwd_pair_kernel) when both
 // shapes take the LDS dX kernel and the paired-column dW kernel; *fused tells
-// the caller whether it ran (else it runs gemm_f32_dx and gemm_f32_dw).
+// the caller whether it ran (else it runs gemm_f32_dx and gemm_f32_dw). With
+// sg_gate / sg_up, dX leaves as the SwiGLU backward [dgate | dup] rows.
 int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, const float* dY, const float* X,
-                      float* dX, float* dW, const dgm_GemmP* p, bool accumulate, bool* fused) {
+                      float* dX, float* dW, const dgm_GemmP* p, bool accumulate, bool* fused, const float* sg_gate,
+                      const float* sg_up) {
     *fused = false;
     GemmArgs ax{};
     ax.A = dY; ax.B = W; ax.scale = scale; ax.out = dX;
+    ax.sg_gate = sg_gate; ax.sg_up = sg_up;
     ax.M = p->M; ax.N = p->N; ax.K = p->K;
     ax.rows = p->M; ax.cols = p->K; ax.red = p->N;
     ax.G = bits == 32 ? 1 : int(p->qGroup);
