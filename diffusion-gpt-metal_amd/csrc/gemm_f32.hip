@@ -245,12 +245,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs a) {
 // consecutive tiles sharing an operand strip (rows of X or dY for the
 // forward/dX, columns of X for dW) run on one XCD, so that strip is fetched
 // into one L2 instead of eight.
+// Body of one tile; `blk` is the workgroup's index within its own grid, part
+// 4 * TM * TN floats of LDS.
 template <int MODE, int BITS, int TM, int TN, int PF>
-__global__ __launch_bounds__(kThreads) void gemm_deep_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+__device__ __forceinline__ void deep_tile(const GemmArgs& a, int tiles_i, int tiles_j, int per_xcd, int blk,
+                                          float (*part)[TM * TN]) {
     constexpr int RT = TM / 16, CT = TN / 16;
-    __shared__ float part[4][TM * TN];
-
-    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    const int t = (blk & 7) * per_xcd + (blk >> 3);
     if (t >= tiles_i * tiles_j) return;
     int ti, tj;
     if constexpr (MODE == MODE_DW) {
@@ -420,6 +421,12 @@ __global__ __launch_bounds__(kThreads) void gemm_deep_kernel(GemmArgs a, int til
             *o = v;
         }
     }
+}
+
+template <int MODE, int BITS, int TM, int TN, int PF>
+__global__ __launch_bounds__(kThreads) void gemm_deep_kernel(GemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
+    __shared__ float part[4][TM * TN];
+    deep_tile<MODE, BITS, TM, TN, PF>(a, tiles_i, tiles_j, per_xcd, int(blockIdx.x), part);
 }
 
 template <int MODE, int BITS, int TM, int TN, int PF>
@@ -1245,6 +1252,21 @@ __global__ __launch_bounds__(kThreads) void gemm_bwd_pair_kernel(GemmArgs ax, in
     }
 }
 
+// The same pairing for contractions too long for the LDS dX kernel: 16 x 16
+// deep-prefetch dX tiles (gemm_deep_kernel<MODE_DX, BITS, 16, 16, 12>) beside
+// the paired-column dW tiles.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void gemm_bwd_deep_pair_kernel(GemmArgs ax, int ti, int tj, int per_x,
+                                                                      GemmArgs aw, int tn, int tk, int per_w) {
+    extern __shared__ __align__(16) float4 sm4[];
+    const int nx = 8 * per_x;
+    if (int(blockIdx.x) < nx) {
+        deep_tile<MODE_DX, BITS, 16, 16, 12>(ax, ti, tj, per_x, int(blockIdx.x), reinterpret_cast<float (*)[256]>(sm4));
+    } else {
+        dw_pair_tile(aw, tn, tk, per_w, int(blockIdx.x) - nx, reinterpret_cast<float (*)[2][16][16]>(sm4));
+    }
+}
+
 bool dw_pair_ok(const GemmArgs& a, const void* dY) {
     return a.M > 0 && a.M % 64 == 0 && a.N >= 2 && a.N % 2 == 0 && a.K > 0 && dgm::aligned(dY, 8);
 }
@@ -1413,7 +1435,31 @@ int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, c
     aw.rows = p->N; aw.cols = p->K; aw.red = p->M;
     aw.G = 1; aw.groups = 0;
     aw.accumulate = accumulate;
-    if (!dx_lds_ok(ax, bits, dY, W) || !dw_pair_ok(aw, dY)) return DGM_OK;
+    if (!dw_pair_ok(aw, dY)) return DGM_OK;
+    if (!dx_lds_ok(ax, bits, dY, W)) {
+        // Deep dX tiles beside the dW tiles, where gemm_f32_dx would pick the
+        // 16 x 16 deep kernel (no SwiGLU epilogue there).
+        const bool vec = (p->N % 4) == 0 && aligned(dY, 16);
+        const int64_t t16x32 = int64_t(dgm::ceil_div(ax.rows, 16)) * dgm::ceil_div(ax.cols, 32);
+        if (sg_gate || !deep_ok<MODE_DX>(ax, bits, vec) || t16x32 >= 2 * g->num_cus) return DGM_OK;
+        const int ti = int(dgm::ceil_div(ax.rows, 16)), tj = int(dgm::ceil_div(ax.cols, 16));
+        const int per_x = int((int64_t(ti) * tj + 7) / 8);
+        const int tn = int(dgm::ceil_div(aw.N, 32)), tk = int(dgm::ceil_div(aw.K, 16));
+        const int per_w = int((int64_t(tn) * tk + 7) / 8);
+        const dim3 grid(unsigned(per_x + per_w) * 8u);
+        const size_t lds = 8 * 1024;   // dW tiles: 8 KB; dX tiles: 4 KB
+        if (bits == 32)
+            hipLaunchKernelGGL(gemm_bwd_deep_pair_kernel<32>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x,
+                               aw, tn, tk, per_w);
+        else if (bits == 8)
+            hipLaunchKernelGGL(gemm_bwd_deep_pair_kernel<8>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x,
+                               aw, tn, tk, per_w);
+        else
+            hipLaunchKernelGGL(gemm_bwd_deep_pair_kernel<4>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x,
+                               aw, tn, tk, per_w);
+        *fused = true;
+        return DGM_OK;
+    }
     const size_t lds = dx_lds_bytes(ax.N);   // >= the 8 KB the dW tiles use (N >= 64)
     const void* kern = bits == 32 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<32>)
                        : bits == 8 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<8>)

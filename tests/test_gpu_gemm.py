@@ -285,9 +285,13 @@ def test_gemm_error_paths(gpu, dgm):
 
 # ---- gemmBwd: the gemmDW(+Acc) / gemmDX pair in one launch ---------------------
 
+# One launch with LDS dX tiles (N % 64 == 0, N <= 448, M % 64 == 0), one launch
+# with deep dX tiles (longer N, small dX: (512, 768, 192), (512, 48, 192)), or
+# the two calls ((512, 768, 768): dX large enough for its own launch; M % 64 or
+# N % 16 off).
 BWD_SHAPES = [(512, 192, 768, 32), (512, 768, 192, 32), (512, 48, 192, 32), (512, 192, 192, 32),
-              (64, 64, 128, 16), (128, 448, 64, 32),      # fused (N % 64 == 0, N <= 448, M % 64 == 0)
-              (512, 768, 768, 32), (100, 192, 768, 32), (64, 62, 128, 16)]   # the two calls
+              (64, 64, 128, 16), (128, 448, 64, 32),
+              (512, 768, 768, 32), (100, 192, 768, 32), (64, 62, 128, 16)]
 
 
 @pytest.mark.parametrize("bits", [32, 8, 4])
@@ -315,7 +319,10 @@ def test_gemm_bwd_is_the_pair(gpu, orc, bits, M, N, K, G, acc):
     assert np.array_equal(from_dev(dx1).view(np.uint32), from_dev(dx2).view(np.uint32))
     assert np.array_equal(from_dev(dw1).view(np.uint32), from_dev(dw2).view(np.uint32))
     cpu = 32 if bits == 4 else 16 if bits == 8 else 4    # codes per 16-byte unit of the LDS dX tile
-    fused = N % 64 == 0 and N <= 448 and M % 64 == 0 and K % cpu == 0 and (bits == 32 or G % cpu == 0)
+    lds_pair = N % 64 == 0 and N <= 448 and K % cpu == 0 and (bits == 32 or G % cpu == 0)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    deep_pair = N % 16 == 0 and -(-M // 16) * -(-K // 32) < 2 * cus
+    fused = M % 64 == 0 and (lds_pair or deep_pair)
     assert (name == {32: "gemm_bwd_f32", 8: "gemm_bwd_i8", 4: "gemm_bwd_i4"}[bits]) == fused, name
     # and against float64 products of the dequantized weights
     wq = w if bits == 32 else orc.dequant(host_codes(q), from_dev(s), N, K, G, bits)
