@@ -107,29 +107,33 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_kernel(const float* __r
     }
 }
 
-// ---- two chained rmsnorm backwards in one launch (the DiT backward's pairs) -------
-// Stage 1 is rms_bwd above: out1 = [add1 +] dx of (x1, r1, w1, dy), dweight
-// w1's gradient += sum over rows by the direct workgroups. With x2 set, stage 2
-// takes out1 as its dy: out2 = [add2 +] dx of (x2, r2, w2, out1), computed by
-// the same wave from out1 held in registers (so add1 may alias out1). Stage
-// 2's dweight needs out1 of every row, so each dx workgroup writes the sums
-// over its 16 rows (in row order) to part2[block][cols], and a later launch
-// adds the blocks in order into the gradient: pin / dwp / npin name such
-// pending partial sums, reduced here by their own workgroups. Row arithmetic
-// is rms_bwd's; cols <= 256.
+// ---- chained rmsnorm backwards in one launch (the DiT backward's runs) -----------
+// Stage 0 is rms_bwd above: out = [add +] dx of (x, r, w, dy), its weight
+// gradient dw0 += sum over rows by the direct workgroups. Each further stage
+// takes the previous stage's out as its dy, computed by the same wave from
+// values held in registers (so a stage's add may alias its out). A further
+// stage's weight gradient needs the previous out of every row, so each dx
+// workgroup writes its sums over its 16 rows (in row order) to
+// part[block][cols], and a later launch adds the blocks in order into the
+// gradient: pin[p] / dwp[p] name such pending partial sums (npin blocks),
+// reduced here by their own workgroups. Row arithmetic is rms_bwd's;
+// cols <= 256.
 constexpr int kChainCols = 256;
+constexpr int kChainStages = 3;
+struct RmsStage {
+    const float *x, *r, *w;
+    float* out;
+    const float* add;
+    float* part;   // stages >= 1
+};
 struct RmsChainArgs {
-    const float *x1, *r1, *w1, *dy;
-    float* out1;
-    const float* add1;
-    float* dw1;
-    const float *x2, *r2, *w2;
-    float* out2;
-    const float* add2;
-    float* part2;
-    const float* pin;
-    float* dwp;
-    int npin;
+    const float* dy;
+    RmsStage st[kChainStages];
+    int nst;
+    float* dw0;
+    const float* pin[2];
+    float* dwp[2];
+    int npend, npin;
     int rows, cols, ndx, ndw;
 };
 
@@ -142,93 +146,96 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainAr
     if (blk < a.ndx) {
         const int row = blk * kDwWaves + wave;
         const bool live = row < rows;
-        float o1[NPL];
-        if (live) {
-            const float* xr = a.x1 + size_t(row) * cols;
-            const float* gr = a.dy + size_t(row) * cols;
-            float pt = 0.0f;
+        // Every stage's operands are loaded before the first stage computes,
+        // so the chain waits for one round of loads, not one per stage.
+        float g[NPL];   // the stage's dy, then its out
+        float xv[kChainStages][NPL], wv[kChainStages][NPL], av[kChainStages][NPL], rv[kChainStages];
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int c = lane + 64 * i;
+            g[i] = live && c < cols ? a.dy[size_t(row) * cols + c] : 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < kChainStages; ++s) {
+            const RmsStage& S = a.st[s];
+            const bool on = live && s < a.nst;
+            rv[s] = on ? S.r[row] : 0.0f;
 #pragma unroll
             for (int i = 0; i < NPL; ++i) {
                 const int c = lane + 64 * i;
-                if (c < cols) pt += (gr[c] * a.w1[c]) * xr[c];
-            }
-            const float meanDyX = wave_sum(pt) / float(cols);
-            const float rs = a.r1[row];
-            const float rs3 = rs * rs * rs;
-            float* o = a.out1 + size_t(row) * cols;
-            const float* ad = a.add1 ? a.add1 + size_t(row) * cols : nullptr;
-#pragma unroll
-            for (int i = 0; i < NPL; ++i) {
-                const int c = lane + 64 * i;
-                o1[i] = 0.0f;
-                if (c < cols) {
-                    const float dyhat = gr[c] * a.w1[c];
-                    const float v = rs * dyhat - xr[c] * rs3 * meanDyX;
-                    o1[i] = ad ? ad[c] + v : v;
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < NPL; ++i) {
-                const int c = lane + 64 * i;
-                if (c < cols) o[c] = o1[i];
+                const bool in = on && c < cols;
+                xv[s][i] = in ? S.x[size_t(row) * cols + c] : 0.0f;
+                wv[s][i] = in ? S.w[c] : 0.0f;
+                av[s][i] = in && S.add ? S.add[size_t(row) * cols + c] : 0.0f;
             }
         }
-        if (!a.x2) return;
-        if (live) {
-            const float* xr = a.x2 + size_t(row) * cols;
-            float pt = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NPL; ++i) {
-                const int c = lane + 64 * i;
-                if (c < cols) pt += (o1[i] * a.w2[c]) * xr[c];
-            }
-            const float meanDyX = wave_sum(pt) / float(cols);
-            const float rs = a.r2[row];
-            const float rs3 = rs * rs * rs;
-            float* o = a.out2 + size_t(row) * cols;
-            const float* ad = a.add2 ? a.add2 + size_t(row) * cols : nullptr;
+        for (int s = 0; s < kChainStages; ++s) {
+            if (s >= a.nst) break;
+            const RmsStage& S = a.st[s];
+            if (live) {
+                float pt = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NPL; ++i) {
-                const int c = lane + 64 * i;
-                if (c < cols) {
-                    const float dyhat = o1[i] * a.w2[c];
-                    const float v = rs * dyhat - xr[c] * rs3 * meanDyX;
-                    o[c] = ad ? ad[c] + v : v;
-                    part[wave][c] = o1[i] * xr[c] * rs;
+                for (int i = 0; i < NPL; ++i) {
+                    const int c = lane + 64 * i;
+                    if (c < cols) pt += (g[i] * wv[s][i]) * xv[s][i];
                 }
-            }
-        } else {
-            for (int c = lane; c < cols; c += 64) part[wave][c] = 0.0f;
-        }
-        __syncthreads();
-        for (int c = threadIdx.x; c < cols; c += 64 * kDwWaves) {
-            float tot = 0.0f;
+                const float meanDyX = wave_sum(pt) / float(cols);
+                const float rs = rv[s];
+                const float rs3 = rs * rs * rs;
+                float* o = S.out + size_t(row) * cols;
 #pragma unroll
-            for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][c];
-            a.part2[size_t(blk) * cols + c] = tot;
+                for (int i = 0; i < NPL; ++i) {
+                    const int c = lane + 64 * i;
+                    if (c < cols) {
+                        if (s > 0) part[wave][c] = g[i] * xv[s][i] * rs;   // this stage's dy * xhat
+                        const float dyhat = g[i] * wv[s][i];
+                        const float v = rs * dyhat - xv[s][i] * rs3 * meanDyX;
+                        g[i] = S.add ? av[s][i] + v : v;
+                        o[c] = g[i];
+                    }
+                }
+            } else if (s > 0) {
+                for (int c = lane; c < cols; c += 64) part[wave][c] = 0.0f;
+            }
+            if (s > 0) {
+                __syncthreads();
+                for (int c = threadIdx.x; c < cols; c += 64 * kDwWaves) {
+                    float tot = 0.0f;
+#pragma unroll
+                    for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][c];
+                    S.part[size_t(blk) * cols + c] = tot;
+                }
+                __syncthreads();
+            }
         }
         return;
     }
-    // direct dweight of stage 1 (as rms_bwd), then the pending partial sums.
-    const bool direct = blk < a.ndx + a.ndw;
-    const int c = (direct ? blk - a.ndx : blk - a.ndx - a.ndw) * 64 + lane;
+    // direct weight gradient of stage 0 (as rms_bwd), then the pending partial sums.
+    const int rest = blk - a.ndx;
+    const bool direct = rest < a.ndw;
+    const int pi = direct ? 0 : (rest - a.ndw) / a.ndw;
+    const int c = (direct ? rest : (rest - a.ndw) % a.ndw) * 64 + lane;
     float acc = 0.0f;
     if (c < cols) {
         if (direct) {
+            const float* x = a.st[0].x;
+            const float* r1 = a.st[0].r;
             int r = wave;
             for (; r + 7 * kDwWaves < rows; r += 8 * kDwWaves) {
                 float v[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const int rr = r + u * kDwWaves;
-                    v[u] = a.dy[size_t(rr) * cols + c] * a.x1[size_t(rr) * cols + c] * a.r1[rr];
+                    v[u] = a.dy[size_t(rr) * cols + c] * x[size_t(rr) * cols + c] * r1[rr];
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) acc += v[u];
             }
-            for (; r < rows; r += kDwWaves) acc += a.dy[size_t(r) * cols + c] * a.x1[size_t(r) * cols + c] * a.r1[r];
+            for (; r < rows; r += kDwWaves) acc += a.dy[size_t(r) * cols + c] * x[size_t(r) * cols + c] * r1[r];
         } else {
-            for (int b = wave; b < a.npin; b += kDwWaves) acc += a.pin[size_t(b) * cols + c];
+            const float* pin = a.pin[pi];
+            for (int b2 = wave; b2 < a.npin; b2 += kDwWaves) acc += pin[size_t(b2) * cols + c];
         }
     }
     part[wave][lane] = acc;
@@ -237,7 +244,7 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainAr
         float tot = 0.0f;
 #pragma unroll
         for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][lane];
-        (direct ? a.dw1 : a.dwp)[c] += tot;
+        (direct ? a.dw0 : a.dwp[pi])[c] += tot;
     }
 }
 
@@ -750,13 +757,12 @@ int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w
     return dgm::check_launch(g, "rms_bwd");
 }
 
-// a.ndx / a.ndw are filled in here; a.pin may be null (no pending sums).
+// a.ndx / a.ndw are filled in here.
 int launch_rms_chain(dgm_gpu* g, RmsChainArgs a) {
     if (a.rows == 0 || a.cols == 0) return DGM_OK;
     a.ndx = (a.rows + kDwWaves - 1) / kDwWaves;
     a.ndw = (a.cols + 63) / 64;
-    const int npend = a.pin ? a.ndw : 0;
-    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndw + npend)), dim3(64 * kDwWaves), 0,
+    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndw * (1 + a.npend))), dim3(64 * kDwWaves), 0,
                        g->stream, a);
     return dgm::check_launch(g, "rms_bwd");
 }
@@ -852,10 +858,11 @@ enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_COUNT
 // Backward scratch.
 // B_DG, B_DU back to back hold [M, 2F] rows [dgate | dup] and B_QPRE, B_KPRE,
 // B_DVPRE [M, C + 2 KV] rows [dq | dk | dv] when the linears are fused.
-// B_RPA / B_RPB: per-16-row-block sums of the chained RMSNorm backwards'
-// second-stage weight gradients (n2b, n1b), reduced by the next chain launch.
+// B_RPA / B_RPB / B_RPC: per-16-row-block sums of the chained RMSNorm
+// backwards' later-stage weight gradients (n2b, n1b, nf), reduced by the next
+// chain launch.
 enum { B_T1, B_T2, B_DLN, B_DSW, B_DG, B_DU, B_DAV, B_DQ, B_DK, B_DV, B_DPROBS, B_DSCORES, B_DK1, B_DV1,
-       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_RPA, B_RPB, B_COUNT };
+       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_RPA, B_RPB, B_RPC, B_COUNT };
 
 inline int64_t pad64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
@@ -874,7 +881,8 @@ void bwd_sizes(const dgm_dit_cfg* c, int64_t* b) {
     const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
     const int64_t RP = (M + kDwWaves - 1) / kDwWaves * C;
     const int64_t bv[B_COUNT] = {M * C, M * C, M * C, M * F, M * F, M * F, M * C,  M * C,  M * C, M * C,
-                                 att,   att,   M * KV, M * KV, M * KV, M * C, M * KV, M * KV, RP,    RP};
+                                 att,   att,   M * KV, M * KV, M * KV, M * C, M * KV, M * KV, RP,    RP,
+                                 RP};
     for (int i = 0; i < B_COUNT; ++i) b[i] = pad64(bv[i]);
 }
 
@@ -1139,38 +1147,47 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     const bool gu1 = dgm::dit_linear_follows(w->wgate, w->wup, F, C, bits, G) && gr->wup == gr->wgate + F * C;
     const int64_t QKV = qkv1 ? C + 2 * KV : 0;
     float* const qkvrow = S[B_QPRE];   // [M, C + 2 KV] rows when qkv1
-    // The RMSNorm backwards that follow each other (nf then n2b, n2 then n1b)
-    // run as one chained launch when C <= 256; the second stage's weight
-    // gradient is summed per row block and added by the next chain launch.
+    // The RMSNorm backwards that follow each other run as one chained launch
+    // when C <= 256: nf + n2b, n2 + n1b, and n1 together with the next loop's
+    // nf + n2b. A later stage's weight gradient is summed per row block (RPA:
+    // n2b, RPB: n1b, RPC: nf) and added by the next chain launch.
     const bool chain = C <= kChainCols;
     const int nrb = int((M + kDwWaves - 1) / kDwWaves);
-    auto rms_chain = [&](const float* x1, const float* r1, const float* w1, const float* dy, float* out1,
-                         const float* add1, float* dw1, const float* x2, const float* r2, const float* w2,
-                         float* out2, float* part2, const float* pin, float* dwp) {
+    auto stage = [](const float* x, const float* r, const float* wt, float* out, const float* add, float* part) {
+        RmsStage st{};
+        st.x = x; st.r = r; st.w = wt; st.out = out; st.add = add; st.part = part;
+        return st;
+    };
+    auto run_chain = [&](const float* dy, float* dw0, int nst, const RmsStage* st, int npend, const float* pin0,
+                         float* dwp0, const float* pin1, float* dwp1) {
         RmsChainArgs ra{};
-        ra.x1 = x1; ra.r1 = r1; ra.w1 = w1; ra.dy = dy; ra.out1 = out1; ra.add1 = add1; ra.dw1 = dw1;
-        ra.x2 = x2; ra.r2 = r2; ra.w2 = w2; ra.out2 = out2; ra.add2 = nullptr; ra.part2 = part2;
-        ra.pin = pin; ra.dwp = dwp; ra.npin = nrb;
-        ra.rows = int(M); ra.cols = int(C);
+        ra.dy = dy; ra.dw0 = dw0; ra.nst = nst;
+        for (int i = 0; i < nst; ++i) ra.st[i] = st[i];
+        ra.npend = npend; ra.pin[0] = pin0; ra.dwp[0] = dwp0; ra.pin[1] = pin1; ra.dwp[1] = dwp1;
+        ra.npin = nrb; ra.rows = int(M); ra.cols = int(C);
         return launch_rms_chain(g, ra);
     };
     DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
-    for (int l = c->loops - 1; l >= 0; --l) {
-        if (chain) {
-            DGM_TRY(rms_chain(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, nullptr, gr->nf, A(l, A_MLP), A(l, A_R2B),
-                              w->n2b, t2, S[B_RPA], nullptr, nullptr));
-        } else {
+    const int L = c->loops;
+    float* dmlp = t2;   // dL/dmlp of the loop about to run
+    if (chain && L > 0) {
+        const RmsStage st[2] = {stage(A(L - 1, A_PRE), A(L - 1, A_RF), w->nf, t1, nullptr, nullptr),
+                                stage(A(L - 1, A_MLP), A(L - 1, A_R2B), w->n2b, t2, nullptr, S[B_RPA])};
+        DGM_TRY(run_chain(gx, gr->nf, 2, st, 0, nullptr, nullptr, nullptr, nullptr));
+    }
+    for (int l = L - 1; l >= 0; --l) {
+        if (!chain) {
             DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
             DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
         }
         if (gu1) {
             // wdown's backward with the SwiGLU backward in its dX epilogue,
             // else the two launches.
-            const int r = dgm::gemm_bwd_swiglu(g, bits, w->wdown.w, w->wdown.q, w->wdown.scale, t2, A(l, A_SW),
+            const int r = dgm::gemm_bwd_swiglu(g, bits, w->wdown.w, w->wdown.q, w->wdown.scale, dmlp, A(l, A_SW),
                                                A(l, A_GATE), A(l, A_UP), S[B_DG], gr->wdown, M, C, F,
                                                bits == 32 ? 8 : G);
             if (r == dgm::kNotFused) {
-                DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
+                DGM_TRY(bwd(w->wdown, dmlp, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
                 DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F,
                                           2 * F));
             } else {
@@ -1178,7 +1195,7 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             }
             DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, 2 * F, C));
         } else {
-            DGM_TRY(bwd(w->wdown, t2, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
+            DGM_TRY(bwd(w->wdown, dmlp, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
             DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
             DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, F, C));
             DGM_TRY(bwd(w->wup, S[B_DU], A(l, A_LN2), dln, gr->wup, F, C));
@@ -1188,8 +1205,12 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         // by the direct weight-gradient workgroups of the same launch).
         float* dattn = t2;
         if (chain) {
-            DGM_TRY(rms_chain(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, t1, gr->n2, A(l, A_ATTN), A(l, A_R1B), w->n1b,
-                              dln, S[B_RPB], S[B_RPA], gr->n2b));
+            const RmsStage st[2] = {stage(A(l, A_MID), A(l, A_R2), w->n2, t1, t1, nullptr),
+                                    stage(A(l, A_ATTN), A(l, A_R1B), w->n1b, dln, nullptr, S[B_RPB])};
+            if (l == L - 1)   // nf's gradient was direct in the first chain
+                DGM_TRY(run_chain(t2, gr->n2, 2, st, 1, S[B_RPA], gr->n2b, nullptr, nullptr));
+            else
+                DGM_TRY(run_chain(t2, gr->n2, 2, st, 2, S[B_RPA], gr->n2b, S[B_RPC], gr->nf));
             dattn = dln;
         } else {
             DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));
@@ -1213,11 +1234,23 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(bwd(w->wv, S[B_DVPRE], A(l, A_LN1), dln, gr->wv, KV, C));
             DGM_TRY(dgm_acc(g, t2, dln, nC));
         }
-        if (chain)   // gx = t1 + dx, and the pending n1b sums
-            DGM_TRY(rms_chain(A(l, A_X), A(l, A_R1), w->n1, t2, gx, t1, gr->n1, nullptr, nullptr, nullptr, nullptr,
-                              nullptr, S[B_RPB], gr->n1b));
-        else
+        if (chain) {
+            // gx = t1 + dx of n1 (and the pending n1b sums); below loop 0 the
+            // next loop's nf and n2b backwards follow in the same launch, its
+            // dL/dmlp going to dln (t2 is read by the direct workgroups).
+            if (l > 0) {
+                const RmsStage st[3] = {stage(A(l, A_X), A(l, A_R1), w->n1, gx, t1, nullptr),
+                                        stage(A(l - 1, A_PRE), A(l - 1, A_RF), w->nf, t1, nullptr, S[B_RPC]),
+                                        stage(A(l - 1, A_MLP), A(l - 1, A_R2B), w->n2b, dln, nullptr, S[B_RPA])};
+                DGM_TRY(run_chain(t2, gr->n1, 3, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr));
+                dmlp = dln;
+            } else {
+                const RmsStage st[1] = {stage(A(l, A_X), A(l, A_R1), w->n1, gx, t1, nullptr)};
+                DGM_TRY(run_chain(t2, gr->n1, 1, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr));
+            }
+        } else {
             DGM_TRY(rms_bwd(A(l, A_X), A(l, A_R1), w->n1, t2, gx, gr->n1, t1));   // gx = t1 + dx
+        }
     }
     return DGM_OK;
 }
