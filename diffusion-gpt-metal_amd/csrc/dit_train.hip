@@ -702,7 +702,23 @@ __global__ __launch_bounds__(kThreads) void qkv_grad_kernel(const float* __restr
     for (int d = lane; d < D; d += 64) {
         const int pd = d < mid ? d + mid : d - mid;
         float a = 0.0f, b = 0.0f, v = 0.0f;
-        for (int h = 0; h < H; ++h) {
+        int h = 0;
+        for (; h + 4 <= H; h += 4) {   // loads of four heads in flight, sums in head order
+            float ka[4], kb[4], vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                ka[u] = kr[(h + u) * D + d];
+                kb[u] = kr[(h + u) * D + pd];
+                vv[u] = vr[(h + u) * D + d];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                a += ka[u];
+                b += kb[u];
+                v += vv[u];
+            }
+        }
+        for (; h < H; ++h) {
             a += kr[h * D + d];
             b += kr[h * D + pd];
             v += vr[h * D + d];
