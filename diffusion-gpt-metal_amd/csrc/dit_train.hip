@@ -10,18 +10,22 @@
 //    fp32, a different order than the reference's sequential loop) and
 //    dweight (16 waves per 64 columns, partial sums added in wave order, then
 //    into dweight: the weight is shared by every loop) in one launch, dx
-//    optionally added to a residual gradient.
-//  * attention backward: one workgroup per (batch, head) with the head in
-//    LDS (T and D multiples of 4, (4TD + 2T^2) floats of LDS), or the
-//    reference's five passes with one lane per output; both sum in the
-//    reference's order and are bitwise the oracle's.
+//    optionally added to a residual gradient; rms_bwd_chain runs up to three
+//    of them back to back per row (the block backward's consecutive norms).
+//  * attention backward: for T % 8 == 0 two launches over 8-row blocks of
+//    each head (query rows: dP, dS, dQ; key rows: dV, dK); else one workgroup
+//    per (batch, head) with the head in LDS (T and D multiples of 4,
+//    (4TD + 2T^2) floats of LDS), or the reference's five passes with one lane
+//    per output. All sum in the reference's order and are bitwise the
+//    oracle's.
 //  * rope_bwd, swiglu_bwd, sum_heads, acc_f, acc_scale_f: elementwise;
 //    qkv_grad: sum_heads, rope_bwd and the value-residual steps of the q / k /
 //    v gradients in one launch, one wave per token row.
 //  * swiglu_bwd and qkv_grad can write [dgate | dup] and [dq | dk | dv] rows,
 //    the output gradient of the stacked [gate; up] and [q; k; v] linears.
 // The block's GEMMs are the library's: dgm_gemmNT and dgm_gemmBwd (gemmDWAcc +
-// gemmDX in one launch) on the fp32 masters (bits 32, as the reference's DiT) or on
+// gemmDX in one launch; for wdown with the SwiGLU backward applied to its dX,
+// dgm::gemm_bwd_swiglu) on the fp32 masters (bits 32, as the reference's DiT) or on
 // the group-quantized codes (bits 8 / 4: forward on the codes, dX through the
 // dequantized codes, dW into the fp32 master gradient: the straight-through
 // estimator of src/GPT.swift's backward).
