@@ -147,6 +147,38 @@ def test_small_block_backward(gpu, dgm, orc, bits, group):
     _check_block(blk, dgm, xg, gg, xo, gx, gw, gn)
 
 
+def test_block_backward_separate_grads(gpu, dgm, orc):
+    """Linear gradients in separate buffers: the backward takes the per-linear
+    path instead of the stacked [wq; wk; wv] / [wgate; wup] weight backwards."""
+    import torch
+    cfg = dgm.DiTConfig(B=2, T=16, C=64, F=128, H=4, D=16, loops=3, group=16, bits=8)
+    shapes, masters, norms, x0, gy = _block_case(dgm, orc, cfg, 77)
+    blk = dgm.DiTBlock(gpu, cfg, {**{n: to_dev(v) for n, v in masters.items()},
+                                  **{n: to_dev(v) for n, v in norms.items()}})
+    blk.zero_grads()
+    for n in dgm.DIT_LINEARS:
+        blk.grads[n] = torch.zeros_like(blk.grads[n]).clone()
+    blk.c_grads = type(blk.c_grads)(*[blk.grads[n].data_ptr() for n in dgm.DIT_LINEARS],
+                                    *[blk.grads[n].data_ptr() for n in dgm.DIT_NORMS])
+    x, g = to_dev(x0), to_dev(gy)
+    gpu.begin()
+    blk.forward_train(x)
+    blk.backward(g)
+    gpu.end()
+    ocfg = orc.DiTCfg(B=cfg.B, T=cfg.T, C=cfg.C, F=cfg.F, H=cfg.H, D=cfg.D, loops=cfg.loops, group=cfg.group,
+                      bits=cfg.bits, eps=cfg.eps, theta=cfg.theta, mix=cfg.mix)
+    lin = {n: (from_dev(blk.codes[n]).view(np.int8), from_dev(blk.scales[n])) for n in dgm.DIT_LINEARS}
+    xo, gx, gw, gn = orc.dit_train(ocfg, lin, norms, x0, gy)
+    _check_block(blk, dgm, from_dev(x), from_dev(g), xo, gx, gw, gn)
+
+
+def test_wide_block_backward(gpu, dgm, orc):
+    """C = 320 > 256: the RMSNorm backwards run one launch each (no chains)."""
+    cfg = dgm.DiTConfig(B=2, T=16, C=320, F=128, H=4, D=80, loops=2, group=16, bits=8)
+    blk, xg, gg, xo, gx, gw, gn, _ = _run_block(gpu, dgm, orc, cfg, 31)
+    _check_block(blk, dgm, xg, gg, xo, gx, gw, gn)
+
+
 def test_forward_train_matches_forward(gpu, dgm, orc):
     """The saving forward and the fused forward give the same xs[loops] (1e-5)."""
     cfg = dgm.DiTConfig()
