@@ -214,6 +214,10 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
             // (a __syncthreads here would also wait for those).
             asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + CB + 2) : "memory");
         }
+        // The last steps' clamped loads (re-reads of the last step, never
+        // consumed) land before the wave ends: no direct-to-LDS write may
+        // outlive the workgroup's LDS.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
     }
 
