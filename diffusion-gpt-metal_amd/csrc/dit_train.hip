@@ -462,7 +462,9 @@ __global__ __launch_bounds__(kAbThreads) void attn_bwd_fused_kernel(AttnBwdArgs 
 constexpr int kAsThreads = 1024;
 constexpr int kAsRows = 8;
 
-size_t attn_split_rows_lds(int T, int D) { return size_t(2 * kAsRows * T + kAsRows * D + 2 * T * D) * sizeof(float); }
+size_t attn_split_rows_lds(int T, int D) {
+    return size_t(2 * kAsRows * T + kAsRows * D + (2 * T + 1) * D) * sizeof(float);
+}
 size_t attn_split_keys_lds(int T, int D) { return size_t(2 * kAsRows * T + 2 * T * D) * sizeof(float); }
 
 // out(r, c, v) for r < rows, c < cols, v = sum_k A(r, k) * B(k, c); one output per thread.
@@ -495,8 +497,8 @@ __global__ __launch_bounds__(kAsThreads) void attn_bwd_rows_kernel(AttnBwdArgs a
     const int b = bh / H, h = bh % H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float* Gr = lds;                 // dO rows [kAsRows][D]
-    float* Vt = Gr + kAsRows * D;    // [D][T]
-    float* Kf = Vt + T * D;          // [T][D]
+    float* Vt = Gr + kAsRows * D;    // [D][T + 1] (padded: the transposing stores spread over the banks)
+    float* Kf = Vt + (T + 1) * D;    // [T][D]
     float* Pr = Kf + T * D;          // P rows [kAsRows][T]
     float* S = Pr + kAsRows * T;     // dP, then dS rows [kAsRows][T]
     const int64_t row_stride = int64_t(H) * D;
@@ -516,10 +518,10 @@ __global__ __launch_bounds__(kAsThreads) void attn_bwd_rows_kernel(AttnBwdArgs a
         if (i < np) pp = reinterpret_cast<const float4*>(a.probs + pm0)[i];
         if (i < nkv) {
             *reinterpret_cast<float4*>(Kf + t * D + c) = kk;
-            Vt[(c + 0) * T + t] = vv.x;
-            Vt[(c + 1) * T + t] = vv.y;
-            Vt[(c + 2) * T + t] = vv.z;
-            Vt[(c + 3) * T + t] = vv.w;
+            Vt[(c + 0) * (T + 1) + t] = vv.x;
+            Vt[(c + 1) * (T + 1) + t] = vv.y;
+            Vt[(c + 2) * (T + 1) + t] = vv.z;
+            Vt[(c + 3) * (T + 1) + t] = vv.w;
         }
         if (i < ng) *reinterpret_cast<float4*>(Gr + t * D + c) = gg;
         if (i < np) reinterpret_cast<float4*>(Pr)[i] = pp;
@@ -527,7 +529,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_bwd_rows_kernel(AttnBwdArgs a
     __syncthreads();
     // dP[t][s] = sum_d dO[t][d] V[s][d]
     split_product(
-        kAsRows, T, D, [&](int r, int d) { return Gr[r * D + d]; }, [&](int d, int s) { return Vt[d * T + s]; },
+        kAsRows, T, D, [&](int r, int d) { return Gr[r * D + d]; }, [&](int d, int s) { return Vt[d * (T + 1) + s]; },
         [&](int r, int s, float v) {
             S[r * T + s] = v;
             a.dprobs[pm0 + r * T + s] = v;
