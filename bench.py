@@ -1,40 +1,51 @@
 """Benchmark of the group-quantized linear path on one MI355X.
 
-Headline ("c2"): one step = the int4 group-quant
-linear forward plus its STE backward on the DiT down-projection shape,
-X[512,768] ~ N(0,1), W[192,768] ~ N(0,0.02) int4 G=32, dY ~ N(0,1e-3):
-    Y  = X deq(W)^T   (gemmNT, gemm_nt_i4)
-    dW = dY^T X       (gemmBwd: the reference's gemmDW + gemmDX pair,
-    dX = dY deq(W)     one launch, bitwise the two calls)
-Inputs are resident in HBM before timing; the weights are quantized once
-before the timed region. value = algorithmic flop of the step / step time.
-The per-kernel times of the separate gemm_dx_i4 and gemm_dw calls are
-reported beside it.
+Headline: BASELINE.json's largest configuration, c5 — the prefill-shaped int4
+group-quant GEMM forward, M=8192, K=4096, N=14336, G=128, on bf16 MFMA with
+the weights dequantized to bf16 in LDS and fp32 accumulation:
+    X[8192,4096] ~ N(0,1) fp32,  W[14336,4096] ~ N(0,0.02) -> int4 codes + fp32
+    scales (quantized once, before the timed region),  Y = X deq(W)^T fp32.
+One step = one gemmNT call (the reference's GPU.gemmNT, src/GPU.swift:227-243)
+with inputs resident in HBM. value = 2*M*N*K / (wall time of the K timed
+steps / K), in TFLOP/s.
 
-Every GPU timing replays a captured HIP graph of the launches (through
-torch.cuda.CUDAGraph), so host-side call overhead never leaks into kernel
-times; HIP events on the launch stream bracket the replay.
+The same JSON line carries:
+  * `roofline`: the dominant kernel (the only kernel of the headline call),
+    algorithmic flop per launch / its average launch duration from HIP events
+    recorded on the launch stream around every timed step, against the dense
+    bf16 MFMA peak; `traffic` = HBM bytes per launch from rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json), each scaled by the
+    counter's reading for a plain copy of known size;
+  * `cpu_baseline`: the reference's scalar CPU path (src/Check.swift:433-494:
+    dequant, then cpuGemmNT), restated in C (oracle/oracle.c, -O2
+    -ffp-contract=off), one thread pinned to one core, on a contiguous slice
+    of N (cost is linear in N; the rate is extrapolated and the slice named);
+  * `hbm_ceiling`: a measured stream copy (512 MiB each way) on this GPU;
+  * `workloads`: every other configuration (c1, c2 step, c3 forward and
+    training step, c4 M = 1/16/64 in both math modes, c5 int8, quantization,
+    AdamW + re-quantization, embed_bwd), each with its own roofline, traffic
+    and one-core CPU baseline.
 
-The JSON line also carries `roofline` (dominant kernel of the step),
-`cpu_baseline` (the reference's scalar CPU path restated in C, one thread,
-bounded sample) and `workloads` (the other configs, each with its own
-roofline: c1 int8 forward, quantization at the c4/c5 weight shape, c4
-decode-shaped int4 with weight copies rotated past the 256 MB Infinity
-Cache, c5 prefill, c3 DiT block forward).
+GPU timings of the short workloads replay a captured HIP graph of many
+launches (through torch.cuda.CUDAGraph) so host overhead never leaks into
+kernel times; HIP events on the launch stream bracket the replay.
 
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extra] [--skip-cpu]
                   [--only name,name] [--calib-copy]
+  python bench.py --list                              workload names
   python bench.py --summarize DIR [--title TEXT]      rocprofv3 csv -> markdown
   python bench.py --traffic NAME FETCH_DIR WRITE_DIR  PMC runs -> profiles/traffic.json
 """
 from __future__ import annotations
 
 import argparse
+import contextlib
 import csv
 import importlib.util
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -46,6 +57,12 @@ METRIC = "group-quant GEMM GB/s & TFLOP/s (% of MI355X roofline); DiT block fwd 
 # MI355X published peaks (dense).
 PEAK = {"hbm_GBps": 8000.0, "fp32_TFLOPs": 157.3, "bf16_TFLOPs": 2500.0, "int8_TOPs": 5000.0}
 CALIB_BYTES = 256 * 2 ** 20   # plain copy kernel used to scale FETCH_SIZE / WRITE_SIZE
+CEIL_BYTES = 512 * 2 ** 20    # stream-copy ceiling leg
+
+C5 = dict(M=8192, N=14336, K=4096, G=128)
+C4 = dict(N=14336, K=4096, G=128)
+C2 = dict(M=512, N=192, K=768, G=32)
+C1 = dict(M=512, N=768, K=192, G=32)
 
 
 def load_package():
@@ -92,6 +109,14 @@ class Bench:
         self.gpu.end()
         return q, s
 
+    @contextlib.contextmanager
+    def math(self, mode: int):
+        self.gpu.set_math(mode)
+        try:
+            yield
+        finally:
+            self.gpu.set_math(self.dgm.DGM_MATH_FP32)
+
     def capture(self, fn, calls: int):
         """A CUDA graph of `calls` invocations fn(0..calls-1). fn runs eagerly
         first, so workspaces exist before capture (no allocation in a graph)."""
@@ -133,6 +158,31 @@ class Bench:
         del g
         return ms
 
+    def time_steps(self, fn, steps: int, warmup: int) -> dict:
+        """Eager calls: `warmup` untimed, then exactly `steps` timed between two
+        device synchronizations, with a HIP event on the launch stream before
+        and after every step. Returns the wall time per step and the event
+        duration of every step."""
+        t = self.torch
+        self.sync()
+        self.gpu.begin()
+        for i in range(warmup):
+            fn(i)
+        self.gpu.end()
+        ev = [t.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        self.sync()
+        t0 = time.perf_counter()
+        self.gpu.begin()
+        ev[0].record(self.stream)
+        for i in range(steps):
+            fn(i)
+            ev[i + 1].record(self.stream)
+        self.gpu.end()
+        self.sync()
+        wall = time.perf_counter() - t0
+        per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+        return {"wall_ms_per_step": wall * 1e3 / steps, "event_ms": per}
+
 
 def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
     return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
@@ -149,73 +199,54 @@ def load_traffic() -> dict:
     return {}
 
 
-def traffic_for(workload: str, kernel_key: str):
+def traffic_for(workload: str, kernel_keys) -> object:
+    """Counted HBM bytes per call: the sum over the call's kernels (names
+    matched by substring), or None when the workload was not profiled."""
     ent = load_traffic().get(workload, {})
-    for name, rec in ent.items():
-        if kernel_key in name:
-            return rec.get("total_bytes")
-    return None
+    total, found = 0, False
+    for key in kernel_keys:
+        for name, rec in ent.items():
+            if not name.startswith("_") and key in name:
+                total += rec.get("total_bytes", 0)
+                found = True
+                break
+    return total if found else None
 
 
-# ---- headline: c2 step -------------------------------------------------------
-
-C2 = dict(M=512, N=192, K=768, G=32, bits=4)
+# ---- the reference's scalar CPU path, one core ---------------------------------
 
 
-def c2_setup(b: Bench):
-    M, N, K, G = C2["M"], C2["N"], C2["K"], C2["G"]
-    x, w, dy = b.randn(M * K, 1.0), b.randn(N * K, 0.02), b.randn(M * N, 1e-3)
-    q, s = b.quantized(w, N, K, G, 4)
-    y, dx, dw = b.zeros(M * N), b.zeros(M * K), b.zeros(N * K)
-    g = b.gpu
-    return {
-        "gemm_nt_i4": lambda i: g.gemmNT(4, None, q, s, x, None, y, M, N, K, G),
-        "gemm_bwd_i4": lambda i: g.gemmBwd(4, None, q, s, dy, x, dx, dw, M, N, K, G),
-        "gemm_dx_i4": lambda i: g.gemmDX(4, None, q, s, dy, dx, M, N, K, G),
-        "gemm_dw": lambda i: g.gemmDW(dy, x, dw, M, N, K),
-    }
-
-
-def c2_flops() -> int:
-    return 3 * 2 * C2["M"] * C2["N"] * C2["K"]
-
-
-def c2_bytes() -> dict:
-    M, N, K, G = C2["M"], C2["N"], C2["K"], C2["G"]
-    q, s = N * K // 2, N * (K // G) * 4
-    return {"gemm_nt_i4": q + s + 4 * (M * K + M * N), "gemm_dx_i4": q + s + 4 * (M * N + M * K),
-            "gemm_dw": 4 * (M * K + M * N + N * K),
-            "gemm_bwd_i4": q + s + 4 * (M * N + M * K + M * K + N * K)}
-
-
-def cpu_baseline_c2(budget_s: float = 12.0) -> dict:
-    """The reference's scalar CPU path (Check.swift:399-494 restated in C,
-    kernel orders of metal/kernels.metal:180-283), single thread, timed on
-    whole c2 steps until ~budget_s of CPU work."""
-    import numpy as np
+def _oracle():
     if REPO not in sys.path:
         sys.path.insert(0, REPO)
     from oracle import oracle as orc
-    M, N, K, G = C2["M"], C2["N"], C2["K"], C2["G"]
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal(M * K, dtype=np.float32)
-    w = (rng.standard_normal(N * K, dtype=np.float32) * np.float32(0.02))
-    dy = (rng.standard_normal(M * N, dtype=np.float32) * np.float32(1e-3))
-    q, s = orc.quant(w, N, K, G, 4)
-    steps, t0 = 0, time.perf_counter()
+    return orc
+
+
+@contextlib.contextmanager
+def one_core():
+    """Pins the calling thread to one core (the first this process may use)
+    for the CPU leg, and restores the previous affinity afterwards. The GPU
+    runtime's own threads are not affected."""
+    prev = os.sched_getaffinity(0)
+    core = min(prev)
+    os.sched_setaffinity(0, {core})
+    try:
+        yield core
+    finally:
+        os.sched_setaffinity(0, prev)
+
+
+def cpu_time(fn, budget_s: float, max_calls: int = 1000) -> tuple:
+    """Calls fn until budget_s of CPU time has passed (at least once); returns
+    (seconds per call, calls)."""
+    calls, t0 = 0, time.perf_counter()
     while True:
-        orc.gemm_nt_q(q, s, x, None, M, N, K, G, 4)
-        orc.gemm_dx_q(q, s, dy, M, N, K, G, 4)
-        orc.gemm_dw(dy, x, M, N, K)
-        steps += 1
+        fn()
+        calls += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 50:
-            break
-    per_step = el / steps
-    return {"value": round(c2_flops() / per_step / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{steps} full c2 steps (gemm_nt_i4 kernel order + gemm_dx_i4 + gemm_dw), "
-                      f"{per_step * 1e3:.1f} ms/step, oracle/oracle.c -O2 -ffp-contract=off, 1 thread",
-            "host_cpu": _cpu_model(), "host_nproc": os.cpu_count()}
+        if el >= budget_s or calls >= max_calls:
+            return el / calls, calls
 
 
 def _cpu_model() -> str:
@@ -229,41 +260,310 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-# ---- other configs -------------------------------------------------------------
+def cpu_record(value: float, unit: str, core: int, sample: str) -> dict:
+    return {"value": round(value, 6), "unit": unit, "cores": 1, "kind": "port", "sample": sample,
+            "pinned_core": core, "host_cpu": _cpu_model(), "host_nproc": os.cpu_count()}
 
 
-def bench_c1(b: Bench, reps: int) -> dict:
-    M, N, K, G = 512, 768, 192, 32
+def cpu_gemm_slice(M: int, N: int, K: int, G: int, bits: int, n_slice: int, budget_s: float) -> dict:
+    """dequant + cpuGemmNT (src/Check.swift:433-494) of the first n_slice output
+    columns of an [M,K] x [N,K]^T forward; the cost is linear in N, so the
+    rate of the slice is the rate of the whole."""
+    import numpy as np
+    orc = _oracle()
+    rng = np.random.default_rng(0)
+    n = min(n_slice, N)
+    x = rng.standard_normal(M * K, dtype=np.float32)
+    w = rng.standard_normal(n * K, dtype=np.float32) * np.float32(0.02)
+    q, s = orc.quant(w, n, K, G, bits)
+
+    def run():
+        wd = orc.dequant(q, s, n, K, G, bits)
+        orc.gemm_nt(x, wd, None, M, n, K)
+
+    with one_core() as core:
+        per, calls = cpu_time(run, budget_s, 50)
+    flops = 2.0 * M * n * K
+    what = "all of N" if n == N else f"N-slice {n} of {N} (cost linear in N; rate extrapolated)"
+    return cpu_record(flops / per / 1e12, "TFLOP/s", core,
+                      f"M={M} K={K} int{bits} G={G}, {what}: {calls} call(s) of dequant + cpuGemmNT, "
+                      f"{per:.3f} s/call, oracle/oracle.c -O2 -ffp-contract=off, 1 thread")
+
+
+# ---- workloads -------------------------------------------------------------------
+
+
+def bench_c5(b: Bench, bits: int, steps: int, warmup: int, cpu: bool) -> dict:
+    """c5: prefill-shaped int4/int8 forward on bf16 MFMA (DGM_MATH_BF16)."""
+    M, N, K, G = C5["M"], C5["N"], C5["K"], C5["G"]
+    w = b.randn(N * K, 0.02)
+    q, s = b.quantized(w, N, K, G, bits)
+    del w
+    x = b.randn(M * K, 1.0)
+    y = b.zeros(M * N)
+    with b.math(b.dgm.DGM_MATH_BF16):
+        r = b.time_steps(lambda i: b.gpu.gemmNT(bits, None, q, s, x, None, y, M, N, K, G), steps, warmup)
+    flops = 2 * M * N * K
+    ev = r["event_ms"]
+    med, mean = statistics.median(ev), sum(ev) / len(ev)
+    nbytes = N * K // (2 if bits == 4 else 1) + N * (K // G) * 4 + 4 * (M * K + M * N)
+    kernels = [f"gemm_bf16_kernel<{bits}>"]
+    roof = roofline(flops / mean / 1e9, PEAK["bf16_TFLOPs"], "TFLOP/s", "mfma",
+                    traffic_for(f"c5_int{bits}", kernels))
+    roof.update({"kernel": f"gemm_nt_i{bits}", "device_kernels": kernels, "avg_launch_us": round(mean * 1e3, 3),
+                 "algorithmic_flop": flops, "algorithmic_bytes": nbytes})
+    out = {"kernel": f"gemm_nt_i{bits}", "math": "bf16", "shape": f"M=8192 K=4096 N=14336 int{bits} G=128",
+           "steps": steps, "us_wall_per_step": round(r["wall_ms_per_step"] * 1e3, 3),
+           "us_median": round(med * 1e3, 3), "us_mean": round(mean * 1e3, 3),
+           "us_min": round(min(ev) * 1e3, 3), "us_max": round(max(ev) * 1e3, 3),
+           "TFLOPs": round(flops / r["wall_ms_per_step"] / 1e9, 3),
+           "TFLOPs_median": round(flops / med / 1e9, 3), "roofline": roof}
+    if cpu:
+        log(f"[bench] c5 int{bits}: cpu baseline")
+        out["cpu_baseline"] = cpu_gemm_slice(M, N, K, G, bits, 256, 8.0)
+    return out
+
+
+def bench_c4(b: Bench, reps: int, M: int, math_mode: int, cpu: bool) -> dict:
+    """Decode-shaped int4: K=4096, N=14336, G=128. Weight copies are rotated so
+    that successive launches never find W in the 256 MB Infinity Cache."""
+    N, K, G = C4["N"], C4["K"], C4["G"]
+    wq_bytes = N * K // 2 + N * (K // G) * 4
+    copies = max(2, -(-512 * 2 ** 20 // wq_bytes))
+    w = b.randn(N * K, 0.02)
+    q0, s0 = b.quantized(w, N, K, G, 4)
+    del w
+    Q = [q0] + [q0.clone() for _ in range(copies - 1)]
+    S = [s0] + [s0.clone() for _ in range(copies - 1)]
+    x = b.randn(M * K, 1.0)
+    y = b.zeros(M * N)
+    with b.math(math_mode):
+        ms = b.time_launches(lambda i: b.gpu.gemmNT(4, None, Q[i % copies], S[i % copies], x, None, y,
+                                                    M, N, K, G), reps)
+    flops = 2 * M * N * K
+    nbytes = wq_bytes + 4 * (M * K + M * N)
+    mode = "fp32" if math_mode == b.dgm.DGM_MATH_FP32 else "bf16"
+    del Q, S
+    name = f"c4_int4_m{M}_{mode}"
+    out = {"kernel": "gemm_nt_i4", "math": mode, "shape": f"M={M} K=4096 N=14336 int4 G=128",
+           "us": round(ms * 1e3, 3), "GBps": round(nbytes / ms / 1e6, 2),
+           "TFLOPs": round(flops / ms / 1e9, 3), "weight_copies_rotated": copies,
+           "algorithmic_bytes": nbytes,
+           "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
+                                traffic_for(name, ["skinny", "tiled", "decode", "gemv"]))}
+    if cpu:
+        # The reference's CPU path does the same work at any M per output
+        # column; time a slice of N sized to about a second.
+        out["cpu_baseline"] = cpu_gemm_slice(M, N, K, G, 4, N if M == 1 else max(256, 16384 // M), 1.5)
+        out["cpu_baseline"]["unit"] = "TFLOP/s"
+    return out
+
+
+def c2_parts(b: Bench):
+    M, N, K, G = C2["M"], C2["N"], C2["K"], C2["G"]
+    x, w, dy = b.randn(M * K, 1.0), b.randn(N * K, 0.02), b.randn(M * N, 1e-3)
+    q, s = b.quantized(w, N, K, G, 4)
+    y, dx, dw = b.zeros(M * N), b.zeros(M * K), b.zeros(N * K)
+    g = b.gpu
+    return {
+        "gemm_nt_i4": lambda i: g.gemmNT(4, None, q, s, x, None, y, M, N, K, G),
+        "gemm_bwd_i4": lambda i: g.gemmBwd(4, None, q, s, dy, x, dx, dw, M, N, K, G),
+        "gemm_dx_i4": lambda i: g.gemmDX(4, None, q, s, dy, dx, M, N, K, G),
+        "gemm_dw": lambda i: g.gemmDW(dy, x, dw, M, N, K),
+    }
+
+
+def bench_c2(b: Bench, reps: int, cpu: bool) -> dict:
+    """c2: one int4 linear forward plus its STE backward, M=512, K=768, N=192,
+    G=32: gemmNT, then gemmBwd (the reference's gemmDW + gemmDX pair in one
+    launch, bitwise the two calls). The separate dX and dW launches are timed
+    beside it."""
+    M, N, K, G = C2["M"], C2["N"], C2["K"], C2["G"]
+    kern = c2_parts(b)
+    step = lambda i: (kern["gemm_nt_i4"](i), kern["gemm_bwd_i4"](i))
+    ms_step = b.time_launches(step, reps)
+    per = {k: b.time_launches(f, reps) for k, f in kern.items()}
+    gemm = 2 * M * N * K
+    q, s = N * K // 2, N * (K // G) * 4
+    nbytes = {"gemm_nt_i4": q + s + 4 * (M * K + M * N), "gemm_bwd_i4": q + s + 4 * (M * N + 2 * M * K + N * K)}
+    out = {"kernel": "gemmNT + gemmBwd", "shape": "M=512 K=768 N=192 int4 G=32",
+           "us_per_step": round(ms_step * 1e3, 3), "TFLOPs": round(3 * gemm / ms_step / 1e9, 3),
+           "per_kernel_us": {k: round(v * 1e3, 3) for k, v in per.items()},
+           "roofline": roofline(2 * gemm / per["gemm_bwd_i4"] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
+                                traffic_for("c2", ["gemm_bwd_pair_kernel<4>"])),
+           "roofline_kernel": "gemm_bwd_i4 (gemm_bwd_pair_kernel<4>)",
+           "algorithmic_bytes": nbytes,
+           "note": "latency-bound shape; fp32 MFMA (157.3 TFLOP/s) is the nearer roof"}
+    if cpu:
+        import numpy as np
+        orc = _oracle()
+        rng = np.random.default_rng(0)
+        x = rng.standard_normal(M * K, dtype=np.float32)
+        w = rng.standard_normal(N * K, dtype=np.float32) * np.float32(0.02)
+        dy = rng.standard_normal(M * N, dtype=np.float32) * np.float32(1e-3)
+        qh, sh = orc.quant(w, N, K, G, 4)
+
+        def run():
+            wd = orc.dequant(qh, sh, N, K, G, 4)
+            orc.gemm_nt(x, wd, None, M, N, K)
+            orc.gemm_dx(dy, wd, M, N, K)
+            orc.gemm_dw(dy, x, M, N, K)
+
+        with one_core() as core:
+            per_s, calls = cpu_time(run, 3.0, 50)
+        out["cpu_baseline"] = cpu_record(3 * gemm / per_s / 1e12, "TFLOP/s", core,
+                                         f"{calls} whole c2 steps (dequant, cpuGemmNT, cpuGemmDX, cpuGemmDW), "
+                                         f"{per_s * 1e3:.1f} ms/step, 1 thread")
+    return out
+
+
+def bench_c1(b: Bench, reps: int, cpu: bool) -> dict:
+    M, N, K, G = C1["M"], C1["N"], C1["K"], C1["G"]
     x, w = b.randn(M * K, 1.0), b.randn(N * K, 0.02)
     q, s = b.quantized(w, N, K, G, 8)
     y = b.zeros(M * N)
     ms = b.time_launches(lambda i: b.gpu.gemmNT(8, None, q, s, x, None, y, M, N, K, G), reps)
     flops = 2 * M * N * K
     nbytes = N * K + N * (K // G) * 4 + 4 * (M * K + M * N)
-    return {"kernel": "gemm_nt_i8", "shape": "M=512 K=192 N=768 int8 G=32", "us": round(ms * 1e3, 3),
-            "TFLOPs": round(flops / ms / 1e9, 3), "GBps": round(nbytes / ms / 1e6, 2),
-            "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
-            "note": "latency-bound; fp32 MFMA is the nearer roof"}
+    out = {"kernel": "gemm_nt_i8", "shape": "M=512 K=192 N=768 int8 G=32", "us": round(ms * 1e3, 3),
+           "TFLOPs": round(flops / ms / 1e9, 3), "GBps": round(nbytes / ms / 1e6, 2),
+           "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
+                                traffic_for("c1", ["gemm_fwd"])),
+           "note": "latency-bound; fp32 MFMA is the nearer roof"}
+    if cpu:
+        out["cpu_baseline"] = cpu_gemm_slice(M, N, K, G, 8, N, 1.5)
+    return out
 
 
-def bench_quant(b: Bench, reps: int, bits: int) -> dict:
-    N, K, G = 14336, 4096, 128
+def c3_flops(cfg) -> int:
+    """Linear + attention flop of the looped block forward (src/DiT.swift:520-550)."""
+    M, C, F, KV, T, H, D = cfg.B * cfg.T, cfg.C, cfg.F, cfg.D, cfg.T, cfg.H, cfg.D
+    lin = 2 * M * C * (C + 2 * KV + C + 2 * F) + 2 * M * F * C
+    att = 2 * 2 * cfg.B * H * T * T * D
+    return cfg.loops * (lin + att)
+
+
+def _dit_block(b: Bench):
+    dgm = b.dgm
+    cfg = dgm.DiTConfig()
+    w = {n: b.randn(N * K, 0.02) for n, (N, K) in cfg.linear_shapes().items()}
+    for n in dgm.DIT_NORMS:
+        w[n] = b.torch.ones(cfg.C, dtype=b.torch.float32, device="cuda")
+    b.sync()
+    with b.torch.cuda.stream(b.stream):
+        blk = dgm.DiTBlock(b.gpu, cfg, w)
+    return cfg, w, blk
+
+
+def _cpu_dit(cfg, train: bool, budget_s: float) -> dict:
+    import numpy as np
+    orc = _oracle()
+    dgm = load_package()
+    rng = np.random.default_rng(0)
+    ocfg = orc.DiTCfg(B=cfg.B, T=cfg.T, C=cfg.C, F=cfg.F, H=cfg.H, D=cfg.D, loops=cfg.loops, group=cfg.group,
+                      bits=cfg.bits, eps=cfg.eps, theta=cfg.theta, mix=cfg.mix)
+    shapes = cfg.linear_shapes()
+    wts = {n: (rng.standard_normal(N * K, dtype=np.float32) * np.float32(0.02)) for n, (N, K) in shapes.items()}
+    qw = {n: orc.quant(wts[n], shapes[n][0], shapes[n][1], cfg.group, cfg.bits) for n in dgm.DIT_LINEARS}
+    norms = {n: np.ones(cfg.C, np.float32) for n in dgm.DIT_NORMS}
+    x0 = rng.standard_normal(cfg.B * cfg.T * cfg.C, dtype=np.float32)
+    if train:
+        gy = rng.standard_normal(cfg.B * cfg.T * cfg.C, dtype=np.float32) * np.float32(1e-2)
+        run = lambda: orc.dit_train(ocfg, qw, norms, x0, gy)
+    else:
+        qw.update(norms)
+        run = lambda: orc.dit_forward(ocfg, qw, x0)
+    with one_core() as core:
+        per, calls = cpu_time(run, budget_s, 20)
+    tokens = cfg.B * cfg.T
+    what = "forward with saved activations + block backward" if train else "forward"
+    return cpu_record(tokens / per, "tokens/s", core,
+                      f"{calls} whole c3 {what} call(s) (4 loops, int8 G=32, quantized linears in the Metal "
+                      f"kernel order), {per * 1e3:.1f} ms/call, 1 thread")
+
+
+def bench_c3(b: Bench, reps: int, cpu: bool) -> dict:
+    """c3: the photos-dit looped block forward, 8x64 tokens, 4 loops, int8 G=32
+    linears; weights ~N(0,0.02), norms 1, xs[0] ~N(0,1), all resident. The
+    timed call is the whole 4-loop forward (dgm_dit_forward), in place on x."""
+    cfg, _, blk = _dit_block(b)
+    x = b.randn(cfg.B * cfg.T * cfg.C, 1.0)
+    ms = b.time_launches(lambda i: blk.forward(x), reps)
+    tokens = cfg.B * cfg.T
+    flops = c3_flops(cfg)
+    out = {"kernel": "dit_forward (4 loops)", "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
+           "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+           "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
+           "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
+                                traffic_for("c3", ["dit_gemm_kernel", "attn_mfma_kernel", "gemm_fwd", "row_fuse"])),
+           "note": "launch/latency-bound: ~2.3 GFLOP and ~0.6 MB of weights per forward; traffic = sum over "
+                   "the forward's kernels"}
+    if cpu:
+        out["cpu_baseline"] = _cpu_dit(cfg, False, 3.0)
+    return out
+
+
+def bench_c3_train(b: Bench, reps: int, cpu: bool) -> dict:
+    """One training step of the c3 block (weights as in bench_c3): the forward
+    that saves every loop's activations, then the block backward (int8 STE:
+    dX through the codes, dW into fp32 gradients) from dL/dxs[4] ~N(0,1e-2).
+    Flop: the forward's, plus dX and dW of every linear and the four
+    attention backward products (3x the forward)."""
+    cfg, _, blk = _dit_block(b)
+    with b.torch.cuda.stream(b.stream):
+        blk.zero_grads()
+    x0 = b.randn(cfg.B * cfg.T * cfg.C, 1.0)
+    g0 = b.randn(cfg.B * cfg.T * cfg.C, 1e-2)
+    x, g = x0.clone(), g0.clone()
+
+    def step(i):
+        blk.forward_train(x)
+        blk.backward(g)
+
+    ms = b.time_launches(step, reps)
+    flops = 3 * c3_flops(cfg)
+    tokens = cfg.B * cfg.T
+    out = {"kernel": "dit_forward_train + dit_backward (4 loops)",
+           "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
+           "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+           "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
+           "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
+           "note": "launch/latency-bound; x and dL/dx are reused in place across the timed steps"}
+    if cpu:
+        out["cpu_baseline"] = _cpu_dit(cfg, True, 4.0)
+    return out
+
+
+def bench_quant(b: Bench, reps: int, bits: int, cpu: bool) -> dict:
+    N, K, G = C4["N"], C4["K"], C4["G"]
     w = b.randn(N * K, 0.02)
     q = b.zeros(N * K // (2 if bits == 4 else 1), b.torch.uint8)
     s = b.zeros(N * (K // G))
     ms = b.time_launches(lambda i: b.gpu.quantize(w, q, s, N, K, bits, G), reps)
     nbytes = 4 * N * K + (N * K // (2 if bits == 4 else 1)) + 4 * N * (K // G)
-    return {"kernel": f"quant_i{bits}", "shape": "W[14336,4096] G=128", "us": round(ms * 1e3, 3),
-            "GBps": round(nbytes / ms / 1e6, 2),
-            "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
+    out = {"kernel": f"quant_i{bits}", "shape": "W[14336,4096] G=128", "us": round(ms * 1e3, 3),
+           "GBps": round(nbytes / ms / 1e6, 2),
+           "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
+                                traffic_for(f"quant_i{bits}", ["quant_vec_kernel"]))}
+    if cpu:
+        import numpy as np
+        orc = _oracle()
+        rows = 1024
+        wh = np.random.default_rng(0).standard_normal(rows * K, dtype=np.float32) * np.float32(0.02)
+        with one_core() as core:
+            per, calls = cpu_time(lambda: orc.quant(wh, rows, K, G, bits), 1.0, 200)
+        out["cpu_baseline"] = cpu_record(rows * K * (4 + (0.5 if bits == 4 else 1)) / per / 1e9, "GB/s", core,
+                                         f"cpuQuant of a {rows}x{K} slice, {calls} calls, {per * 1e3:.1f} ms "
+                                         f"each, 1 thread")
+    return out
 
 
-def bench_adam_quant(b: Bench, reps: int, bits: int) -> dict:
+def bench_adam_quant(b: Bench, reps: int, bits: int, cpu: bool) -> dict:
     """AdamW + re-quantization of the c4/c5 weight (W[14336,4096], G=128): the
     fused pass against adam followed by quantize. Algorithmic bytes per
     element: w, g, m, v read (16) + w, m, v written (12) + codes (0.5 or 1),
     plus the scales."""
-    N, K, G = 14336, 4096, 128
+    N, K, G = C4["N"], C4["K"], C4["G"]
     n = N * K
     w, g = b.randn(n, 0.02), b.randn(n, 1.0)
     m, v = b.zeros(n), b.zeros(n)
@@ -279,138 +579,79 @@ def bench_adam_quant(b: Bench, reps: int, bits: int) -> dict:
     unfused = b.time_launches(pair, reps)
     code_b = n // (2 if bits == 4 else 1)
     nbytes = 28 * n + code_b + 4 * N * (K // G)
-    return {"kernel": "adam_quantize", "shape": f"W[14336,4096] int{bits} G=128", "us": round(fused * 1e3, 3),
-            "GBps": round(nbytes / fused / 1e6, 2), "unfused_us": round(unfused * 1e3, 3),
-            "roofline": roofline(nbytes / fused / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
+    out = {"kernel": "adam_quantize", "shape": f"W[14336,4096] int{bits} G=128", "us": round(fused * 1e3, 3),
+           "GBps": round(nbytes / fused / 1e6, 2), "unfused_us": round(unfused * 1e3, 3),
+           "roofline": roofline(nbytes / fused / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
+                                traffic_for(f"adam_quant_i{bits}", ["adam_quant_kernel"]))}
+    if cpu:
+        import numpy as np
+        orc = _oracle()
+        rows = 512
+        rng = np.random.default_rng(0)
+        wh = rng.standard_normal(rows * K, dtype=np.float32) * np.float32(0.02)
+        gh = rng.standard_normal(rows * K, dtype=np.float32)
+        z = np.zeros(rows * K, np.float32)
+        with one_core() as core:
+            per, calls = cpu_time(lambda: orc.adam_quantize(wh, gh, z, z, rows, K, G, bits, *hp), 1.0, 200)
+        out["cpu_baseline"] = cpu_record(rows * K * (28 + (0.5 if bits == 4 else 1)) / per / 1e9, "GB/s", core,
+                                         f"adamw then cpuQuant of a {rows}x{K} slice, {calls} calls, "
+                                         f"{per * 1e3:.1f} ms each, 1 thread")
+    return out
 
 
-def bench_embed_bwd(b: Bench, reps: int) -> dict:
+def bench_embed_bwd(b: Bench, reps: int, cpu: bool) -> dict:
     """embed_bwd at the quantized GPT's default shape (src/GPT.swift:374-376;
     16 x 64 tokens, C 128, a 65-symbol vocabulary) with Zipf-like token counts."""
     t = b.torch
     B, T, C, V = 16, 64, 128, 65
     ranks = t.arange(1, V + 1, dtype=t.float64)
     probs = (1.0 / ranks) / (1.0 / ranks).sum()
-    toks = t.multinomial(probs, B * T, replacement=True, generator=b.gen).to(t.int32).to("cuda")
+    toks = t.multinomial(probs, B * T, replacement=True, generator=b.gen).to(t.int32)
     dx, dwe = b.randn(B * T * C, 1.0), b.zeros(V * C)
-    ms = b.time_launches(lambda i: b.gpu.embedBwd(toks, dx, dwe, B, T, C, V), reps)
+    toks_d = toks.to("cuda")
+    ms = b.time_launches(lambda i: b.gpu.embedBwd(toks_d, dx, dwe, B, T, C, V), reps)
     nbytes = 4 * (B * T * C + 2 * V * C + B * T)
-    return {"kernel": "embed_bwd", "shape": "B=16 T=64 C=128 V=65", "us": round(ms * 1e3, 3),
-            "GBps": round(nbytes / ms / 1e6, 2), "note": "latency-bound: 1 MB of traffic"}
+    out = {"kernel": "embed_bwd", "shape": "B=16 T=64 C=128 V=65", "us": round(ms * 1e3, 3),
+           "GBps": round(nbytes / ms / 1e6, 2), "note": "latency-bound: 1 MB of traffic",
+           "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
+                                traffic_for("embed_bwd", ["embed_bwd_kernel"]))}
+    if cpu:
+        import numpy as np
+        orc = _oracle()
+        th = toks.numpy().astype(np.uint32)
+        dxh = np.random.default_rng(0).standard_normal(B * T * C, dtype=np.float32)
+        z = np.zeros(V * C, np.float32)
+        with one_core() as core:
+            per, calls = cpu_time(lambda: orc.embed_bwd(th, dxh, z, B, T, C, V), 1.0, 200)
+        out["cpu_baseline"] = cpu_record(nbytes / per / 1e9, "GB/s", core,
+                                         f"embed_bwd (V*B*T*C scan of the reference kernel), {calls} calls, "
+                                         f"{per * 1e3:.2f} ms each, 1 thread")
+    return out
 
 
-def bench_c4(b: Bench, reps: int, M: int, math_mode: int) -> dict:
-    """Decode-shaped int4: K=4096, N=14336, G=128. Weight copies are rotated so
-    that successive launches never find W in the 256 MB Infinity Cache."""
-    N, K, G = 14336, 4096, 128
-    wq_bytes = N * K // 2 + N * (K // G) * 4
-    copies = max(2, -(-512 * 2 ** 20 // wq_bytes))
-    w = b.randn(N * K, 0.02)
-    q0, s0 = b.quantized(w, N, K, G, 4)
-    del w
-    Q = [q0] + [q0.clone() for _ in range(copies - 1)]
-    S = [s0] + [s0.clone() for _ in range(copies - 1)]
-    x = b.randn(M * K, 1.0)
-    y = b.zeros(M * N)
-    b.gpu.set_math(math_mode)
-    try:
-        ms = b.time_launches(lambda i: b.gpu.gemmNT(4, None, Q[i % copies], S[i % copies], x, None, y,
-                                                    M, N, K, G), reps)
-    finally:
-        b.gpu.set_math(b.dgm.DGM_MATH_FP32)
-    flops = 2 * M * N * K
-    nbytes = wq_bytes + 4 * (M * K + M * N)
-    mode = "fp32" if math_mode == b.dgm.DGM_MATH_FP32 else "bf16"
-    del Q, S
-    return {"kernel": "gemm_nt_i4", "math": mode, "shape": f"M={M} K=4096 N=14336 int4 G=128",
-            "us": round(ms * 1e3, 3), "GBps": round(nbytes / ms / 1e6, 2),
-            "TFLOPs": round(flops / ms / 1e9, 3), "weight_copies_rotated": copies,
-            "algorithmic_bytes": nbytes,
-            "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm")}
-
-
-def c3_flops(cfg) -> int:
-    """Linear + attention flop of the looped block forward (src/DiT.swift:520-550)."""
-    M, C, F, KV, T, H, D = cfg.B * cfg.T, cfg.C, cfg.F, cfg.D, cfg.T, cfg.H, cfg.D
-    lin = 2 * M * C * (C + 2 * KV + C + 2 * F) + 2 * M * F * C
-    att = 2 * 2 * cfg.B * H * T * T * D
-    return cfg.loops * (lin + att)
-
-
-def bench_c3(b: Bench, reps: int) -> dict:
-    """c3: the photos-dit looped block forward, 8x64 tokens, 4 loops, int8 G=32
-    linears; weights ~N(0,0.02), norms 1, xs[0] ~N(0,1), all resident. The
-    timed call is the whole 4-loop forward (dgm_dit_forward), in place on x."""
-    dgm = b.dgm
-    cfg = dgm.DiTConfig()
-    w = {n: b.randn(N * K, 0.02) for n, (N, K) in cfg.linear_shapes().items()}
-    for n in dgm.DIT_NORMS:
-        w[n] = b.torch.ones(cfg.C, dtype=b.torch.float32, device="cuda")
+def hbm_ceiling(b: Bench) -> dict:
+    """The box's measured stream ceiling: a device copy of CEIL_BYTES (read
+    CEIL_BYTES + write CEIL_BYTES, 2x the 256 MB Infinity Cache each way),
+    20 copies bracketed by HIP events."""
+    t = b.torch
+    n = CEIL_BYTES // 4
+    src = t.ones(n, device="cuda")
+    dst = t.zeros(n, device="cuda")
     b.sync()
-    with b.torch.cuda.stream(b.stream):
-        blk = dgm.DiTBlock(b.gpu, cfg, w)
-    x = b.randn(cfg.B * cfg.T * cfg.C, 1.0)
-    ms = b.time_launches(lambda i: blk.forward(x), reps)
-    tokens = cfg.B * cfg.T
-    flops = c3_flops(cfg)
-    return {"kernel": "dit_forward (4 loops)", "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
-            "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
-            "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
-            "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
-            "note": "launch/latency-bound: ~2.3 GFLOP and ~0.6 MB of weights per forward"}
-
-
-def bench_c3_train(b: Bench, reps: int) -> dict:
-    """One training step of the c3 block (weights as in bench_c3): the forward
-    that saves every loop's activations, then the block backward (int8 STE:
-    dX through the codes, dW into fp32 gradients) from dL/dxs[4] ~N(0,1e-2).
-    Flop: the forward's, plus dX and dW of every linear and the four
-    attention backward products (3x the forward)."""
-    dgm = b.dgm
-    cfg = dgm.DiTConfig()
-    w = {n: b.randn(N * K, 0.02) for n, (N, K) in cfg.linear_shapes().items()}
-    for n in dgm.DIT_NORMS:
-        w[n] = b.torch.ones(cfg.C, dtype=b.torch.float32, device="cuda")
-    b.sync()
-    with b.torch.cuda.stream(b.stream):
-        blk = dgm.DiTBlock(b.gpu, cfg, w)
-        blk.zero_grads()
-    x0 = b.randn(cfg.B * cfg.T * cfg.C, 1.0)
-    g0 = b.randn(cfg.B * cfg.T * cfg.C, 1e-2)
-    x, g = x0.clone(), g0.clone()
-
-    def step(i):
-        blk.forward_train(x)
-        blk.backward(g)
-
-    ms = b.time_launches(step, reps)
-    flops = 3 * c3_flops(cfg)
-    tokens = cfg.B * cfg.T
-    return {"kernel": "dit_forward_train + dit_backward (4 loops)", "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
-            "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
-            "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
-            "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
-            "note": "launch/latency-bound; x and dL/dx are reused in place across the timed steps"}
-
-
-def bench_c5(b: Bench, reps: int, bits: int, math_mode: int) -> dict:
-    M, N, K, G = 8192, 14336, 4096, 128
-    w = b.randn(N * K, 0.02)
-    q, s = b.quantized(w, N, K, G, bits)
-    del w
-    x = b.randn(M * K, 1.0)
-    y = b.zeros(M * N)
-    b.gpu.set_math(math_mode)
-    try:
-        ms = b.time_launches(lambda i: b.gpu.gemmNT(bits, None, q, s, x, None, y, M, N, K, G), reps)
-    finally:
-        b.gpu.set_math(b.dgm.DGM_MATH_FP32)
-    flops = 2 * M * N * K
-    mode = "fp32" if math_mode == b.dgm.DGM_MATH_FP32 else "bf16"
-    peak = PEAK["fp32_TFLOPs"] if mode == "fp32" else PEAK["bf16_TFLOPs"]
-    return {"kernel": f"gemm_nt_i{bits}", "math": mode, "shape": f"M=8192 K=4096 N=14336 int{bits} G=128",
-            "us": round(ms * 1e3, 3), "TFLOPs": round(flops / ms / 1e9, 3),
-            "roofline": roofline(flops / ms / 1e9, peak, "TFLOP/s", "mfma")}
+    with t.cuda.stream(b.stream):
+        for _ in range(3):
+            dst.copy_(src)
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record(b.stream)
+        for _ in range(20):
+            dst.copy_(src)
+        e1.record(b.stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / 20
+    gbps = 2 * CEIL_BYTES / ms / 1e6
+    del src, dst
+    return {"kernel": "torch device copy", "bytes_each_way": CEIL_BYTES, "us": round(ms * 1e3, 3),
+            "GBps": round(gbps, 1), "frac_of_8TBps": round(gbps / PEAK["hbm_GBps"], 4)}
 
 
 def calib_copy(b: Bench) -> dict:
@@ -425,6 +666,27 @@ def calib_copy(b: Bench) -> dict:
         dst.copy_(src)
     b.sync()
     return {"bytes": CALIB_BYTES}
+
+
+def workload_table(b, args, cpu: bool):
+    F, H = 0, 1   # DGM_MATH_FP32, DGM_MATH_BF16 (include/dgm_quant.h)
+    return [
+        ("c5_int8", lambda: bench_c5(b, 8, max(args.steps, 20), max(args.warmup, 3), cpu)),
+        ("c4_int4_m1_fp32", lambda: bench_c4(b, 72, 1, F, cpu)),
+        ("c4_int4_m16_fp32", lambda: bench_c4(b, 72, 16, F, cpu)),
+        ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, H, False)),
+        ("c4_int4_m64_fp32", lambda: bench_c4(b, 72, 64, F, cpu)),
+        ("c4_int4_m64_bf16", lambda: bench_c4(b, 72, 64, H, False)),
+        ("c1", lambda: bench_c1(b, args.reps, cpu)),
+        ("c2", lambda: bench_c2(b, args.reps, cpu)),
+        ("c3", lambda: bench_c3(b, 50, cpu)),
+        ("c3_train", lambda: bench_c3_train(b, 10, cpu)),
+        ("quant_i4", lambda: bench_quant(b, 20, 4, cpu)),
+        ("quant_i8", lambda: bench_quant(b, 20, 8, cpu)),
+        ("adam_quant_i4", lambda: bench_adam_quant(b, 10, 4, cpu)),
+        ("adam_quant_i8", lambda: bench_adam_quant(b, 10, 8, cpu)),
+        ("embed_bwd", lambda: bench_embed_bwd(b, 50, cpu)),
+    ]
 
 
 # ---- rocprofv3 output helpers (run on the CPU) ---------------------------------
@@ -494,7 +756,7 @@ def traffic(name: str, fetch_dir: str, write_dir: str) -> dict:
     w_scale = CALIB_BYTES / (write.get(ck, 0.0) * 1024.0) if write.get(ck) else 1.0
     rec = {"_calibration": {"kernel": ck, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}}
     for k in fetch:
-        if k == ck:
+        if k == ck or "copy" in k.lower() or "elementwise" in k.lower() or "fill" in k.lower():
             continue
         fb = fetch[k] * 1024.0 * f_scale
         wb = write.get(k, 0.0) * 1024.0 * w_scale
@@ -513,12 +775,13 @@ def traffic(name: str, fetch_dir: str, write_dir: str) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--reps", type=int, default=100, help="launches per per-kernel timing")
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--reps", type=int, default=100, help="launches per graph-timed workload")
     ap.add_argument("--skip-extra", action="store_true", help="headline only")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extra workloads to run")
+    ap.add_argument("--only", default="", help="comma list of workloads (c5_int4 = the headline)")
+    ap.add_argument("--list", action="store_true")
     ap.add_argument("--calib-copy", action="store_true", help="run the traffic calibration copy at the end")
     ap.add_argument("--summarize", metavar="DIR")
     ap.add_argument("--title", default="rocprofv3 summary")
@@ -538,113 +801,73 @@ def main() -> int:
               "(the reference is single-device); run with --gpus 1.", file=sys.stderr)
         return 2
 
+    if args.list:
+        print("\n".join(["c5_int4 (headline)", "hbm_ceiling"] + [n for n, _ in workload_table(None, args, False)]))
+        return 0
     import torch
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     dgm = load_package()
     b = Bench(dgm, torch)
+    cpu = not args.skip_cpu
+    only = set(filter(None, args.only.split(",")))
+    want = lambda name: not only or name in only
 
-    # -- headline step ----------------------------------------------------------
-    log("[bench] c2 step setup")
-    kern = c2_setup(b)
-    order = ["gemm_nt_i4", "gemm_bwd_i4"]
+    out: dict = {}
+    if want("c5_int4"):
+        log(f"[bench] headline c5 int4: {args.warmup} warmup + {args.steps} timed steps")
+        head = bench_c5(b, 4, args.steps, args.warmup, cpu)
+        torch.cuda.empty_cache()
+        M, N, K = C5["M"], C5["N"], C5["K"]
+        out = {
+            "metric": METRIC,
+            "value": head["TFLOPs"],
+            "unit": "TFLOP/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(head["us_wall_per_step"] / 1e3, 6),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic (torch CPU generator, seed 1234: X~N(0,1), W~N(0,0.02) quantized int4 G=128 once "
+                    "before timing)",
+            "config": {"workload": "c5: prefill-shaped int4 group-quant GEMM forward (gemmNT), W dequantized to "
+                                   "bf16 in LDS, bf16 MFMA, fp32 accumulate",
+                       "M": M, "K": K, "N": N, "group": C5["G"], "bits": 4, "math": "DGM_MATH_BF16",
+                       "parallelism": "single GPU", "timing": "eager calls, wall clock over the timed steps"},
+            "us_median": head["us_median"],
+            "TFLOPs_median": head["TFLOPs_median"],
+            "frac_of_bf16_peak": round(head["TFLOPs"] / PEAK["bf16_TFLOPs"], 4),
+            "roofline": head["roofline"],
+        }
+        if "cpu_baseline" in head:
+            out["cpu_baseline"] = head["cpu_baseline"]
+        log(f"[bench] c5 int4 {head['us_wall_per_step']:.1f} us/step = {head['TFLOPs']:.1f} TFLOP/s")
 
-    def step(i):
-        for k in order:
-            kern[k](i)
-
-    steps = b.capture(step, args.steps)
-    warm = b.capture(step, max(args.warmup, 1))
-    b.graph_ms(warm)
-    b.sync()
-    t0 = time.perf_counter()
-    with torch.cuda.stream(b.stream):
-        steps.replay()
-    b.sync()
-    wall = time.perf_counter() - t0
-    ms_step = wall * 1e3 / args.steps
-    gpu_ms_step = b.graph_ms(steps) / args.steps
-    del steps, warm
-    log(f"[bench] c2 step {ms_step * 1e3:.2f} us wall, {gpu_ms_step * 1e3:.2f} us on the stream")
-
-    per_kernel = {k: b.time_launches(kern[k], args.reps) for k in order + ["gemm_dx_i4", "gemm_dw"]}
-    dom = max(order, key=per_kernel.get)
-    gemm_flop = 2 * C2["M"] * C2["N"] * C2["K"]
-    flops_k = 2 * gemm_flop if dom == "gemm_bwd_i4" else gemm_flop
-    # HIP kernel behind each entry point at the c2 shape (names as rocprofv3 prints them).
-    device_kernel = {"gemm_nt_i4": "gemm_fwd_lds_kernel<4, 4>", "gemm_dx_i4": "gemm_dx_lds_kernel<4>",
-                     "gemm_dw": "gemm_dw_pair_kernel", "gemm_bwd_i4": "gemm_bwd_pair_kernel<4>"}
-    roof = roofline(flops_k / per_kernel[dom] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
-                    traffic_for("c2", device_kernel[dom]))
-    roof["kernel"] = dom
-    roof["device_kernel"] = device_kernel[dom]
-    roof["avg_launch_us"] = round(per_kernel[dom] * 1e3, 3)
-    roof["algorithmic_bytes"] = c2_bytes()[dom]
-    roof["algorithmic_flop"] = flops_k
-    roof["note"] = ("latency-bound shape; fp32 MFMA (157.3 TFLOP/s) is the nearer roof than HBM "
-                    f"({c2_bytes()[dom] / 8e12 * 1e6:.2f} us at 8 TB/s)")
-
-    out = {
-        "metric": METRIC,
-        "value": round(c2_flops() / (ms_step * 1e-3) / 1e12, 4),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (torch CPU generator, seed 1234: X~N(0,1), W~N(0,0.02), dY~N(0,1e-3))",
-        "config": {"workload": "c2: int4 group-quant linear fwd + STE bwd (gemmNT; gemmBwd = gemmDW + gemmDX "
-                               "in one launch)",
-                   "M": C2["M"], "K": C2["K"], "N": C2["N"], "group": C2["G"], "bits": 4,
-                   "parallelism": "single GPU", "timing": "one HIP graph of the timed steps"},
-        "GBps": round(sum(c2_bytes().values()) / (ms_step * 1e-3) / 1e9, 2),
-        "per_kernel_us": {k: round(v * 1e3, 3) for k, v in per_kernel.items()},
-        "roofline": roof,
-    }
+    if want("hbm_ceiling") or not only:
+        log("[bench] hbm ceiling (stream copy)")
+        out["hbm_ceiling"] = hbm_ceiling(b)
+        torch.cuda.empty_cache()
 
     if not args.skip_extra:
-        only = set(filter(None, args.only.split(",")))
         W = {}
-        jobs = [
-            ("c1_int8_fwd", lambda: bench_c1(b, args.reps)),
-            ("c3_dit_fwd", lambda: bench_c3(b, 50)),
-            ("c3_dit_train_step", lambda: bench_c3_train(b, 10)),
-            ("quant_i4_14336x4096", lambda: bench_quant(b, 20, 4)),
-            ("quant_i8_14336x4096", lambda: bench_quant(b, 20, 8)),
-            ("adam_quant_i4_14336x4096", lambda: bench_adam_quant(b, 10, 4)),
-            ("adam_quant_i8_14336x4096", lambda: bench_adam_quant(b, 10, 8)),
-            ("embed_bwd_gpt", lambda: bench_embed_bwd(b, 50)),
-            ("c4_int4_m1_fp32", lambda: bench_c4(b, 72, 1, dgm.DGM_MATH_FP32)),
-            ("c4_int4_m16_fp32", lambda: bench_c4(b, 72, 16, dgm.DGM_MATH_FP32)),
-            ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, dgm.DGM_MATH_BF16)),
-            ("c4_int4_m64_fp32", lambda: bench_c4(b, 72, 64, dgm.DGM_MATH_FP32)),
-            ("c4_int4_m64_bf16", lambda: bench_c4(b, 72, 64, dgm.DGM_MATH_BF16)),
-            ("c5_int4_bf16", lambda: bench_c5(b, 5, 4, dgm.DGM_MATH_BF16)),
-            ("c5_int8_bf16", lambda: bench_c5(b, 5, 8, dgm.DGM_MATH_BF16)),
-        ]
-        for name, fn in jobs:
-            if only and name not in only:
+        for name, fn in workload_table(b, args, cpu):
+            if not want(name):
                 continue
             log(f"[bench] {name}")
             try:
                 W[name] = fn()
             except Exception as e:   # report, keep the headline line intact
-                W[name] = {"error": str(e)}
+                W[name] = {"error": f"{type(e).__name__}: {e}"}
             torch.cuda.empty_cache()
         out["workloads"] = W
 
     if args.calib_copy:
         log("[bench] calibration copy")
         out["calibration_copy"] = calib_copy(b)
-
-    if not args.skip_cpu:
-        log("[bench] cpu baseline (oracle, 1 thread)")
-        out["cpu_baseline"] = cpu_baseline_c2()
     print(json.dumps(out), flush=True)
     return 0
 

@@ -21,10 +21,16 @@ struct dgm_gpu {
     int first_err = DGM_OK;           // first error since begin()
     char last_kernel[64] = {0};
     char err_msg[320] = {0};
-    // Grow-only device workspace for staging (bf16 activations, split-K
-    // partials). Owned by the context, freed in dgm_gpu_destroy.
+    // Grow-only device workspace for staging (the decode kernels' activation
+    // pieces, sum-of-squares partials). Owned by the context. A grown
+    // workspace keeps its predecessors (at most kMaxRetired, each at most half
+    // the next) until dgm_gpu_destroy, since queued work and captured graphs
+    // may still use them.
+    static constexpr int kMaxRetired = 48;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    void* retired[kMaxRetired] = {};
+    int n_retired = 0;
 };
 
 namespace dgm {
@@ -41,8 +47,11 @@ int enter(dgm_gpu* g, const char* name);
 int check_launch(dgm_gpu* g, const char* name);
 
 // Ensures the context workspace holds at least `bytes`; returns nullptr on
-// allocation failure (error recorded).
+// failure (error recorded): allocation failure, or growth needed while the
+// context's stream is capturing a graph.
 void* workspace(dgm_gpu* g, size_t bytes);
+// The status a caller returns when workspace() gave nullptr.
+int ws_error(dgm_gpu* g);
 
 constexpr int64_t kMaxIndex = (int64_t(1) << 31) - 1;
 

@@ -37,22 +37,38 @@ int check_launch(dgm_gpu* g, const char* name) {
 
 void* workspace(dgm_gpu* g, size_t bytes) {
     if (bytes <= g->ws_bytes) return g->ws;
-    // Work already queued may still read the old buffer.
-    if (g->ws) {
-        (void)hipStreamSynchronize(g->stream);
-        (void)hipFree(g->ws);
-        g->ws = nullptr;
-        g->ws_bytes = 0;
+    // Growing inside a graph capture would bake a fresh allocation into the
+    // graph (and hipMalloc is not capturable): refuse, and let the caller make
+    // one such call before capturing.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        fail(g, DGM_ERR_UNSUPPORTED,
+             "workspace would grow to %zu bytes during graph capture; run one such call before capturing", bytes);
+        return nullptr;
     }
-    size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-    if (hipMalloc(&g->ws, want) != hipSuccess) {
-        g->ws = nullptr;
+    if (g->n_retired == dgm_gpu::kMaxRetired) {
+        fail(g, DGM_ERR_UNSUPPORTED, "workspace grew %d times; the context keeps every retired buffer",
+             dgm_gpu::kMaxRetired);
+        return nullptr;
+    }
+    // At least double, so the retired buffers total less than the live one.
+    size_t want = bytes < 2 * g->ws_bytes ? 2 * g->ws_bytes : bytes;
+    if (want < (size_t(1) << 20)) want = size_t(1) << 20;
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
         fail(g, DGM_ERR_HIP, "workspace allocation of %zu bytes failed", want);
         return nullptr;
     }
+    // The old buffer is not freed here: work still queued on any stream and
+    // graphs captured earlier may read or write it. It lives until
+    // dgm_gpu_destroy.
+    if (g->ws) g->retired[g->n_retired++] = g->ws;
+    g->ws = p;
     g->ws_bytes = want;
     return g->ws;
 }
+
+int ws_error(dgm_gpu* g) { return g->first_err != DGM_OK ? g->first_err : DGM_ERR_HIP; }
 
 }  // namespace dgm
 
@@ -82,7 +98,9 @@ int dgm_gpu_create(dgm_gpu** out) {
 void dgm_gpu_destroy(dgm_gpu* g) {
     if (!g) return;
     if (g->stream) (void)hipStreamSynchronize(g->stream);
+    (void)hipDeviceSynchronize();   // any stream or graph may still use a workspace
     if (g->ws) (void)hipFree(g->ws);
+    for (int i = 0; i < g->n_retired; ++i) (void)hipFree(g->retired[i]);
     if (g->own_stream) (void)hipStreamDestroy(g->own_stream);
     delete g;
 }

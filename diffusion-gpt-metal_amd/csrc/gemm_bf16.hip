@@ -286,7 +286,7 @@ int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const floa
              float* Y, const dgm_GemmP* p) {
     const int64_t mk = int64_t(p->M) * p->K;
     uint16_t* xb = static_cast<uint16_t*>(workspace(g, size_t(mk) * 2));
-    if (!xb) return DGM_ERR_HIP;
+    if (!xb) return ws_error(g);
     hipStream_t st = g->stream;
     const int64_t n8 = mk / 8;
     hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, st, X, xb, n8);

@@ -693,7 +693,7 @@ int launch_tiled(dgm_gpu* g, const SkinnyArgs& s, hipStream_t st) {
     const int TP = SH::TP;
     const size_t xp_bytes = size_t(K_of(s)) / SH::KBK * TP * SH::H * 1024;
     uint8_t* ws = static_cast<uint8_t*>(dgm::workspace(g, xp_bytes + 64 * sizeof(float) + 256));
-    if (!ws) return DGM_ERR_HIP;
+    if (!ws) return dgm::ws_error(g);
     int8_t* xp = reinterpret_cast<int8_t*>(ws);
     float* xs = reinterpret_cast<float*>(ws + ((xp_bytes + 255) & ~size_t(255)));
     hipLaunchKernelGGL((tiled_prepare_kernel<BITS, P>), dim3(s.M), dim3(256), 0, st, s.X, xp, xs, s.M, s.K, TP);
@@ -749,7 +749,7 @@ int dispatch_pieces(dgm_gpu* g, SkinnyArgs& a, hipStream_t st) {
     const int TT = T <= 4 ? T : (T <= 8 ? 8 : 12);
     const size_t xp_bytes = size_t(a.K / KBlock<BITS>::K) * TT * KBlock<BITS>::H * 1024;
     uint8_t* ws = static_cast<uint8_t*>(dgm::workspace(g, xp_bytes + 64 * sizeof(float) + 256));
-    if (!ws) return DGM_ERR_HIP;
+    if (!ws) return dgm::ws_error(g);
     int8_t* xp = reinterpret_cast<int8_t*>(ws);
     float* xs = reinterpret_cast<float*>(ws + ((xp_bytes + 255) & ~size_t(255)));
     hipLaunchKernelGGL((tiled_prepare_kernel<BITS, P>), dim3(M), dim3(256), 0, st, a.X, xp, xs, M, a.K, TT);

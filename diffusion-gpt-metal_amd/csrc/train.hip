@@ -382,7 +382,7 @@ int launch_sumsq(dgm_gpu* g, const float* x, float* out, int64_t n) {
         hipLaunchKernelGGL(sumsq_partial_kernel, dim3(1), dim3(kThreads), 0, g->stream, x, n, out);
     } else {
         float* part = static_cast<float*>(dgm::workspace(g, size_t(nb) * sizeof(float)));
-        if (!part) return g->first_err ? g->first_err : DGM_ERR_HIP;
+        if (!part) return dgm::ws_error(g);
         hipLaunchKernelGGL(sumsq_partial_kernel, dim3(unsigned(nb)), dim3(kThreads), 0, g->stream, x,
                            n, part);
         hipLaunchKernelGGL(sum_final_kernel, dim3(1), dim3(kThreads), 0, g->stream, part, nb, out);

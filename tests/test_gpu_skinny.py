@@ -100,11 +100,15 @@ def test_tiled_decode_many_chunks(gpu, dgm, orc, bits, G, K, M):
     w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
     bias = rng.standard_normal(N).astype(np.float32) if M % 2 == 0 else None
     q, s = _quantize(gpu, to_dev(w), N, K, G, bits)
-    ref = _ref(orc, q, s, x, bias, M, N, K, G, bits)
-    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_FP32)
-    assert rel_err(y, ref) <= 1e-5
-    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16)
-    assert rel_err(y, ref) <= 1e-2
+    ref = _ref(orc, q, s, x, bias, M, N, K, G, bits).reshape(M, N)
+    # Per row: row 0 is 1e-3 of the others, so a whole-output metric would
+    # let its error hide under the larger rows' maximum.
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_FP32).reshape(M, N)
+    worst = max(rel_err(y[m], ref[m]) for m in range(M))
+    assert worst <= 1e-5, worst
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16).reshape(M, N)
+    worst = max(rel_err(y[m], ref[m]) for m in range(M))
+    assert worst <= 1e-2, worst
 
 
 def test_rows_of_very_different_magnitude(gpu, dgm, orc):
