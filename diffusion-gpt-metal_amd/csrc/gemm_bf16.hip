@@ -67,22 +67,40 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// X fp32 -> bf16 (nearest even), 8 elements per thread.
+// X fp32 -> bf16 (nearest even). A block converts 1024 chunks of 8 floats:
+// thread t takes chunks t, t + 256, t + 512, t + 768 (consecutive threads on
+// consecutive 32-byte chunks), issuing all eight 16-byte loads before the
+// first conversion. X is read once here, so its loads bypass the caches'
+// retention (non-temporal); the bf16 copy is stored normally, to be re-read
+// by the GEMM.
+constexpr int CVT_CHUNKS = 4;
 __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict__ X, uint16_t* __restrict__ Xb,
                                                         int64_t n8) {
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n8) return;
-    const float4 a = reinterpret_cast<const float4*>(X)[2 * i];
-    const float4 b = reinterpret_cast<const float4*>(X)[2 * i + 1];
-    reinterpret_cast<uint4*>(Xb)[i] =
-        make_uint4(pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y), pack_bf16(b.z, b.w));
+    const int64_t base = int64_t(blockIdx.x) * (256 * CVT_CHUNKS) + threadIdx.x;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 v[2 * CVT_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < CVT_CHUNKS; ++c) {
+        const int64_t i = min(base + 256 * c, n8 - 1);
+        const f32x4* p = reinterpret_cast<const f32x4*>(X) + 2 * i;
+        v[2 * c] = __builtin_nontemporal_load(p);
+        v[2 * c + 1] = __builtin_nontemporal_load(p + 1);
+    }
+#pragma unroll
+    for (int c = 0; c < CVT_CHUNKS; ++c) {
+        const int64_t i = base + 256 * c;
+        if (i < n8)
+            reinterpret_cast<uint4*>(Xb)[i] =
+                make_uint4(pack_bf16(v[2 * c][0], v[2 * c][1]), pack_bf16(v[2 * c][2], v[2 * c][3]),
+                           pack_bf16(v[2 * c + 1][0], v[2 * c + 1][1]), pack_bf16(v[2 * c + 1][2], v[2 * c + 1][3]));
+    }
 }
 
 typedef __attribute__((address_space(1))) const void global_cvoid;
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Byte offset of 16-byte chunk c of row r in a swizzled operand tile.
-__device__ __forceinline__ int swz(int r, int c) { return r * RS + ((c ^ (r & 7)) << 4); }
+__device__ __forceinline__ int swz(int r, int c) { return r * RS + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4); }
 
 // ---- the kernel ------------------------------------------------------------------
 // Twelve waves: waves 0-7 only read LDS and issue MFMAs (a 64 x 128 block
@@ -124,7 +142,7 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int r = p * 64 + j * 8 + arl;
-            aoff[j] = uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8);
+            aoff[j] = uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7) ^ ((r >> 3) & 1)) * 8);
         }
         const int brow = p * 64 + lane;
         const int bn = min(n0 + brow, N - 1);
@@ -228,7 +246,8 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int cw0 = ((0 * 4 + q) ^ (l16 & 7)) << 4, cw1 = ((1 * 4 + q) ^ (l16 & 7)) << 4;
+    const int cw0 = ((0 * 4 + q) ^ (l16 & 7) ^ ((l16 >> 3) & 1)) << 4,
+              cw1 = ((1 * 4 + q) ^ (l16 & 7) ^ ((l16 >> 3) & 1)) << 4;
     auto compute = [&](int xs, int ws) {
         const uint8_t* As = smem + xs * TILE + (wm * 64 + l16) * RS;
         const uint8_t* Bs = smem + (3 + ws) * TILE + (wn * 128 + l16) * RS;
@@ -262,7 +281,7 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm * 64 + i * 16 + 4 * q + r;
-                if (row < M && col < N) a.Y[size_t(row) * N + col] = acc[i][j][r] + bv;
+                if (row < M && col < N) __builtin_nontemporal_store(acc[i][j][r] + bv, a.Y + size_t(row) * N + col);
             }
     }
 }
@@ -289,7 +308,8 @@ int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const floa
     if (!xb) return ws_error(g);
     hipStream_t st = g->stream;
     const int64_t n8 = mk / 8;
-    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, st, X, xb, n8);
+    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(unsigned((n8 + 256 * CVT_CHUNKS - 1) / (256 * CVT_CHUNKS))), dim3(256), 0,
+                       st, X, xb, n8);
 
     Bf16Args a{};
     a.Xb = xb;
