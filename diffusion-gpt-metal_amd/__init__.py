@@ -7,7 +7,7 @@ The directory name is not a Python identifier, so load it with
 """
 from .abi import (DGM_ERR_ARG, DGM_ERR_BITS, DGM_ERR_HIP, DGM_ERR_NOT_BEGUN,
                   DGM_ERR_SHAPE, DGM_ERR_UNSUPPORTED, DGM_MATH_BF16,
-                  DGM_MATH_FP32, DGM_OK, HEADER, LIB_PATH, PROTOTYPES,
+                  DGM_MATH_FP32, DGM_NOALLOC_SCRATCH_BYTES, DGM_OK, HEADER, LIB_PATH, PROTOTYPES,
                   DIT_LINEARS, DIT_NORMS, DgmError, DiTCfg, DiTLinear,
                   DiTWeights, GemmP, QuantP, AdamP, EmbP, EmbBwdP, PosP, BiasP,
                   ReduceP, ScaleP, UnaryP, DiTGrads, load_library)
@@ -20,7 +20,7 @@ __all__ = [
     "GPU", "Buf", "RawBuf", "GemmP", "QuantP", "DgmError", "load_library",
     "LIB_PATH", "HEADER", "PROTOTYPES", "DGM_OK", "DGM_ERR_ARG", "DGM_ERR_SHAPE",
     "DGM_ERR_NOT_BEGUN", "DGM_ERR_HIP", "DGM_ERR_BITS", "DGM_ERR_UNSUPPORTED",
-    "DGM_MATH_FP32", "DGM_MATH_BF16", "DiTBlock", "DiTConfig", "DiTCfg", "DiTLinear",
+    "DGM_MATH_FP32", "DGM_MATH_BF16", "DGM_NOALLOC_SCRATCH_BYTES", "DiTBlock", "DiTConfig", "DiTCfg", "DiTLinear",
     "DiTWeights", "DIT_LINEARS", "DIT_NORMS", "rope_tables", "AdamP", "EmbP", "EmbBwdP",
     "PosP", "BiasP", "ReduceP", "ScaleP", "UnaryP", "Param", "bias_corrections", "grad_norm",
     "optimizer_step", "zero_grads", "DiTGrads", "load_dit_block", "load_gpt", "read_tdit", "read_tgmt",

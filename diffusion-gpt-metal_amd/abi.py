@@ -23,6 +23,7 @@ DGM_ERR_UNSUPPORTED = 6
 
 DGM_MATH_FP32 = 0
 DGM_MATH_BF16 = 1
+DGM_NOALLOC_SCRATCH_BYTES = 8 << 20   # static scratch of dgm_gemmNT_noalloc (include/dgm_quant.h)
 
 
 class GemmP(ctypes.Structure):
@@ -163,6 +164,7 @@ PROTOTYPES = {
     "dgm_gemm_dw_acc": (_I, [_P, _P, _P, _P, _GP]),
     "dgm_quantize": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmNT": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_gemmNT_noalloc": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmDX": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmDW": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
     "dgm_gemmDWAcc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),

@@ -31,6 +31,11 @@ struct dgm_gpu {
     size_t ws_bytes = 0;
     void* retired[kMaxRetired] = {};
     int n_retired = 0;
+    // The static device scratch of the allocation-free entry point (its
+    // address on this context's device, resolved in dgm_gpu_create), and
+    // whether the current call draws its workspace from it instead.
+    void* scratch = nullptr;
+    bool use_scratch = false;
 };
 
 namespace dgm {
@@ -52,6 +57,8 @@ int check_launch(dgm_gpu* g, const char* name);
 void* workspace(dgm_gpu* g, size_t bytes);
 // The status a caller returns when workspace() gave nullptr.
 int ws_error(dgm_gpu* g);
+// Bytes of the static device scratch behind dgm_gemmNT_noalloc.
+constexpr size_t kScratchBytes = size_t(8) << 20;
 
 constexpr int64_t kMaxIndex = (int64_t(1) << 31) - 1;
 

@@ -1,9 +1,41 @@
 // Context lifecycle and dispatch-region semantics of the C ABI
 // (mirrors src/GPU.swift:118-198: init, begin, end, go's bookkeeping).
 #include <cstdarg>
+#include <mutex>
 #include <new>
 
 #include "common.hpp"
+
+namespace {
+
+// Scratch of the allocation-free entry point (dgm_gemmNT_noalloc): every
+// device holds its own copy from library load to process end. Host code uses
+// only the per-device address from hipGetSymbolAddress, never this name.
+__device__ __align__(256) uint8_t scratch[dgm::kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_addr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (current), resolved once per
+// device. Returns nullptr (and the HIP error) when it cannot be resolved.
+void* scratch_for(int device, hipError_t* err) {
+    *err = hipSuccess;
+    if (device < 0 || device >= kMaxDevices) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_addr[device]) {
+        void* p = nullptr;
+        *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (*err != hipSuccess) return nullptr;
+        scratch_addr[device] = p;
+    }
+    return scratch_addr[device];
+}
+
+}  // namespace
 
 namespace dgm {
 
@@ -36,6 +68,19 @@ int check_launch(dgm_gpu* g, const char* name) {
 }
 
 void* workspace(dgm_gpu* g, size_t bytes) {
+    if (g->use_scratch) {
+        // dgm_gemmNT_noalloc: the static scratch or nothing, never hipMalloc.
+        if (!g->scratch) {
+            fail(g, DGM_ERR_HIP, "the static scratch of device %d could not be resolved", g->device);
+            return nullptr;
+        }
+        if (bytes > kScratchBytes) {
+            fail(g, DGM_ERR_UNSUPPORTED, "this call needs %zu bytes of scratch; the static scratch holds %zu", bytes,
+                 kScratchBytes);
+            return nullptr;
+        }
+        return g->scratch;
+    }
     if (bytes <= g->ws_bytes) return g->ws;
     // Growing inside a graph capture would bake a fresh allocation into the
     // graph (and hipMalloc is not capturable): refuse, and let the caller make
@@ -83,6 +128,10 @@ int dgm_gpu_create(dgm_gpu** out) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, g->device) == hipSuccess && prop.multiProcessorCount > 0)
         g->num_cus = prop.multiProcessorCount;
+    // The allocation-free entry point's scratch on this device (resolved once
+    // per device; a failure surfaces only when that entry point is called).
+    hipError_t se;
+    g->scratch = scratch_for(g->device, &se);
     // A blocking stream: it orders itself after work on the null stream, where
     // callers that allocate with torch or hipMemset may still be filling the
     // buffers they hand over.

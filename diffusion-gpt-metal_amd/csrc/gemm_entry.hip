@@ -123,6 +123,18 @@ int dgm_gemmNT(dgm_gpu* g, int64_t bits, const float* w, const void* q, const fl
     }
 }
 
+int dgm_gemmNT_noalloc(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale,
+                       const float* x, const float* bias, float* y, int64_t M, int64_t N, int64_t K, int64_t qGroup) {
+    // dgm_gemmNT with every staging buffer taken from the static device
+    // scratch: nothing is allocated, and a call that would need more than
+    // kScratchBytes fails with DGM_ERR_UNSUPPORTED before launching anything.
+    if (!g) return DGM_ERR_ARG;
+    g->use_scratch = true;
+    const int rc = dgm_gemmNT(g, bits, w, q, scale, x, bias, y, M, N, K, qGroup);
+    g->use_scratch = false;
+    return rc;
+}
+
 int dgm_gemmDX(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale,
                const float* dy, float* dx, int64_t M, int64_t N, int64_t K, int64_t qGroup) {
     if (!g) return DGM_ERR_ARG;

@@ -111,6 +111,12 @@ class GPU:
         self._check(self.lib.dgm_gemmNT(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(x),
                                         _ptr(bias), _ptr(y), M, N, K, qGroup))
 
+    def gemmNT_noalloc(self, bits: int, w, q, scale, x, bias, y, M: int, N: int, K: int, qGroup: int) -> None:
+        """gemmNT with staging in the library's static device scratch (no
+        allocation; DGM_ERR_UNSUPPORTED when the call needs more scratch)."""
+        self._check(self.lib.dgm_gemmNT_noalloc(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(x),
+                                                 _ptr(bias), _ptr(y), M, N, K, qGroup))
+
     def gemmDX(self, bits: int, w, q, scale, dy, dx, M: int, N: int, K: int, qGroup: int) -> None:
         self._check(self.lib.dgm_gemmDX(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(dy),
                                         _ptr(dx), M, N, K, qGroup))

@@ -139,6 +139,23 @@ int dgm_quantize(dgm_gpu* g, const float* w, void* q, float* scale,
 int dgm_gemmNT(dgm_gpu* g, int64_t bits, const float* w, const void* q,
                const float* scale, const float* x, const float* bias, float* y,
                int64_t M, int64_t N, int64_t K, int64_t qGroup);
+/* No counterpart in the reference: dgm_gemmNT for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, kernels and results
+ * (bitwise) as dgm_gemmNT, but every staging buffer (the decode kernels'
+ * activation pieces, the bf16 copy of X of the reduced-precision prefill
+ * path) comes from a static device scratch of DGM_NOALLOC_SCRATCH_BYTES per
+ * GPU, held from library load until the process ends; nothing is allocated.
+ * A call that would need more scratch returns DGM_ERR_UNSUPPORTED before
+ * launching anything (the decode path needs about 192 * K bytes at M <= 64;
+ * the bf16 prefill path 2 * M * K bytes). Every such call on one GPU shares
+ * that scratch, which keeps the last call's contents (no kernel relies on it
+ * starting at zero): calls that overlap in time on one GPU (other streams,
+ * other contexts, other threads) race and must be serialized by the caller. */
+#define DGM_NOALLOC_SCRATCH_BYTES (8u << 20)
+int dgm_gemmNT_noalloc(dgm_gpu* g, int64_t bits, const float* w, const void* q,
+                       const float* scale, const float* x, const float* bias, float* y,
+                       int64_t M, int64_t N, int64_t K, int64_t qGroup);
 /* GPU.gemmDX (src/GPU.swift:245-260). */
 int dgm_gemmDX(dgm_gpu* g, int64_t bits, const float* w, const void* q,
                const float* scale, const float* dy, float* dx,

@@ -1,0 +1,124 @@
+"""dgm_gemmNT_noalloc: dgm_gemmNT with its staging buffers in the library's
+static device scratch, called through the C ABI.
+
+* On each forward path that stages data (decode pieces at M <= 64 in both
+  math modes, the bf16 prefill path's bf16 copy of X) and on one that stages
+  nothing (fp32 tiles), two calls in a row, the second with a smaller input,
+  return exactly dgm_gemmNT's bytes.
+* On a fresh context the call can be captured in a HIP graph (nothing to
+  allocate), and every replay, with eager work between replays, matches the
+  eager result.
+* A call that needs more scratch than the library holds fails with
+  DGM_ERR_UNSUPPORTED and leaves its output untouched.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(gpu, M, N, K, G, bits, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    x = to_dev(rng.standard_normal(M * K).astype(np.float32))
+    w = to_dev((rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    bias = to_dev(rng.standard_normal(N).astype(np.float32)) if seed % 2 else None
+    q = torch.zeros(N * K // (2 if bits == 4 else 1), dtype=torch.uint8 if bits == 4 else torch.int8, device="cuda")
+    s = torch.zeros(N * (K // G), device="cuda")
+    gpu.begin()
+    gpu.quantize(w, q, s, N, K, bits, G)
+    gpu.end()
+    return x, q, s, bias
+
+
+def _both(gpu, dgm, math, bits, M, N, K, G, seed):
+    import torch
+    x, q, s, bias = _case(gpu, M, N, K, G, bits, seed)
+    ya = torch.full((M * N,), float("nan"), device="cuda")
+    yb = torch.full((M * N,), float("nan"), device="cuda")
+    gpu.set_math(math)
+    try:
+        gpu.begin()
+        gpu.gemmNT(bits, None, q, s, x, bias, ya, M, N, K, G)
+        gpu.gemmNT_noalloc(bits, None, q, s, x, bias, yb, M, N, K, G)
+        gpu.end()
+    finally:
+        gpu.set_math(dgm.DGM_MATH_FP32)
+    return from_dev(ya), from_dev(yb)
+
+
+# (math, bits, first shape, second shape): decode pieces (fused, prepared,
+# tiled), bf16 prefill, fp32 tiles (no staging).
+CASES = [
+    ("fp32", 4, (16, 1024, 4096, 128), (3, 520, 2048, 128)),
+    ("fp32", 8, (64, 700, 2048, 64), (7, 300, 1024, 64)),
+    ("bf16", 4, (64, 900, 4096, 128), (16, 256, 1024, 128)),
+    ("bf16", 4, (1024, 768, 2048, 128), (300, 500, 1024, 32)),
+    ("bf16", 8, (512, 512, 1024, 64), (130, 260, 512, 32)),
+    ("fp32", 4, (512, 192, 768, 32), (100, 64, 256, 32)),
+]
+
+
+@pytest.mark.parametrize("math,bits,first,second", CASES)
+def test_matches_gemmNT_twice(gpu, dgm, math, bits, first, second):
+    mode = dgm.DGM_MATH_FP32 if math == "fp32" else dgm.DGM_MATH_BF16
+    for i, (M, N, K, G) in enumerate((first, second)):
+        ya, yb = _both(gpu, dgm, mode, bits, M, N, K, G, 17 * i + M)
+        assert np.all(np.isfinite(ya))
+        assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (math, bits, M, N, K, G)
+
+
+def test_captured_on_a_fresh_context(dgm, orc, torch_cuda):
+    torch = torch_cuda
+    stream = torch.cuda.Stream()
+    g = dgm.GPU(stream=stream)   # empty workspace: the regular entry would have to allocate
+    try:
+        M, N, K, G = 16, 512, 2048, 128
+        x, q, s, _ = _case(g, M, N, K, G, 4, 5)
+        y = torch.zeros(M * N, device="cuda")
+        ref = torch.zeros(M * N, device="cuda")
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            g.begin()
+            g.gemmNT_noalloc(4, None, q, s, x, None, y, M, N, K, G)
+        with torch.cuda.stream(stream):
+            g.begin()
+            g.gemmNT(4, None, q, s, x, None, ref, M, N, K, G)
+            g.end()
+        want = from_dev(ref)
+        for _ in range(3):
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                graph.replay()
+            stream.synchronize()
+            assert np.array_equal(from_dev(y).view(np.uint32), want.view(np.uint32))
+        del graph
+    finally:
+        torch.cuda.synchronize()
+        g.close()
+
+
+def test_too_large_is_refused(gpu, dgm):
+    import torch
+    # bf16 prefill: its bf16 copy of X needs 2*M*K bytes > the scratch.
+    M, N, K, G = 2048, 256, 4096, 128
+    assert 2 * M * K > dgm.DGM_NOALLOC_SCRATCH_BYTES
+    x, q, s, _ = _case(gpu, M, N, K, G, 4, 9)
+    y = torch.full((M * N,), 7.0, device="cuda")
+    gpu.set_math(dgm.DGM_MATH_BF16)
+    try:
+        gpu.begin()
+        with pytest.raises(dgm.DgmError) as e:
+            gpu.gemmNT_noalloc(4, None, q, s, x, None, y, M, N, K, G)
+        assert e.value.code == dgm.DGM_ERR_UNSUPPORTED
+        gpu.begin()
+        gpu.end()
+    finally:
+        gpu.set_math(dgm.DGM_MATH_FP32)
+    assert np.all(from_dev(y) == 7.0)
