@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import argparse
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -49,14 +50,42 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libdgm_amd.so)")
 
 
+# Sources whose kernels issue loads as inline asm and wait for them by hand
+# (gemm_decode.hip): a register spilled or copied while such a load is in
+# flight would be read before the load fills it, so these kernels must not
+# use scratch. The build checks the compiler's resource-usage remarks.
+NO_SCRATCH = {"gemm_decode.hip"}
+REMARK = "-Rpass-analysis=kernel-resource-usage"
+
+
+def _scratch_users(stderr: str) -> list:
+    users, fn = [], None
+    for line in stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            fn = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and fn and int(m.group(1)) > 0:
+            users.append(f"{fn} ({m.group(1)} bytes/lane)")
+    return users
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    check = os.path.basename(src) in NO_SCRATCH
+    cmd = [hipcc(), *HIPCC_FLAGS, *([REMARK] if check else []), "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    lines = [l for l in proc.stderr.splitlines() if noise not in l]
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+        raise RuntimeError(f"hipcc failed for {src}:\n" + "\n".join(lines))
+    if check:
+        bad = _scratch_users(proc.stderr)
+        if bad:
+            os.remove(obj)
+            raise RuntimeError(f"{src}: kernels with hand-waited loads use scratch: {', '.join(bad)}")
+        lines = [l for l in lines if REMARK not in l]
+    err = "\n".join(lines)
     if err.strip():
         sys.stderr.write(err + "\n")
     return obj

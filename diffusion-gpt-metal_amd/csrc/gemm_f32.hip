@@ -1327,6 +1327,10 @@ int check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits) {
 namespace dgm {
 
 bool skinny_ok(int bits, const void* W, const float* X, const dgm_GemmP* p);
+bool skinny_fused_ok(dgm_gpu* g, int bits, const void* W, const float* X, const dgm_GemmP* p);
+bool decode_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
+int decode_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X, const float* bias, float* Y,
+               const dgm_GemmP* p);
 int skinny_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
                const float* bias, float* Y, const dgm_GemmP* p);
 bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
@@ -1336,7 +1340,13 @@ int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const floa
 // Entry used by the dispatcher in gemm_entry.hip; declared there.
 int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
                  const float* bias, float* Y, const dgm_GemmP* p) {
-    // Decode-shaped quantized forwards stream W once through int8 MFMA.
+    // Decode-shaped quantized forwards stream W once. GEMV-like calls (a few
+    // rows) take the int8-MFMA kernel, whose weight unpack is three bit
+    // operations per 8 weights and whose activation pieces fill spare MFMA
+    // rows; more rows take f16 MFMA over exact f16 activation pieces
+    // (gemm_decode.hip), or the int8-MFMA kernel outside that domain.
+    if (skinny_fused_ok(g, bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
+    if (decode_ok(bits, W, X, scale, p)) return decode_fwd(g, bits, W, scale, X, bias, Y, p);
     if (skinny_ok(bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
     // Larger M in the reduced-precision mode: bf16 MFMA with W dequantized in LDS.
     if (g->math == DGM_MATH_BF16 && bf16_ok(bits, W, X, scale, p))

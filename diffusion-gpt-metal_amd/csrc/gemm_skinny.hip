@@ -105,16 +105,16 @@ __device__ __forceinline__ int row_sigma(float maxabs) {
     return 6 - e;
 }
 
-__device__ __forceinline__ void split_pieces(float x, int sigma, int (&c)[3]) {
-    const float u = ldexpf(x, sigma);           // exact scaling
-    const float a = rintf(u);
-    const float t = (u - a) * 128.0f;           // u - a and the *128 are exact
-    const float b = rintf(t);
-    const float t2 = (t - b) * 128.0f;
-    const float d = rintf(t2);
-    c[0] = int(a);
-    c[1] = int(b);
-    c[2] = int(d);
+// u = x * 2^sigma = c0 + c1 / 128 + c2 / 128^2 + c3 / 128^3 + r, |r| <= 2^-22:
+// every step (the difference and the scaling by 128) is exact in fp32.
+__device__ __forceinline__ void split_pieces(float x, int sigma, int (&c)[4]) {
+    float t = ldexpf(x, sigma);   // exact scaling
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = rintf(t);
+        c[i] = int(a);
+        t = (t - a) * 128.0f;
+    }
 }
 
 // Writes the P pieces of 16 consecutive elements x[k0 .. k0+15] of one row to
@@ -122,7 +122,7 @@ __device__ __forceinline__ void split_pieces(float x, int sigma, int (&c)[3]) {
 template <int BITS, int P>
 __device__ __forceinline__ void store_pieces16(int8_t* const (&base)[P], int k0, const float (&x)[16],
                                                int sigma) {
-    int c[16][3];
+    int c[16][4];
 #pragma unroll
     for (int i = 0; i < 16; ++i) split_pieces(x[i], sigma, c[i]);
 #pragma unroll
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(256) void tiled_prepare_kernel(const float* __restr
             const float4 v = *reinterpret_cast<const float4*>(xr + k0 + 4 * i);
             x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
         }
-        int c[16][3];
+        int c[16][4];
 #pragma unroll
         for (int i = 0; i < 16; ++i) split_pieces(x[i], sigma, c[i]);
         const int kb = k0 / KBK, kk = k0 - kb * KBK;
@@ -725,17 +725,25 @@ bool tiled_fits(const SkinnyArgs& s) {
     return lds <= 160 * 1024 && size_t(16) * SH::TP * 64 * 4 <= 2 * size_t(SH::BUF);
 }
 
+// GEMV-like calls prepare X inside every workgroup (no second launch): at
+// most 4 rows (the kernel's row registers), P * M virtual rows in one 16-row
+// tile, and a wave's k-range (a quarter of K) at most 64 lanes x 16 elements.
+bool fused_fits(int bits, int M, int K, int P) {
+    const int kbk = bits == 4 ? 128 : 64;
+    return M <= 4 && P * M <= 16 && ((K / kbk + 3) / 4) * kbk <= 1024;
+}
+
+template <int BITS, int P>
+int launch_fused(dgm_gpu* g, SkinnyArgs& a, hipStream_t st) {
+    if (a.M == 1) return launch_skinny<BITS, P, 1, 2, 8, 4, 1>(g, a, st);
+    return launch_skinny<BITS, P, 1, 2, 8, 4, 4>(g, a, st);
+}
+
 template <int BITS, int P>
 int dispatch_pieces(dgm_gpu* g, SkinnyArgs& a, hipStream_t st) {
     const int M = a.M;
     const int rows = P * M;
-    // GEMV-like calls prepare X inside every workgroup (no second launch):
-    // a wave's k-range is at most 64 lanes x 16 elements.
-    const int nkb = a.K / KBlock<BITS>::K;
-    if (rows <= 16 && ((nkb + 3) / 4) * KBlock<BITS>::K <= 1024) {
-        if (M == 1) return launch_skinny<BITS, P, 1, 2, 8, 4, 1>(g, a, st);
-        if (M <= 4) return launch_skinny<BITS, P, 1, 2, 8, 4, 4>(g, a, st);
-    }
+    if (fused_fits(BITS, M, a.K, P)) return launch_fused<BITS, P>(g, a, st);
     // Beyond 4 tiles of virtual rows the accumulators of the k-split kernel
     // crowd the register file; the tiled kernel splits the rows over waves.
     if (rows > 64 && rows <= 192) {
@@ -797,8 +805,21 @@ int skinny_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const fl
     a.gshift = __builtin_ctz(p->qGroup / (bits == 4 ? 128u : 64u));
     const bool exact = g->math == DGM_MATH_FP32;
     hipStream_t st = g->stream;
+    // The fp32 mode takes four pieces where they fit one tile (M <= 4): the
+    // pieces then hold 2^-27 of the maximum of each wave's k-range, so an
+    // outlier costs its neighbours nothing measurable. Elsewhere three.
+    if (exact && fused_fits(bits, a.M, a.K, 4))
+        return bits == 4 ? launch_fused<4, 4>(g, a, st) : launch_fused<8, 4>(g, a, st);
     if (bits == 4) return exact ? dispatch_pieces<4, 3>(g, a, st) : dispatch_pieces<4, 2>(g, a, st);
     return exact ? dispatch_pieces<8, 3>(g, a, st) : dispatch_pieces<8, 2>(g, a, st);
+}
+
+// The GEMV-like shapes (M <= 3) where the skinny kernel's one-launch path
+// applies in the current math mode (four pieces in the fp32 mode, two in the
+// reduced one). From M = 4 on, the f16 decode kernel is as fast (c4 shape).
+bool skinny_fused_ok(dgm_gpu* g, int bits, const void* W, const float* X, const dgm_GemmP* p) {
+    if (p->M > 3 || !skinny_ok(bits, W, X, p)) return false;
+    return fused_fits(bits, int(p->M), int(p->K), g->math == DGM_MATH_FP32 ? 4 : 2);
 }
 
 }  // namespace dgm

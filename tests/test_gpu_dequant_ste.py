@@ -101,12 +101,14 @@ def test_dequant_exact_fp32_tiles(gpu, dgm, orc, bits, K, N, G):
 @pytest.mark.parametrize("bits,G", [(4, 128), (4, 256), (8, 64), (8, 128)])
 @pytest.mark.parametrize("M", [1, 16, 64])
 @pytest.mark.parametrize("math", ["fp32", "bf16"])
-def test_dequant_exact_decode(gpu, dgm, orc, bits, G, M, math):
-    """M <= 64: the decode kernels (int8 MFMA over exact activation pieces).
-    Each call selects M weights per row of W with a one-hot row per output
-    row; the calls cover every k of the matrix (M = 1: the first group and a
-    spread of single columns)."""
-    N, K = 72, 2 * max(G, 128)
+@pytest.mark.parametrize("span", [2, 4])
+def test_dequant_exact_decode(gpu, dgm, orc, bits, G, M, math, span):
+    """M <= 64: the decode kernels (f16 MFMA over exact activation pieces;
+    span 4 gives a multiple of four groups, the one-launch kernel's domain at
+    M <= 16). Each call selects M weights per row of W with a one-hot row per
+    output row; the calls cover every k of the matrix (M = 1: the first group
+    and a spread of single columns)."""
+    N, K = 72, span * max(G, 128)
     w = _weights(N, K, M + G + bits)
     q, s = _quantize(gpu, w, N, K, G, bits)
     deq = _deq(orc, q, s, N, K, G, bits)

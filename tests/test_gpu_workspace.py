@@ -38,20 +38,22 @@ def test_graph_survives_workspace_growth(dgm, orc, torch_cuda):
     stream = torch.cuda.Stream()
     gpu = dgm.GPU(stream=stream)
     try:
+        # M = 32 and 64: the decode path that stages prepared activation
+        # pieces in the workspace (M <= 16 converts them inside the kernel).
         N, K, G = 512, 2048, 128
-        xs, qs, ss, refs = _setup(gpu, orc, 16, N, K, G, 1)
+        xs, qs, ss, refs = _setup(gpu, orc, 32, N, K, G, 1)
         xl, ql, sl, refl = _setup(gpu, orc, 64, N, K * 4, G, 2)
-        ys = torch.zeros(16 * N, device="cuda")
+        ys = torch.zeros(32 * N, device="cuda")
         yl = torch.zeros(64 * N, device="cuda")
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
             gpu.begin()
-            gpu.gemmNT(4, None, qs, ss, xs, None, ys, 16, N, K, G)   # sizes the workspace
+            gpu.gemmNT(4, None, qs, ss, xs, None, ys, 32, N, K, G)   # sizes the workspace
             gpu.end()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             gpu.begin()
-            gpu.gemmNT(4, None, qs, ss, xs, None, ys, 16, N, K, G)
+            gpu.gemmNT(4, None, qs, ss, xs, None, ys, 32, N, K, G)
         gpu.begin()
         # A larger call grows the workspace (4x the pieces).
         with torch.cuda.stream(stream):
@@ -76,16 +78,18 @@ def test_growth_during_capture_is_refused(dgm, orc, torch_cuda):
     stream = torch.cuda.Stream()
     gpu = dgm.GPU(stream=stream)   # a fresh context: empty workspace
     try:
-        N, K, G = 256, 1024, 128
-        x, q, s, ref = _setup(gpu, orc, 16, N, K, G, 3)
-        y = torch.zeros(16 * N, device="cuda")
+        # M = 64: the decode path that stages prepared activation pieces in
+        # the workspace (M <= 16 converts them inside the kernel instead).
+        M, N, K, G = 64, 256, 1024, 128
+        x, q, s, ref = _setup(gpu, orc, M, N, K, G, 3)
+        y = torch.zeros(M * N, device="cuda")
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         err = None
         with torch.cuda.graph(graph, stream=stream):
             gpu.begin()
             try:
-                gpu.gemmNT(4, None, q, s, x, None, y, 16, N, K, G)
+                gpu.gemmNT(4, None, q, s, x, None, y, M, N, K, G)
             except dgm.DgmError as e:
                 err = e
         assert err is not None and err.code == dgm.DGM_ERR_UNSUPPORTED, err
@@ -93,7 +97,7 @@ def test_growth_during_capture_is_refused(dgm, orc, torch_cuda):
         # Outside capture the same call sizes the workspace and succeeds.
         with torch.cuda.stream(stream):
             gpu.begin()
-            gpu.gemmNT(4, None, q, s, x, None, y, 16, N, K, G)
+            gpu.gemmNT(4, None, q, s, x, None, y, M, N, K, G)
             gpu.end()
         assert rel_err(from_dev(y), ref) <= 1e-5
     finally:
