@@ -53,6 +53,8 @@
 // results).
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -60,6 +62,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int DEC_COLS = 64;                 // W rows (output columns) per workgroup
 constexpr int DEC_SLOTS = 4;                 // intervals (4 chunks each) in the weight ring
@@ -202,11 +205,11 @@ struct Schedule {
 // (d & m & ~f) | (~d & m & f) | (~m & c): the bits of d under the mask m,
 // flipped where f is set, the constant c elsewhere. One v_bitop3 with f and c
 // packed into one operand (they never overlap): truth table 0x6A over
-// (d, m, fc) (table bit (d << 2) | (m << 1) | fc).
+// (d, m, fc) (table bit (d << 2) | (m << 1) | fc). The builtin, not inline
+// asm, so that the compiler sees the result register: an MFMA that reads a
+// VALU result needs wait states the compiler inserts only for what it sees.
 __device__ __forceinline__ uint32_t pick_flip(uint32_t d, uint32_t m, uint32_t fc) {
-    uint32_t r;
-    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6A" : "=v"(r) : "v"(d), "v"(m), "v"(fc));
-    return r;
+    return __builtin_amdgcn_bitop3_b32(d, m, fc, 0x6A);
 }
 
 // One code dword (int4: 8 nibbles; int8: 4 bytes) -> f16 pairs in frag_k
@@ -231,6 +234,18 @@ __device__ __forceinline__ void codes_to_f16(uint32_t dw, f16x2* out) {
         out[0] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, pick_flip(dw, mlo, flo)), s1, o1);   // k 0, 2
         out[1] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, pick_flip(y, mlo, flo)), s1, o1);    // k 1, 3
     }
+}
+
+// One int4 code dword (8 nibbles) -> bf16 pairs 128 + (code + 8), in frag_k
+// order: bf16 keeps 7 mantissa bits, so each nibble goes to bits 0-3 of its
+// half (three shifts) and is flipped to offset binary under the exponent of
+// 128.0 (0x4300) by one v_bitop3. The offset 136 = 128 + 8 is removed in the
+// accumulator (see the reduced-precision path of decode_small_kernel).
+__device__ __forceinline__ bf16x8 codes_to_bf16_off(uint32_t dw) {
+    const uint32_t m = 0x000F000Fu, fc = 0x43084308u;
+    const u32x4 o = {pick_flip(dw, m, fc), pick_flip(dw >> 4, m, fc), pick_flip(dw >> 8, m, fc),
+                     pick_flip(dw >> 12, m, fc)};   // k 0,4 | 1,5 | 2,6 | 3,7
+    return __builtin_bit_cast(bf16x8, o);
 }
 
 // Five waves: waves 0-3 compute (wave w takes chunks w, w + 4, ...: interval
@@ -482,11 +497,27 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
 // half-block global -> LDS with direct-to-LDS loads (whole 256- or 128-byte
 // row runs; 16-byte slots XOR-swizzled by row, so the fragment reads are
 // conflict-free), two half-blocks ahead, into a private three-slot ring: no
-// other wave reads it, so no barrier guards it. The stream wave moves the
+// other wave reads it, so nothing guards it. The stream wave moves the
 // workgroup's scales once and the weight blocks per interval (interval t =
 // k-blocks 4t .. 4t+3) into a three-interval ring. The loop is unrolled over
 // the ring so that every LDS slot offset is an immediate. Each half-block has
 // its own power-of-two activation factor.
+//
+// No workgroup barrier per interval (it would hold both waves of a SIMD in
+// the same phase): the stream wave publishes in LDS how many intervals have
+// landed (after its own load-counter wait), each compute wave adds one to
+// its slot's count when it has read an interval, and the stream wave refills
+// a slot only when all eight waves have read it. A wave's LDS operations are
+// performed in issue order, so a count raised after a wave's reads is seen
+// only after those reads. Every wait is bounded (DS_SPIN rounds of s_sleep):
+// a fault in this protocol gives wrong results, never a hang.
+//
+// Reduced-precision int4 (one piece) runs on bf16 instead: x rounded to bf16
+// keeps its own exponent (no block maximum, no factor, no rescale), and the
+// codes enter as 128 + (code + 8), exact in bf16. The offset is removed inside
+// the accumulator: one more MFMA per step multiplies the same activations by
+// the constant -136, and the code MFMAs of every column tile accumulate onto
+// that. The fp32 partial then only takes the group scale.
 //
 // A non-finite activation propagates: NaN gives a NaN output row, an infinity
 // an infinite or NaN one (two pieces: NaN, as inf - f16(inf) is NaN).
@@ -500,8 +531,10 @@ constexpr int DS_WINT = 4 * DS_WBLK;         // one interval
 constexpr int DS_XOFF = 0;
 constexpr int DS_WOFF = DS_XOFF + DS_CW * DS_XS * DS_XSLOT;   // 96 KB
 constexpr int DS_SOFF = DS_WOFF + DS_WS * DS_WINT;            // 144 KB
-constexpr int DS_SMAX = 16384;                                // scales of 64 rows: groups <= 64
-constexpr int DS_LDS = DS_SOFF + DS_SMAX;                     // 160 KB
+constexpr int DS_SMAX = 16384 - 16;                           // scales of 64 rows: groups <= 63
+constexpr int DS_FOFF = DS_SOFF + DS_SMAX;                    // hand-over counters (4 x u32)
+constexpr int DS_LDS = DS_FOFF + 16;                          // 160 KB
+constexpr int DS_SPIN = 1 << 22;                              // bound of every hand-over wait
 static_assert(DS_XS == DS_WS, "one unrolled loop walks both rings");
 static_assert(DS_CW * 16 * 64 * 4 <= DS_WOFF, "the partials fit the activation slots");
 
@@ -517,6 +550,8 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
     constexpr int RPI = 1024 / XROW;            // rows per DMA instruction (4 or 8)
     constexpr int PQ = KLH / 4;                 // pieces per lane group q (4 or 2)
     constexpr int RSH = 16 / PR;                // rows sharing a 256-byte bank sweep (1 or 2)
+    constexpr bool BF = BITS == 4 && P == 1;    // reduced-precision int4: bf16 path
+    using XF = std::conditional_t<BF, bf16x8, f16x8>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -527,26 +562,32 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
     const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
     // Slot of activation piece p of row r: conflict-free for 16 consecutive rows.
     auto xslot = [](int p, int r) { return p ^ ((r / RSH) % PR); };
+    // Hand-over counters: [0] intervals landed, [1 + s] reads of ring slot s
+    // (an LDS pointer, so that polling them is a ds_read).
+    typedef __attribute__((address_space(3))) uint32_t lds_u32;
+    volatile lds_u32* cnt = (volatile lds_u32*)(reinterpret_cast<uintptr_t>(smem) + DS_FOFF);
+    if (threadIdx.x < 4) cnt[threadIdx.x] = 0u;
+    __syncthreads();
+    auto wait_for = [&](int i, uint32_t want) {
+#pragma nounroll
+        for (int spin = 0; spin < DS_SPIN; ++spin) {
+            if (__builtin_amdgcn_readfirstlane(cnt[i]) >= want) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");
+    };
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
     if (w == DS_CW) {
-        // ---- stream wave: the scales of rows n0 .. n0+63 (row-major, once),
-        // then weight interval t into slot t % DS_WS, two intervals ahead.
-        // Weight DMA instruction i of a block covers rows 16i .. 16i+15: lane
-        // l lands at slot l % 4 of row 16i + l / 4 and fetches the piece
-        // that belongs there (slot = piece ^ ((row >> 2) & 3)).
+        // ---- stream wave: weight interval t into slot t % DS_WS, two
+        // intervals ahead, and once (after interval 0) the scales of rows
+        // n0 .. n0+63, transposed to [group][64 columns]: one 4-byte gather
+        // per group. Weight DMA instruction i of a block covers rows
+        // 16i .. 16i+15: lane l lands at slot l % 4 of row 16i + l / 4 and
+        // fetches the piece that belongs there (slot = piece ^ ((row >> 2) & 3)).
         // M0 carries the LDS destination of a direct-to-LDS load. The
         // compiler reserves M0 but uses it in this kernel for nothing else.
-        const int spr = a.groups / 4;   // 16-byte pieces per scale row = DMA instructions
-        for (int i = 0; i < spr; ++i) {
-            const int p = 64 * i + lane;
-            const int r = p / spr, pc = p - r * spr;
-            const uint32_t src = (uint32_t(min(n0 + r, a.N - 1)) * uint32_t(a.groups) + 4u * uint32_t(pc)) * 4u;
-            asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds0 + DS_SOFF + i * 1024),
-                         "v"(src), "s"(a.S)
-                         : "memory", "m0");
-        }
         uint32_t woff[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -567,6 +608,11 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
             }
         };
         dma_interval(0);
+        const uint32_t srow = uint32_t(min(n0 + lane, a.N - 1)) * uint32_t(a.groups) * 4u;
+        for (int g = 0; g < a.groups; ++g)
+            asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds0 + DS_SOFF + g * 256),
+                         "v"(srow + 4u * uint32_t(g)), "s"(a.S)
+                         : "memory", "m0");
         if (T > 1) dma_interval(1);
         for (int t = 0; t < T; ++t) {
             // Interval t (and the scales) have landed; interval t + 1 (16
@@ -575,8 +621,13 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
                 asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
             else
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (t + 2 < T) dma_interval(t + 2);   // slot of t - 1: every wave is past it
+            cnt[0] = uint32_t(t + 1);
+            if (t + 2 < T) {
+                // Interval t + 2 refills the slot of t - 1 once all eight
+                // compute waves have read t - 1 (its (t - 1) / 3 + 1-th use).
+                if (t >= 1) wait_for(1 + (t - 1) % DS_WS, uint32_t(DS_CW * ((t - 1) / DS_WS + 1)));
+                dma_interval(t + 2);
+            }
         }
         __syncthreads();   // compute waves past their last block
         __syncthreads();   // partials written
@@ -613,8 +664,8 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
         const int r = 16 * ct + c;
         wo[ct] = DS_WOFF + wb * DS_WBLK + r * 64 + (((2 * h + (q >> 1)) ^ ((r >> 2) & 3)) << 4) + ((q & 1) << 3);
     }
-    // Scales of the lane's output columns 16 ct + 4 q + r (row-major [64][groups]).
-    const uint32_t so = DS_SOFF + uint32_t(4 * q * a.groups) * 4u;
+    // Scales of the lane's output columns 16 ct + 4 q .. + 3 ([group][64]).
+    const uint32_t so = DS_SOFF + 16u * uint32_t(q);
 
     // The MFMA takes the weights as A and the activations as B, so the
     // accumulator element r of lane (q, c) is output column 16 ct + 4 q + r
@@ -626,13 +677,21 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
     // Activation pieces of a half-block: row c, k = KLH q .. KLH q + KLH - 1,
     // against the power of two 2^e of the row's half-block maximum (the four
     // lanes q of row c meet through two lane swaps). No branch.
-    auto convert_x = [&](int slot, f16x8 (&xa)[SPH][P], float& inv) {
+    auto convert_x = [&](int slot, XF (&xa)[SPH][P], float& inv) {
         float v[KLH];
 #pragma unroll
         for (int i = 0; i < PQ; ++i) {
             const f32x4 f = *reinterpret_cast<const f32x4*>(smem + xo[i] + slot * DS_XSLOT);
             v[4 * i] = f[0]; v[4 * i + 1] = f[1]; v[4 * i + 2] = f[2]; v[4 * i + 3] = f[3];
         }
+        if constexpr (BF) {
+#pragma unroll
+            for (int kk = 0; kk < SPH; ++kk)
+#pragma unroll
+                for (int t8 = 0; t8 < 8; ++t8) xa[kk][0][t8] = __bf16(v[frag_k<BITS>(0, kk, t8)]);
+            inv = 1.0f;
+            return;
+        } else {
         float mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < KLH; ++i) mx = fmaxf(mx, fabsf(v[i]));
@@ -662,22 +721,40 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
                 xa[kk][0][t8] = h1;
                 if constexpr (P == 2) xa[kk][1][t8] = _Float16(__builtin_fmaf(xv, pw, -float(h1)));
             }
+        }
     };
 
     // The half-block's weights (interval slot) against the converted activations.
-    auto weights = [&](int t, int slot, const f16x8 (&xa)[SPH][P], float inv) {
+    auto weights = [&](int t, int slot, const XF (&xa)[SPH][P], float inv) {
         const int gb = 4 * t + wb;
         u32x2 wd[4];
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) wd[ct] = *reinterpret_cast<const u32x2*>(smem + wo[ct] + slot * DS_WINT);
-        const uint32_t g4 = so + uint32_t(gb >> a.gshift) * 4u;
+        const uint32_t gs = so + uint32_t(gb >> a.gshift) * 256u;
         float f[4][4];   // 2^-e * scale of column 16 ct + 4 q + r
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
+        for (int ct = 0; ct < 4; ++ct) {
+            const f32x4 sv = *reinterpret_cast<const f32x4*>(smem + gs + 64 * ct);
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                f[ct][r] = inv * *reinterpret_cast<const float*>(smem + g4 + uint32_t((16 * ct + r) * a.groups) * 4u);
+            for (int r = 0; r < 4; ++r) f[ct][r] = BF ? sv[r] : inv * sv[r];
+        }
         f32x4 tmp[4];
+        if constexpr (BF) {
+            // -136 * sum of the activations, then the biased codes on top.
+            const __bf16 n136 = __bf16(-136.0f);
+            const bf16x8 neg = {n136, n136, n136, n136, n136, n136, n136, n136};
+            f32x4 corr = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < SPH; ++kk) corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(neg, xa[kk][0], corr, 0, 0, 0);
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                f32x4 t0 = corr;
+#pragma unroll
+                for (int kk = 0; kk < SPH; ++kk)
+                    t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_to_bf16_off(wd[ct][kk]), xa[kk][0], t0, 0, 0, 0);
+                tmp[ct] = t0;
+            }
+        } else {
 #pragma unroll
         for (int kk = 0; kk < SPH; ++kk) {
 #pragma unroll
@@ -695,6 +772,7 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
                 for (int p = 0; p < P; ++p) t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, xa[kk][p], t0, 0, 0, 0);
                 tmp[ct] = t0;
             }
+        }
         }
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
@@ -719,11 +797,16 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
             // The activations need no other wave: convert them before the
             // barrier that hands over the weights.
             const bool live = 4 * t + wb < nblk;
-            f16x8 xa[SPH][P];
+            XF xa[SPH][P];
             float inv = 1.0f;
             if (live) convert_x(u, xa, inv);
-            __syncthreads();   // weight interval t is in LDS
+            wait_for(0, uint32_t(t + 1));   // weight interval t is in LDS
             if (live) weights(t, u, xa, inv);
+            // This wave's reads of slot u are issued: count them.
+            asm volatile("" ::: "memory");
+            if (lane == 0)
+                __hip_atomic_fetch_add(const_cast<lds_u32*>(cnt + 1 + u), 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
 
@@ -770,11 +853,10 @@ int launch_decode(dgm_gpu* g, const DecArgs& a) {
     return DGM_OK;
 }
 
-// The one-launch kernel's domain: M <= 16, the scales of 64 rows in 16 KB of
-// LDS as whole 16-byte pieces (groups a multiple of 4, at most 64), 32-bit X
-// offsets.
+// The one-launch kernel's domain: M <= 16, the scales of 64 rows in LDS (at
+// most 63 groups), 32-bit X offsets.
 bool small_ok(int M, int K, int groups) {
-    return M <= 16 && groups % 4 == 0 && groups <= DS_SMAX / 256 && int64_t(M) * K * 4 < (int64_t(1) << 32);
+    return M <= 16 && groups <= DS_SMAX / 256 && int64_t(M) * K * 4 < (int64_t(1) << 32);
 }
 
 template <int BITS, int P>
