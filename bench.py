@@ -204,12 +204,10 @@ def traffic_for(workload: str, kernel_keys) -> object:
     matched by substring), or None when the workload was not profiled."""
     ent = load_traffic().get(workload, {})
     total, found = 0, False
-    for key in kernel_keys:
-        for name, rec in ent.items():
-            if not name.startswith("_") and key in name:
-                total += rec.get("total_bytes", 0)
-                found = True
-                break
+    for name, rec in ent.items():   # every kernel of the call once
+        if name != "_calibration" and any(key in name for key in kernel_keys):
+            total += rec.get("total_bytes", 0)
+            found = True
     return total if found else None
 
 
@@ -307,7 +305,7 @@ def bench_c5(b: Bench, bits: int, steps: int, warmup: int, cpu: bool) -> dict:
     ev = r["event_ms"]
     med, mean = statistics.median(ev), sum(ev) / len(ev)
     nbytes = N * K // (2 if bits == 4 else 1) + N * (K // G) * 4 + 4 * (M * K + M * N)
-    kernels = [f"gemm_bf16_kernel<{bits}>"]
+    kernels = [f"gemm_bf16_kernel<{bits}>", "x_to_bf16_kernel"]   # the call's two launches
     roof = roofline(flops / mean / 1e9, PEAK["bf16_TFLOPs"], "TFLOP/s", "mfma",
                     traffic_for(f"c5_int{bits}", kernels))
     roof.update({"kernel": f"gemm_nt_i{bits}", "device_kernels": kernels, "avg_launch_us": round(mean * 1e3, 3),
@@ -732,7 +730,7 @@ def summarize(d: str, title: str) -> str:
     return "\n".join(out)
 
 
-def _counter_means(d: str, counter: str) -> dict:
+def _counter_values(d: str, counter: str) -> dict:
     cc = _find(d, "counter_collection.csv")
     if not cc:
         raise FileNotFoundError(f"no counter_collection.csv under {d}")
@@ -740,20 +738,25 @@ def _counter_means(d: str, counter: str) -> dict:
     for r in csv.DictReader(open(cc)):
         if r["Counter_Name"] == counter:
             agg.setdefault(_short(r["Kernel_Name"]), []).append(float(r["Counter_Value"]))
-    return {k: sum(v) / len(v) for k, v in agg.items()}
+    return agg
 
 
 def traffic(name: str, fetch_dir: str, write_dir: str) -> dict:
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) -> bytes per launch, scaled so
-    that the calibration copy reads and writes exactly CALIB_BYTES."""
-    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
-    write = _counter_means(write_dir, "WRITE_SIZE")
+    that the calibration copy reads and writes exactly CALIB_BYTES. The
+    calibration copy is the largest single dispatch of the copy kernel (the
+    workloads' own buffer copies use the same kernel); every other kernel is
+    averaged over its dispatches."""
+    fv = _counter_values(fetch_dir, "FETCH_SIZE")
+    wv = _counter_values(write_dir, "WRITE_SIZE")
+    fetch = {k: sum(v) / len(v) for k, v in fv.items()}
+    write = {k: sum(v) / len(v) for k, v in wv.items()}
     copy = [k for k in fetch if "copy" in k.lower() or "elementwise" in k.lower()]
     if not copy:
         raise RuntimeError("calibration copy kernel not found (run the PMC passes with --calib-copy)")
-    ck = max(copy, key=lambda k: fetch[k])
-    f_scale = CALIB_BYTES / (fetch[ck] * 1024.0)
-    w_scale = CALIB_BYTES / (write.get(ck, 0.0) * 1024.0) if write.get(ck) else 1.0
+    ck = max(copy, key=lambda k: max(fv[k]))
+    f_scale = CALIB_BYTES / (max(fv[ck]) * 1024.0)
+    w_scale = CALIB_BYTES / (max(wv[ck]) * 1024.0) if wv.get(ck) else 1.0
     rec = {"_calibration": {"kernel": ck, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}}
     for k in fetch:
         if k == ck or "copy" in k.lower() or "elementwise" in k.lower() or "fill" in k.lower():
