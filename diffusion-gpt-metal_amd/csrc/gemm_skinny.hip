@@ -16,14 +16,20 @@
 //    sign-extension work, so one 16-byte load of 32 nibbles becomes the B
 //    operands of two MFMAs (even k, odd k) with three bit ops per 8 weights.
 //    int8 codes are used as they are.
-//  * X is split exactly into int8 pieces against a per-row power-of-two scale
-//    2^-sigma chosen so that max|x| * 2^sigma lies in [32, 64):
-//        u = x * 2^sigma = c1 + c2 / 128 + c3 / 128^2 + r,  |r| <= 2^-15,
+//  * X is split exactly into int8 pieces against a power-of-two scale 2^-sigma
+//    (per row, or per wave k-range in the one-launch variant) chosen so that
+//    max|x| * 2^sigma lies in [32, 64):
+//        u = x * 2^sigma = c1 + c2 / 128 + c3 / 128^2 + c4 / 128^3 + r,
 //    each c in [-64, 64]. The MFMA products and the int32 group sums are exact;
-//    with three pieces the representation error is 2^-20 of the row maximum,
-//    below the fp32 GEMM's own rounding, so results meet the fp32 bar (max
-//    relative error 1e-5). Two pieces (error 2^-13 of the row maximum) form
-//    the reduced-precision mode (bar 1e-2).
+//    the representation error is what limits accuracy: 2^-20 of the range
+//    maximum with three pieces, 2^-27 with four. Relative to the output, the
+//    error is that fraction of max|x| times sum|w|, so an activation outlier
+//    (1e2 - 1e4 x the row's other values) costs three pieces up to ~3e-5 of
+//    max|y|: the fp32 mode therefore takes four pieces in the one-launch
+//    variant (M <= 4, where they fit one 16-row tile). Calls the library routes
+//    here in the fp32 mode are those M <= 3 (four pieces) and the shapes outside
+//    the f16 decode kernels' domain (gemm_decode.hip; three pieces). Two pieces
+//    (2^-13 of the range maximum) form the reduced-precision mode (bar 1e-2).
 //  * Pieces occupy MFMA rows: virtual row v = p * M + m, so M = 1 with three
 //    pieces uses 3 of 16 rows of a single tile; the wasted rows cost MFMA
 //    cycles only, which this HBM-bound shape has to spare.
