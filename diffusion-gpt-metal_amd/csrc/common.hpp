@@ -80,6 +80,29 @@ int64_t dit_train_scratch_floats(const dgm_dit_cfg* c);
 int dit_forward_train_fused(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
                             const float* sinv, float* x, const DitSaves* saves, float* scratch,
                             int64_t scratch_floats);
+// The three-launch loop body (dit_loop.hip): whether the config is one of its
+// built shapes (int8 / int4, group 32, C % 64 == 0, F % 128 == 0),
+// whether the weights also fit it (linears back to back, aligned), and the
+// floats of its wdown slabs ([F / 128][B*T][C]).
+bool dit_loop_shape_ok(const dgm_dit_cfg* c);
+bool dit_loop_ok(const dgm_dit_cfg* c, const dgm_dit_weights* w);
+int64_t dit_loop_part_floats(const dgm_dit_cfg* c);
+// Buffers of the loops: the wdown slabs and loop 0's v [B*T, D]; for the
+// inference run also (the training run keeps these in its saves) q [B*T, C],
+// k and v [B*T, D], two [B*T, C] buffers that alternate as mid, ln2
+// [B*T, C], and the last loop's probs (may be null).
+struct DitLoopBufs {
+    float* part;
+    float* vfirst;
+    float *q, *k, *v;
+    float* mid[2];
+    float* ln2;
+    float* probs_last;
+};
+// Runs the loops on x in place; saves (null for inference) as for
+// dit_forward_train_fused. Needs dit_loop_ok.
+int dit_forward_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
+                      const float* sinv, float* x, const DitLoopBufs& buf, const DitSaves* saves);
 // True when `next`'s weights (fp32 for bits 32, else codes and scales)
 // start where `first`'s `rows` x K end, so the two act as one [2 rows, K]
 // linear.

@@ -16,6 +16,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "dit_rows.hpp"
 
 namespace dgm {
 int gemm_check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits);
@@ -85,15 +86,7 @@ __global__ __launch_bounds__(kThreads) void repeat_heads_kernel(const float* __r
 }
 
 // ---- swiglu_fwd (metal/kernels.metal:911-930) ----------------------------------
-__device__ __forceinline__ float silu_sigmoid(float z) {
-#pragma clang fp contract(off)
-    if (z >= 0.0f) {
-        const float e = expf(-z);
-        return 1.0f / (1.0f + e);
-    }
-    const float e = expf(z);
-    return e / (1.0f + e);
-}
+using dgm_rows::silu_sigmoid;
 
 __global__ __launch_bounds__(kThreads) void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                           float* __restrict__ y, int64_t n) {
@@ -645,36 +638,9 @@ struct DitGemmArgs {
     float *lnout, *side1, *rs1, *rs2, *rs3, *gate_out, *up_out;
 };
 
-__device__ __forceinline__ float sum16(float v) {
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
-    return v;
-}
-
-template <int J>
-__device__ __forceinline__ float rstd16(const float4 (&v)[J], int cols, float eps) {
-#pragma clang fp contract(off)
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        ss += v[j].x * v[j].x;
-        ss += v[j].y * v[j].y;
-        ss += v[j].z * v[j].z;
-        ss += v[j].w * v[j].w;
-    }
-    ss = sum16(ss);
-    const float mean = ss / float(cols);
-    return 1.0f / sqrtf(mean + eps);
-}
-
-__device__ __forceinline__ float4 norm4(float4 v, float rs, float4 w) {
-#pragma clang fp contract(off)
-    return make_float4((v.x * rs) * w.x, (v.y * rs) * w.y, (v.z * rs) * w.z, (v.w * rs) * w.w);
-}
-
-__device__ __forceinline__ float4 add4(float4 a, float4 b) {
-    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
+using dgm_rows::add4;
+using dgm_rows::norm4;
+using dgm_rows::rstd16;
 
 template <int BITS, bool PAIR, int J>
 __global__ __launch_bounds__(kThreads) void dit_gemm_kernel(DitGemmArgs a, int tiles_i, int tiles_j, int per_xcd) {
@@ -1182,6 +1148,16 @@ int dgm_dit_forward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, 
     for (int i = 0; i < NBUF; ++i) {
         p[i] = cur;
         cur += (sz[i] + 63) & ~int64_t(63);
+    }
+    // Three launches per loop when the shape is built for it: the wdown
+    // slabs take the gu | sw pieces (contiguous), loop 0's v the qkv0 piece,
+    // q | k | v the qkv1 piece, and mid alternates between the mid and pre
+    // pieces.
+    if (dgm::dit_loop_ok(c, w) && dgm::dit_loop_part_floats(c) <= (p[SW] - p[GU]) + sz[SW]) {
+        const int64_t MC = int64_t(c->B) * c->T * c->C, MD = int64_t(c->B) * c->T * c->D;
+        const dgm::DitLoopBufs buf{p[GU], p[QKV0], p[QKV1], p[QKV1] + MC, p[QKV1] + MC + MD,
+                                   {p[MID], p[PRE]}, p[LN2], p[PROBS]};
+        return dgm::dit_forward_loops(g, c, w, cosv, sinv, x, buf, nullptr);
     }
     const int B = c->B, T = c->T, H = c->H, D = c->D, bits = c->bits, G = c->group;
     const int64_t M = int64_t(B) * T, C = c->C, F = c->F, KV = D, QKV = C + 2 * KV;

@@ -1,0 +1,862 @@
+// Looped DiT block forward in three launches per loop (src/DiT.swift:520-550),
+// for the block shapes it is built for: int8 / int4 linears with group 32,
+// one KV head, C a multiple of 64, F a multiple of 128.
+//
+//  * loop_row_kernel: one workgroup of 16 waves per (16 rows, column group);
+//    wave w owns row w. The row chain that closes the previous loop
+//    (mlp = the previous loop's wdown slabs added in slab order;
+//    pre = mid + rms(mlp)*n2b; x = rms(pre)*nf; loop 0: x = the input), then
+//    ln1 = rms(x)*n1, and the group's columns of the [wq; wk; wv] projection
+//    (HG query heads, or k | v), with RoPE on q and k and the value residual
+//    on v.
+//  * loop_attn_kernel: one workgroup of 16 waves per (sequence b, 16 query
+//    rows): scores, row softmax and P.V on fp32 MFMA (the stages of
+//    attn_mfma_kernel in dit.hip, every query head against the one KV head),
+//    the wo projection, then mid = x + rms(attn)*n1b and ln2 = rms(mid)*n2.
+//  * loop_mlp_kernel: one workgroup of 8 waves per (16 rows, slice of 128
+//    SwiGLU columns): gate and up of those columns, SwiGLU, and the slice's
+//    share of wdown (its sum over the slice's 128 contraction indices) into
+//    slab `slice` of [P][M][C].
+//  * loop_tail_kernel after the last loop: the closing row chain.
+// A sequence's workgroups run on one XCD (block b + 8 j), where the previous
+// launch left its rows.
+//
+// Projections run on v_mfma_f32_16x16x32_bf16 with exact operands: a code is
+// an integer of at most 8 bits (exact in bf16), and every activation is split
+// into three bf16 pieces hi + mid + lo whose sum is the fp32 value exactly
+// (hi: the top 8 significand bits, mid: the next 8 of the remainder, lo: what
+// is left, at most 8 bits). Every product is exact; each 32-k group's sum is
+// accumulated in fp32 (lo, mid, then hi pieces) and multiplied by the group's
+// scale. The row chains, RoPE, softmax and SwiGLU use the standalone kernels'
+// formulas, so results agree with the oracle to fp32 rounding of the sums.
+#include <algorithm>
+#include <cmath>
+
+#include "common.hpp"
+#include "dit_rows.hpp"
+
+namespace {
+
+using dgm_rows::add4;
+using dgm_rows::norm4;
+using dgm_rows::rstd16;
+using dgm_rows::silu_sigmoid;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSlice = 128;          // SwiGLU columns per mlp workgroup (8 waves x 16)
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// x = h + m + l exactly; each piece has a zero low half (a bf16 value).
+__device__ __forceinline__ void split3(float x, float& h, float& m, float& l) {
+    h = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
+    const float r = x - h;
+    m = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u);
+    l = r - m;
+}
+
+// Pieces of 4 consecutive values into planes P (hi), P + ps (mid), P + 2 ps
+// (lo) at element o (o % 4 == 0).
+__device__ __forceinline__ void put4(__bf16* P, int ps, int o, float4 v) {
+    float h[4], m[4], l[4];
+    split3(v.x, h[0], m[0], l[0]);
+    split3(v.y, h[1], m[1], l[1]);
+    split3(v.z, h[2], m[2], l[2]);
+    split3(v.w, h[3], m[3], l[3]);
+    *reinterpret_cast<uint2*>(P + o) = make_uint2(pk_bf16(h[0], h[1]), pk_bf16(h[2], h[3]));
+    *reinterpret_cast<uint2*>(P + ps + o) = make_uint2(pk_bf16(m[0], m[1]), pk_bf16(m[2], m[3]));
+    *reinterpret_cast<uint2*>(P + 2 * ps + o) = make_uint2(pk_bf16(l[0], l[1]), pk_bf16(l[2], l[3]));
+}
+
+__device__ __forceinline__ void put1(__bf16* P, int ps, int o, float v) {
+    float h, m, l;
+    split3(v, h, m, l);
+    uint16_t* Q = reinterpret_cast<uint16_t*>(P);
+    Q[o] = uint16_t(__float_as_uint(h) >> 16);
+    Q[ps + o] = uint16_t(__float_as_uint(m) >> 16);
+    Q[2 * ps + o] = uint16_t(__float_as_uint(l) >> 16);
+}
+
+// 8 consecutive codes k .. k+7 of weight row `row` ([rows, K] row-major):
+// int8 as 8 bytes, int4 as 8 nibbles (low nibble first) in .x.
+template <int BITS>
+__device__ __forceinline__ uint2 codes_at(const void* W, size_t row, int K, int k) {
+    if constexpr (BITS == 8) {
+        return *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(W) + row * size_t(K) + k);
+    } else {
+        const uint8_t* p = static_cast<const uint8_t*>(W) + ((row * size_t(K) + size_t(k)) >> 1);
+        return make_uint2(*reinterpret_cast<const uint32_t*>(p), 0u);
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ bf16x8 codes_bf16(uint2 w) {
+    u32x4 r;
+    if constexpr (BITS == 8) {
+        r.x = pk_bf16(float(int8_t(w.x)), float(int8_t(w.x >> 8)));
+        r.y = pk_bf16(float(int8_t(w.x >> 16)), float(int8_t(w.x >> 24)));
+        r.z = pk_bf16(float(int8_t(w.y)), float(int8_t(w.y >> 8)));
+        r.w = pk_bf16(float(int8_t(w.y >> 16)), float(int8_t(w.y >> 24)));
+    } else {
+        const uint32_t v = w.x;
+        auto nib = [v](int i) { return float(int32_t(v << (28 - 4 * i)) >> 28); };
+        r.x = pk_bf16(nib(0), nib(1));
+        r.y = pk_bf16(nib(2), nib(3));
+        r.z = pk_bf16(nib(4), nib(5));
+        r.w = pk_bf16(nib(6), nib(7));
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// One 32-k step of a 16x16 tile: sum over the three activation pieces of
+// pieces x codes. `a` is this lane's 8 k of the hi plane (row r16, k 8*q4);
+// the mid and lo planes follow at +ps and +2ps.
+__device__ __forceinline__ f32x4 step3(const __bf16* a, int ps, bf16x8 b) {
+    const bf16x8 lo = *reinterpret_cast<const bf16x8*>(a + 2 * ps);
+    const bf16x8 mi = *reinterpret_cast<const bf16x8*>(a + ps);
+    const bf16x8 hi = *reinterpret_cast<const bf16x8*>(a);
+    f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mi, b, t, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, t, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 scale_add(f32x4 acc, f32x4 t, float s) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(t[e], s, acc[e]);
+    return acc;
+}
+
+// 16x16 tile of A . B^T over n (n % 16 == 0) fp32 contraction indices, rows in
+// LDS: a at (row r16, 4*q4) of A, b at (row r16, 4*q4) of B. fp32 MFMA.
+__device__ __forceinline__ f32x4 dot_tile(const float* a, const float* b, int n) {
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int d0 = 0; d0 < n; d0 += 16) {
+        const float4 x = *reinterpret_cast<const float4*>(a + d0);
+        const float4 y = *reinterpret_cast<const float4*>(b + d0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, y.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, y.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, y.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, y.w, acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+// Cross-lane sums and maxima on DPP and permlane swaps (no LDS round trips).
+// Every lane of the reduced group gets the same bits: each step adds a value
+// and its partner's, and addition is commutative.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    v += dpp_f<0x141>(v);   // row_half_mirror: the other quad of the 8
+    v += dpp_f<0x140>(v);   // row_mirror: the other 8 of the 16
+    return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+
+__device__ __forceinline__ float wave64_sum(float v) {
+    v = row16_sum(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);   // rows 0 <-> 1, 2 <-> 3
+    v = __builtin_bit_cast(float, uint32_t(r16[0])) + __builtin_bit_cast(float, uint32_t(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);   // lanes 0-31 <-> 32-63
+    return __builtin_bit_cast(float, uint32_t(r32[0])) + __builtin_bit_cast(float, uint32_t(r32[1]));
+}
+
+// rstd of one row held by a whole wave, one float4 per lane (columns 4 lane ..
+// 4 lane + 3; lanes past the row's end hold zeros): 1 / sqrt(mean(x^2) + eps).
+__device__ __forceinline__ float rstd_row(float4 v, int cols, float eps) {
+#pragma clang fp contract(off)
+    float ss = v.x * v.x;
+    ss += v.y * v.y;
+    ss += v.z * v.z;
+    ss += v.w * v.w;
+    ss = wave64_sum(ss);
+    const float mean = ss / float(cols);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+// Barrier for LDS hand-over only: waits for this wave's LDS operations, not
+// for its outstanding global loads or stores (each value loaded from global
+// memory is waited for where it is used).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Sequence-major block order: block i runs on XCD i % 8; the blocks of
+// sequence b (items per_seq of them) take XCD b % 8. Returns false for the
+// padding blocks past the last sequence.
+__device__ __forceinline__ bool seq_block(int B, int per_seq, int& b, int& item) {
+    const int j = int(blockIdx.x >> 3);
+    b = int(blockIdx.x & 7) + 8 * (j / per_seq);
+    item = j % per_seq;
+    return b < B;
+}
+
+// The KS group scales of one weight row (KS consecutive floats, 8-byte
+// aligned when KS is even).
+template <int KS>
+__device__ __forceinline__ void load_scales(const float* p, float (&s)[KS]) {
+    if constexpr (KS % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < KS / 2; ++i) {
+            const float2 v = *reinterpret_cast<const float2*>(p + 2 * i);
+            s[2 * i] = v.x;
+            s[2 * i + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < KS; ++i) s[i] = p[i];
+    }
+}
+
+// ---- loop_row_kernel ------------------------------------------------------------------
+// One workgroup of 16 waves per (16 rows, column group); wave w owns row w
+// (64 lanes, columns lane + 64 u). Column groups: HG query heads each, then
+// one group of k | v.
+struct LoopRowArgs {
+    const float* x;          // loop 0: the input rows [M, C]
+    const float* part;       // later loops: the previous loop's wdown slabs [P][M][C]
+    const float* mid_prev;   // later loops: the previous loop's mid [M, C]
+    const float *n1, *n2b, *nf;
+    const void* Wqkv;        // [C + 2D, C] codes of wq, wk, wv back to back
+    const float* Sqkv;
+    const float *cosv, *sinv;   // [T, D]
+    float* vfirst;              // [M, D]: loop 0 stores its v, later loops mix it in
+    float* q;                   // [M, C] after RoPE
+    float *k, *v;               // rows of kv_ld floats: k after RoPE, v after the mix,
+    int kv_ld, krep;            // each written to krep heads (columns h*D)
+    float* xo;                  // this loop's x [M, C] (loop 0: a copy of the input), or null
+    // Optional training saves: ln1 and its rstd; the previous loop's mlp,
+    // pre and their rstd.
+    float *sln1, *sr1, *pmlp, *ppre, *pr2b, *prf;
+    int B, T, NG, HG;
+    float eps, ca, cb;
+    int first;
+};
+
+template <int BITS, int KS, int DT, int NP>
+__global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
+#pragma clang fp contract(off)
+    constexpr int C = 32 * KS, D = 16 * DT, C4 = C / 4, LDA = C + 8, OLD = 2 * D + 4;
+    static_assert(C4 <= 64, "one float4 of the row per lane");
+    __shared__ __align__(16) __bf16 Ap[3 * 16 * LDA];
+    __shared__ __align__(16) float os[16 * OLD];
+    int b, item;
+    if (!seq_block(a.B, (a.T / 16) * a.NG, b, item)) return;
+    const int g = item % a.NG;
+    const size_t row0 = size_t(b) * a.T + size_t(item / a.NG) * 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const bool kvg = g == a.NG - 1;
+    const int ntile = kvg ? 2 * DT : a.HG * DT;
+    const int nbase = kvg ? C : g * a.HG * D;   // first weight row (output column) of the group
+
+    // -- loads: this wave's row (lane l: columns 4l .. 4l+3), then its
+    // projection tile's codes and scales.
+    const size_t row = row0 + wave;
+    const bool act = lane < C4;
+    const int c0 = 4 * (act ? lane : C4 - 1);
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 y, mp, w2, w3;
+    if (a.first) {
+        y = ld4(a.x + row * C + c0);
+    } else {
+        float4 pp[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) pp[p] = ld4(a.part + (size_t(p) * a.B * a.T + row) * C + c0);
+        mp = ld4(a.mid_prev + row * C + c0);
+        w2 = ld4(a.n2b + c0);
+        w3 = ld4(a.nf + c0);
+        y = pp[0];
+#pragma unroll
+        for (int p = 1; p < NP; ++p) y = add4(y, pp[p]);   // slab order
+    }
+    const float4 w1 = ld4(a.n1 + c0);
+    uint2 wr[KS];
+    float wsc[KS];
+    if (wave < ntile) {
+        const size_t n = size_t(nbase + wave * 16 + r16);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) wr[s] = codes_at<BITS>(a.Wqkv, n, C, 32 * s + 8 * q4);
+        load_scales<KS>(a.Sqkv + n * KS, wsc);
+    }
+
+    // -- the row chain (group 0 stores the row outputs), ln1 pieces into LDS.
+    const bool saver = g == 0;
+    float rs;
+    if (!a.first) {
+        rs = rstd_row(act ? y : z4, C, a.eps);   // rms(mlp)
+        if (saver && act && a.pmlp) st4(a.pmlp + row * C + c0, y);
+        if (saver && a.pr2b && lane == 0) a.pr2b[row] = rs;
+        y = add4(mp, norm4(y, rs, w2));          // pre = mid + rms(mlp) * n2b
+        if (saver && act && a.ppre) st4(a.ppre + row * C + c0, y);
+        rs = rstd_row(act ? y : z4, C, a.eps);   // rms(pre)
+        if (saver && a.prf && lane == 0) a.prf[row] = rs;
+        y = norm4(y, rs, w3);                    // x = rms(pre) * nf
+    }
+    if (saver && act && a.xo) st4(a.xo + row * C + c0, y);
+    rs = rstd_row(act ? y : z4, C, a.eps);       // ln1 = rms(x) * n1
+    if (saver && a.sr1 && lane == 0) a.sr1[row] = rs;
+    const float4 ln = norm4(y, rs, w1);
+    if (saver && act && a.sln1) st4(a.sln1 + row * C + c0, ln);
+    if (act) put4(Ap, 16 * LDA, wave * LDA + c0, ln);
+    lds_barrier();
+
+    // -- the group's projection tiles (wave w: tile w).
+    if (wave < ntile) {
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            acc = scale_add(acc, step3(Ap + r16 * LDA + 32 * s + 8 * q4, 16 * LDA, codes_bf16<BITS>(wr[s])), wsc[s]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) os[(4 * q4 + e) * OLD + wave * 16 + r16] = acc[e];
+    }
+    lds_barrier();
+
+    // -- RoPE of q / k (rope_fwd's formula), the value residual, stores.
+    constexpr int half = D / 2;
+    const int t0 = int(row0 % size_t(a.T));   // token position of row 0
+    auto rope = [&](const float* src, int r, int d, float& ya, float& yb) {
+        const float xa = src[d], xb = src[d + half];
+        const int tok = t0 + r;
+        const float c1 = a.cosv[tok * D + d], c2 = a.cosv[tok * D + d + half];
+        const float s1 = a.sinv[tok * D + d], s2 = a.sinv[tok * D + d + half];
+        const float p1 = xa * c1, r1 = -xb * s1;   // d < D/2: rot = -x[d + D/2]
+        const float p2 = xb * c2, r2 = xa * s2;    // d >= D/2: rot = x[d - D/2]
+        ya = p1 + r1;
+        yb = p2 + r2;
+    };
+    if (!kvg) {
+        const int np = 16 * a.HG * half;
+        for (int e = threadIdx.x; e < np; e += 1024) {
+            const int r = e / (a.HG * half), rem = e - r * (a.HG * half), hh = rem / half, d = rem - hh * half;
+            float ya, yb;
+            rope(os + r * OLD + hh * D, r, d, ya, yb);
+            float* o = a.q + (row0 + r) * C + nbase + hh * D;
+            o[d] = ya;
+            o[d + half] = yb;
+        }
+    } else {
+        for (int e = threadIdx.x; e < 16 * half; e += 1024) {
+            const int r = e / half, d = e - r * half;
+            float ya, yb;
+            rope(os + r * OLD, r, d, ya, yb);
+            float* o = a.k + (row0 + r) * a.kv_ld;
+            for (int h = 0; h < a.krep; ++h) {
+                o[h * D + d] = ya;
+                o[h * D + d + half] = yb;
+            }
+        }
+        for (int e = threadIdx.x; e < 16 * D; e += 1024) {
+            const int r = e / D, d = e - r * D;
+            float vv = os[r * OLD + D + d];
+            float* f = a.vfirst + (row0 + r) * D + d;
+            if (a.first) {
+                *f = vv;
+            } else {
+                const float pa = a.ca * vv;
+                const float pb = a.cb * *f;
+                vv = pa + pb;
+            }
+            float* o = a.v + (row0 + r) * a.kv_ld;
+            for (int h = 0; h < a.krep; ++h) o[h * D + d] = vv;
+        }
+    }
+}
+
+// ---- loop_attn_kernel -----------------------------------------------------------------
+// One workgroup of 16 waves per (sequence b, 16 query rows).
+struct LoopAttnArgs {
+    const float* q;          // [M, C] after RoPE
+    const float *k, *v;      // rows of kv_ld floats, the KV head at column 0
+    int kv_ld;
+    const float* x;          // this loop's x [M, C] (the residual)
+    const float *n1b, *n2;
+    const void* Wo;          // [C, C]
+    const float* So;
+    float *mid, *ln2;        // outputs [M, C]
+    float* probs;            // optional [B, H, T, T]
+    float *sav, *sattn, *sr1b, *sr2;   // optional training saves
+    int B;
+    float eps, scale;
+};
+
+template <int KS, int TT, int DT>
+struct AttnShape {
+    static constexpr int C = 32 * KS, D = 16 * DT, H = C / D, T = 16 * TT;
+    static constexpr int LDA = C + 8, QLD = C + 4, KLD = D + 4, VLD = T + 4;
+    static constexpr int QS = 0, XS = QS + 16 * QLD * 4, KO = XS + 16 * QLD * 4, VT = KO + T * KLD * 4;
+    static constexpr int PS = VT + D * VLD * 4, AV = PS + H * 16 * VLD * 4, AT = AV + 3 * 16 * LDA * 2;
+    static constexpr int NRM = AT + 16 * QLD * 4, BYTES = NRM + 2 * C * 4;
+    static constexpr int WPW = (2 * KS + 15) / 16;   // wo column tiles per wave
+    static_assert(KS % 2 == 0 && C % D == 0 && TT >= 1 && C / 4 <= 64, "loop_attn shape");
+    static_assert(BYTES <= 160 * 1024, "loop_attn LDS");
+};
+
+template <int BITS, int KS, int TT, int DT>
+__global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
+#pragma clang fp contract(off)
+    using S = AttnShape<KS, TT, DT>;
+    constexpr int C = S::C, D = S::D, H = S::H, T = S::T;
+    constexpr int LDA = S::LDA, QLD = S::QLD, KLD = S::KLD, VLD = S::VLD;
+    extern __shared__ __align__(16) unsigned char lds[];
+    float* qs = reinterpret_cast<float*>(lds + S::QS);
+    float* xs = reinterpret_cast<float*>(lds + S::XS);
+    float* ks = reinterpret_cast<float*>(lds + S::KO);
+    float* vt = reinterpret_cast<float*>(lds + S::VT);
+    float* ps = reinterpret_cast<float*>(lds + S::PS);
+    __bf16* Av = reinterpret_cast<__bf16*>(lds + S::AV);
+    float* at = reinterpret_cast<float*>(lds + S::AT);
+    float* nrm = reinterpret_cast<float*>(lds + S::NRM);   // n1b | n2
+    int b, qt;
+    if (!seq_block(a.B, TT, b, qt)) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const size_t seq0 = size_t(b) * T, own0 = seq0 + size_t(qt) * 16;
+
+    // -- wo codes of this wave's column tiles, then q, x (16 rows), k, v (T
+    // rows) and the norms, all issued before any is used.
+    uint2 wo[S::WPW][KS];
+    float wos[S::WPW][KS];
+#pragma unroll
+    for (int i = 0; i < S::WPW; ++i) {
+        const int ct = wave + 16 * i;
+        if (ct < 2 * KS) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s) wo[i][s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, 32 * s + 8 * q4);
+            load_scales<KS>(a.So + size_t(ct * 16 + r16) * KS, wos[i]);
+        }
+    }
+    constexpr int QC = 16 * C / 4, KC = T * D / 4, NC = 2 * C / 4;   // float4 chunks
+    constexpr int RQ = (QC + 1023) / 1024, RK = (KC + 1023) / 1024;
+    float4 qv[RQ], xv[RQ], kv[RK], vv[RK], nv;
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+        const int e = min(tid + 1024 * i, QC - 1), r = e / (C / 4), c4 = e - r * (C / 4);
+        qv[i] = ld4(a.q + (own0 + r) * C + 4 * c4);
+        xv[i] = ld4(a.x + (own0 + r) * C + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < RK; ++i) {
+        const int e = min(tid + 1024 * i, KC - 1), t = e / (D / 4), c4 = e - t * (D / 4);
+        kv[i] = ld4(a.k + (seq0 + t) * a.kv_ld + 4 * c4);
+        vv[i] = ld4(a.v + (seq0 + t) * a.kv_ld + 4 * c4);
+    }
+    if (tid < NC) nv = ld4((tid < C / 4 ? a.n1b : a.n2) + 4 * (tid % (C / 4)));
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+        const int e = tid + 1024 * i, r = e / (C / 4), c4 = e - r * (C / 4);
+        if (e < QC) {
+            st4(qs + r * QLD + 4 * c4, qv[i]);
+            st4(xs + r * QLD + 4 * c4, xv[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RK; ++i) {
+        const int e = tid + 1024 * i, t = e / (D / 4), c4 = e - t * (D / 4);
+        if (e < KC) {
+            st4(ks + t * KLD + 4 * c4, kv[i]);
+            vt[(4 * c4 + 0) * VLD + t] = vv[i].x;
+            vt[(4 * c4 + 1) * VLD + t] = vv[i].y;
+            vt[(4 * c4 + 2) * VLD + t] = vv[i].z;
+            vt[(4 * c4 + 3) * VLD + t] = vv[i].w;
+        }
+    }
+    if (tid < NC) st4(nrm + 4 * tid, nv);
+    lds_barrier();
+
+    // -- scores = (q . k) * scale per (head, 16 keys).
+    for (int tile = wave; tile < H * TT; tile += 16) {
+        const int h = tile / TT, kt = tile - h * TT;
+        const f32x4 acc = dot_tile(qs + r16 * QLD + h * D + 4 * q4, ks + (kt * 16 + r16) * KLD + 4 * q4, D);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ps[(h * 16 + 4 * q4 + e) * VLD + kt * 16 + r16] = acc[e] * a.scale;
+    }
+    lds_barrier();
+
+    // -- row softmax, 16 lanes per (head, query row): attn_softmax's max, sum
+    // of exp and normalize (each exp computed once).
+    for (int rr = 4 * wave + q4; rr < H * 16; rr += 64) {
+        float* rp = ps + rr * VLD;
+        float ev[TT];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+            ev[i] = rp[r16 + 16 * i];
+            mx = fmaxf(mx, ev[i]);
+        }
+        mx = row16_max(mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+            ev[i] = expf(ev[i] - mx);
+            sum += ev[i];
+        }
+        sum = row16_sum(sum);
+        const float inv = 1.0f / sum;
+        float* po = a.probs ? a.probs + ((size_t(b) * H + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T : nullptr;
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+            const float pv = ev[i] * inv;
+            rp[r16 + 16 * i] = pv;
+            if (po) po[r16 + 16 * i] = pv;
+        }
+    }
+    lds_barrier();
+
+    // -- av = P.V per (head, 16 columns), kept as bf16 pieces for wo.
+    for (int tile = wave; tile < H * DT; tile += 16) {
+        const int h = tile / DT, dt = tile - h * DT;
+        const f32x4 acc = dot_tile(ps + (h * 16 + r16) * VLD + 4 * q4, vt + (dt * 16 + r16) * VLD + 4 * q4, T);
+        const int col = h * D + dt * 16 + r16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * q4 + e;
+            if (a.sav) a.sav[(own0 + r) * C + col] = acc[e];
+            put1(Av, 16 * LDA, r * LDA + col, acc[e]);
+        }
+    }
+    lds_barrier();
+
+    // -- attn = av . wo^T.
+#pragma unroll
+    for (int i = 0; i < S::WPW; ++i) {
+        const int ct = wave + 16 * i;
+        if (ct >= 2 * KS) break;
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            acc = scale_add(acc, step3(Av + r16 * LDA + 32 * s + 8 * q4, 16 * LDA, codes_bf16<BITS>(wo[i][s])),
+                            wos[i][s]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * q4 + e;
+            at[r * QLD + ct * 16 + r16] = acc[e];
+            if (a.sattn) a.sattn[(own0 + r) * C + ct * 16 + r16] = acc[e];
+        }
+    }
+    lds_barrier();
+
+    // -- mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2 (wave w: row w; lane l:
+    // columns 4l .. 4l+3).
+    {
+        const int r = wave;
+        const bool act = lane < C / 4;
+        const int c0 = 4 * (act ? lane : C / 4 - 1);
+        const size_t o = (own0 + r) * C + c0;
+        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 y = ld4(at + r * QLD + c0);
+        float rs = rstd_row(act ? y : z4, C, a.eps);
+        if (lane == 0 && a.sr1b) a.sr1b[own0 + r] = rs;
+        y = add4(ld4(xs + r * QLD + c0), norm4(y, rs, ld4(nrm + c0)));
+        if (act) st4(a.mid + o, y);
+        rs = rstd_row(act ? y : z4, C, a.eps);
+        if (lane == 0 && a.sr2) a.sr2[own0 + r] = rs;
+        if (act) st4(a.ln2 + o, norm4(y, rs, ld4(nrm + C + c0)));
+    }
+}
+
+// ---- loop_mlp_kernel ------------------------------------------------------------------
+// One workgroup of 8 waves per (16 rows, slice of kSlice SwiGLU columns).
+struct LoopMlpArgs {
+    const float* ln2;        // [M, C]
+    const void* Wgu;         // [2F, C] codes of wgate, wup back to back
+    const float* Sgu;
+    const void* Wd;          // [C, F]
+    const float* Sd;
+    float* part;             // [P][M][C]
+    float *sgate, *sup, *ssw;   // optional saves [M, F]
+    int B, TT, M, F, P;
+};
+
+template <int BITS, int KS>
+__global__ __launch_bounds__(512) void loop_mlp_kernel(LoopMlpArgs a) {
+#pragma clang fp contract(off)
+    constexpr int C = 32 * KS, J = C / 64, LDA = C + 8, LDW = kSlice + 8, FKS = kSlice / 32;
+    constexpr int DPW = (2 * KS + 7) / 8;   // wdown column tiles per wave
+    __shared__ __align__(16) __bf16 Ah[3 * 16 * LDA];
+    __shared__ __align__(16) __bf16 Sw[3 * 16 * LDW];
+    int b, item;
+    if (!seq_block(a.B, a.TT * a.P, b, item)) return;
+    const int slice = item % a.P;
+    const size_t row0 = (size_t(b) * a.TT + item / a.P) * 16;
+    const int f0 = slice * kSlice;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+
+    // ln2 rows, then the codes: gate / up column tile `wave`, wdown column
+    // tiles wave, wave + 8, ...
+    float4 xv[J];
+    if (wave < 4) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) xv[j] = ld4(a.ln2 + (row0 + 4 * wave + q4) * C + 4 * (r16 + 16 * j));
+    }
+    const size_t n = size_t(f0 + wave * 16 + r16);
+    uint2 gw[KS], uw[KS];
+    float gs[KS], us[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        gw[s] = codes_at<BITS>(a.Wgu, n, C, 32 * s + 8 * q4);
+        uw[s] = codes_at<BITS>(a.Wgu, size_t(a.F) + n, C, 32 * s + 8 * q4);
+    }
+    load_scales<KS>(a.Sgu + n * KS, gs);
+    load_scales<KS>(a.Sgu + (size_t(a.F) + n) * KS, us);
+    const int fgroups = a.F / 32;
+    uint2 dw[DPW][FKS];
+    float dsc[DPW][FKS];
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        const int ct = wave + 8 * i;
+        if (ct < 2 * KS) {
+#pragma unroll
+            for (int s = 0; s < FKS; ++s) dw[i][s] = codes_at<BITS>(a.Wd, size_t(ct * 16 + r16), a.F, f0 + 32 * s + 8 * q4);
+            load_scales<FKS>(a.Sd + size_t(ct * 16 + r16) * fgroups + f0 / 32, dsc[i]);
+        }
+    }
+    if (wave < 4) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) put4(Ah, 16 * LDA, (4 * wave + q4) * LDA + 4 * (r16 + 16 * j), xv[j]);
+    }
+    lds_barrier();
+
+    // gate and up of this wave's 16 columns, SwiGLU (swiglu_fwd's formula).
+    f32x4 ag = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, au = ag;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const __bf16* ap = Ah + r16 * LDA + 32 * s + 8 * q4;
+        ag = scale_add(ag, step3(ap, 16 * LDA, codes_bf16<BITS>(gw[s])), gs[s]);
+        au = scale_add(au, step3(ap, 16 * LDA, codes_bf16<BITS>(uw[s])), us[s]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int r = 4 * q4 + e;
+        const float z = ag[e];
+        const float act = z * silu_sigmoid(z);
+        const float sw = act * au[e];
+        if (a.sgate) {
+            const size_t o = (row0 + r) * a.F + f0 + wave * 16 + r16;
+            a.sgate[o] = z;
+            a.sup[o] = au[e];
+            a.ssw[o] = sw;
+        }
+        put1(Sw, 16 * LDW, r * LDW + wave * 16 + r16, sw);
+    }
+    lds_barrier();
+
+    // The slice's share of wdown: sw[:, f0 : f0 + kSlice] . wdown[:, f0 : f0 + kSlice]^T.
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        const int ct = wave + 8 * i;
+        if (ct >= 2 * KS) break;
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < FKS; ++s)
+            acc = scale_add(acc, step3(Sw + r16 * LDW + 32 * s + 8 * q4, 16 * LDW, codes_bf16<BITS>(dw[i][s])),
+                            dsc[i][s]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            a.part[(size_t(slice) * a.M + row0 + 4 * q4 + e) * C + ct * 16 + r16] = acc[e];
+    }
+}
+
+// ---- loop_tail_kernel: the row chain after the last loop ------------------------------
+// mlp = the slabs in slab order; pre = mid + rms(mlp)*n2b; x = rms(pre)*nf.
+// One row per wave (lane l: columns 4l .. 4l+3), 4 rows per workgroup.
+struct LoopTailArgs {
+    const float* part;
+    const float* mid;
+    const float *n2b, *nf;
+    float* x;
+    float *pmlp, *ppre, *pr2b, *prf;   // optional saves of the last loop
+    int M;
+    float eps;
+};
+
+template <int C, int NP>
+__global__ __launch_bounds__(256) void loop_tail_kernel(LoopTailArgs a) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const size_t row = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= size_t(a.M)) return;
+    const bool act = lane < C / 4;
+    const int c0 = 4 * (act ? lane : C / 4 - 1);
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 pp[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) pp[p] = ld4(a.part + (size_t(p) * a.M + row) * C + c0);
+    const float4 m = ld4(a.mid + row * C + c0), w2 = ld4(a.n2b + c0), w3 = ld4(a.nf + c0);
+    float4 y = pp[0];
+#pragma unroll
+    for (int p = 1; p < NP; ++p) y = add4(y, pp[p]);   // slab order
+    if (act && a.pmlp) st4(a.pmlp + row * C + c0, y);
+    float rs = rstd_row(act ? y : z4, C, a.eps);
+    if (a.pr2b && lane == 0) a.pr2b[row] = rs;
+    y = add4(m, norm4(y, rs, w2));
+    if (act && a.ppre) st4(a.ppre + row * C + c0, y);
+    rs = rstd_row(act ? y : z4, C, a.eps);
+    if (a.prf && lane == 0) a.prf[row] = rs;
+    if (act) st4(a.x + row * C + c0, norm4(y, rs, w3));
+}
+
+// ---- host side -------------------------------------------------------------------------
+template <int BITS, int KS, int TT, int DT, int NP>
+int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv, const float* sinv,
+              float* x, const dgm::DitLoopBufs& buf, const dgm::DitSaves* sv) {
+    using S = AttnShape<KS, TT, DT>;
+    const int B = c->B, L = c->loops, T = S::T, H = S::H, D = S::D, C = S::C;
+    const int M = B * T;
+    const int gb = 8 * ((B + 7) / 8);   // blocks of sequence b run on XCD b % 8
+    const int HG = H % 2 == 0 ? 2 : 1, NG = H / HG + 1;
+    auto attn_k = loop_attn_kernel<BITS, KS, TT, DT>;
+    if (S::BYTES > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_k),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES);
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "dit_forward: cannot reserve %d bytes of LDS: %s", S::BYTES,
+                             hipGetErrorString(e));
+    }
+    // mid alternates between two buffers (a loop reads the previous loop's
+    // mid while writing its own), or is saved per loop; q / k / v are the
+    // training saves ([M, C], k and v repeated to every head) or the
+    // inference buffers (k, v as [M, D]).
+    auto mid_of = [&](int l) { return sv ? sv[l].mid : buf.mid[l & 1]; };
+    auto ln2_of = [&](int l) { return sv ? sv[l].ln2 : buf.ln2; };
+    for (int l = 0; l < L; ++l) {
+        float* q = sv ? sv[l].q : buf.q;
+        float* k = sv ? sv[l].k : buf.k;
+        float* v = sv ? sv[l].v : buf.v;
+        const int kv_ld = sv ? C : D;
+        float* xl = sv ? sv[l].x : x;   // this loop's x, the residual of its attention half
+
+        LoopRowArgs ra{};
+        ra.first = l == 0;
+        ra.x = x;
+        ra.part = buf.part;
+        ra.mid_prev = l > 0 ? mid_of(l - 1) : nullptr;
+        ra.n1 = w->n1; ra.n2b = w->n2b; ra.nf = w->nf;
+        ra.Wqkv = w->wq.q; ra.Sqkv = w->wq.scale;
+        ra.cosv = cosv; ra.sinv = sinv;
+        ra.vfirst = buf.vfirst;
+        ra.q = q; ra.k = k; ra.v = v; ra.kv_ld = kv_ld; ra.krep = sv ? H : 1;
+        ra.xo = (sv || l > 0) ? xl : nullptr;
+        if (sv) {
+            ra.sln1 = sv[l].ln1; ra.sr1 = sv[l].r1;
+            if (l > 0) { ra.pmlp = sv[l - 1].mlp; ra.ppre = sv[l - 1].pre; ra.pr2b = sv[l - 1].r2b; ra.prf = sv[l - 1].rf; }
+        }
+        ra.B = B; ra.T = T; ra.NG = NG; ra.HG = HG;
+        ra.eps = c->eps; ra.ca = 1.0f - c->mix; ra.cb = c->mix;
+        hipLaunchKernelGGL((loop_row_kernel<BITS, KS, DT, NP>), dim3(unsigned(gb * TT * NG)), dim3(1024), 0,
+                           g->stream, ra);
+        DGM_LAUNCH_CHECK(g, "dit_forward loop_row");
+
+        LoopAttnArgs aa{};
+        aa.q = q; aa.k = k; aa.v = v; aa.kv_ld = kv_ld;
+        aa.x = xl;
+        aa.n1b = w->n1b; aa.n2 = w->n2;
+        aa.Wo = w->wo.q; aa.So = w->wo.scale;
+        aa.mid = mid_of(l); aa.ln2 = ln2_of(l);
+        aa.probs = sv ? sv[l].probs : (l == L - 1 ? buf.probs_last : nullptr);
+        if (sv) { aa.sav = sv[l].av; aa.sattn = sv[l].attn; aa.sr1b = sv[l].r1b; aa.sr2 = sv[l].r2; }
+        aa.B = B; aa.eps = c->eps; aa.scale = 1.0f / sqrtf(float(D));
+        hipLaunchKernelGGL(attn_k, dim3(unsigned(gb * TT)), dim3(1024), size_t(S::BYTES), g->stream, aa);
+        DGM_LAUNCH_CHECK(g, "dit_forward loop_attn");
+
+        LoopMlpArgs ma{};
+        ma.ln2 = ln2_of(l);
+        ma.Wgu = w->wgate.q; ma.Sgu = w->wgate.scale;
+        ma.Wd = w->wdown.q; ma.Sd = w->wdown.scale;
+        ma.part = buf.part;
+        if (sv) { ma.sgate = sv[l].gate; ma.sup = sv[l].up; ma.ssw = sv[l].sw; }
+        ma.B = B; ma.TT = TT; ma.M = M; ma.F = c->F; ma.P = NP;
+        hipLaunchKernelGGL((loop_mlp_kernel<BITS, KS>), dim3(unsigned(gb * TT * NP)), dim3(512), 0, g->stream, ma);
+        DGM_LAUNCH_CHECK(g, "dit_forward loop_mlp");
+    }
+    if (L > 0) {
+        LoopTailArgs ta{};
+        ta.part = buf.part;
+        ta.mid = mid_of(L - 1);
+        ta.n2b = w->n2b; ta.nf = w->nf;
+        ta.x = x;
+        if (sv) { ta.pmlp = sv[L - 1].mlp; ta.ppre = sv[L - 1].pre; ta.pr2b = sv[L - 1].r2b; ta.prf = sv[L - 1].rf; }
+        ta.M = M;
+        ta.eps = c->eps;
+        hipLaunchKernelGGL((loop_tail_kernel<32 * KS, NP>), dim3(unsigned((M + 3) / 4)), dim3(256), 0, g->stream, ta);
+        DGM_LAUNCH_CHECK(g, "dit_forward loop_tail");
+    }
+    return DGM_OK;
+}
+
+// The built shapes: (C / 32, T / 16, D / 16, F / kSlice).
+template <int BITS>
+int dispatch(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv, const float* sinv,
+             float* x, const dgm::DitLoopBufs& buf, const dgm::DitSaves* sv) {
+    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16, np = c->F / kSlice;
+    if (ks == 6 && tt == 4 && dt == 3 && np == 6) return run_loops<BITS, 6, 4, 3, 6>(g, c, w, cosv, sinv, x, buf, sv);
+    if (ks == 2 && tt == 1 && dt == 1 && np == 1) return run_loops<BITS, 2, 1, 1, 1>(g, c, w, cosv, sinv, x, buf, sv);
+    return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: no loop kernels built for this shape");
+}
+
+bool shape_built(const dgm_dit_cfg* c) {
+    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16, np = c->F / kSlice;
+    return (ks == 6 && tt == 4 && dt == 3 && np == 6) || (ks == 2 && tt == 1 && dt == 1 && np == 1);
+}
+
+}  // namespace
+
+namespace dgm {
+
+bool dit_loop_shape_ok(const dgm_dit_cfg* c) {
+    if (!c || (c->bits != 8 && c->bits != 4) || c->group != 32 || c->loops < 0 || c->B <= 0) return false;
+    if (c->C % 64 != 0 || c->D % 16 != 0 || c->H * c->D != c->C || c->T % 16 != 0) return false;
+    if (c->F % kSlice != 0 || c->F <= 0) return false;
+    return shape_built(c);
+}
+
+int64_t dit_loop_part_floats(const dgm_dit_cfg* c) {
+    if (!dit_loop_shape_ok(c)) return 0;
+    return int64_t(c->F / kSlice) * c->B * c->T * c->C;
+}
+
+bool dit_loop_ok(const dgm_dit_cfg* c, const dgm_dit_weights* w) {
+    if (!dit_loop_shape_ok(c)) return false;
+    const int64_t C = c->C, F = c->F, KV = c->D;
+    if (!dit_linear_follows(w->wq, w->wk, C, C, c->bits, c->group) ||
+        !dit_linear_follows(w->wk, w->wv, KV, C, c->bits, c->group) ||
+        !dit_linear_follows(w->wgate, w->wup, F, C, c->bits, c->group))
+        return false;
+    const size_t al = c->bits == 8 ? 8 : 4;
+    return aligned(w->wq.q, al) && aligned(w->wo.q, al) && aligned(w->wgate.q, al) && aligned(w->wdown.q, al) &&
+           aligned(w->wq.scale, 8) && aligned(w->wo.scale, 8) && aligned(w->wgate.scale, 8) &&
+           aligned(w->wdown.scale, 8) && aligned(w->n1, 16) && aligned(w->n1b, 16) && aligned(w->n2, 16) &&
+           aligned(w->n2b, 16) && aligned(w->nf, 16);
+}
+
+int dit_forward_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv,
+                      const float* sinv, float* x, const DitLoopBufs& buf, const DitSaves* saves) {
+    return c->bits == 8 ? dispatch<8>(g, c, w, cosv, sinv, x, buf, saves)
+                        : dispatch<4>(g, c, w, cosv, sinv, x, buf, saves);
+}
+
+}  // namespace dgm

@@ -876,7 +876,8 @@ int check_bthd(dgm_gpu* g, const char* name, int64_t B, int64_t T, int64_t H, in
 // then the forward's shared scratch.
 enum { A_X, A_LN1, A_R1, A_Q, A_K, A_V, A_PROBS, A_AV, A_ATTN, A_R1B, A_MID, A_LN2, A_R2, A_GATE, A_UP, A_SW,
        A_MLP, A_R2B, A_PRE, A_RF, A_COUNT };
-enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_COUNT };
+// F_PART: the three-launch loop's wdown slabs (empty when the shape is not built for it).
+enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_PART, F_COUNT };
 // Backward scratch.
 // B_DG, B_DU back to back hold [M, 2F] rows [dgate | dup] and B_QPRE, B_KPRE,
 // B_DVPRE [M, C + 2 KV] rows [dq | dk | dv] when the linears are fused.
@@ -893,7 +894,8 @@ void act_sizes(const dgm_dit_cfg* c, int64_t* a, int64_t* f) {
     const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
     const int64_t av[A_COUNT] = {M * C, M * C, M, M * C, M * C, M * C, att, M * C, M * C, M,
                                  M * C, M * C, M, M * F, M * F, M * F, M * C, M, M * C, M};
-    const int64_t fv[F_COUNT] = {M * C, M * KV, M * KV, M * KV, M * KV, M * KV, att, M * C};
+    const int64_t fv[F_COUNT] = {M * C, M * KV, M * KV, M * KV, M * KV, M * KV, att, M * C,
+                                 dgm::dit_loop_part_floats(c)};
     for (int i = 0; i < A_COUNT; ++i) a[i] = pad64(av[i]);
     for (int i = 0; i < F_COUNT; ++i) f[i] = pad64(fv[i]);
 }
@@ -1068,8 +1070,18 @@ int dgm_dit_forward_train(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weight
                                   A(l, A_MID), A(l, A_LN2), A(l, A_R2),   A(l, A_GATE), A(l, A_UP),
                                   A(l, A_SW),  A(l, A_MLP), A(l, A_R2B),  A(l, A_PRE), A(l, A_RF)};
         }
+        // Three launches per loop when the shape is built for it.
+        bool loop2 = dgm::dit_loop_ok(c, w) && dgm::aligned(x, 16);
+        for (int l = 0; loop2 && l < L; ++l)
+            for (const float* p : {sv[l].x, sv[l].ln1, sv[l].mlp, sv[l].pre})
+                if (!dgm::aligned(p, 16)) loop2 = false;
+        if (loop2) {
+            const dgm::DitLoopBufs buf{S[F_PART], S[F_VFIRST], nullptr, nullptr, nullptr, {nullptr, nullptr}, nullptr,
+                                       nullptr};
+            return dgm::dit_forward_loops(g, c, w, cosv, sinv, x, buf, sv);
+        }
         int64_t fn = 0;
-        for (int i = 0; i < F_COUNT; ++i) fn += fsz[i];
+        for (int i = 0; i < F_PART; ++i) fn += fsz[i];
         const int r = dgm::dit_forward_train_fused(g, c, w, cosv, sinv, x, sv, S[0], fn);
         if (r != dgm::kNotFused) return r;
     }

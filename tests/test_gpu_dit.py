@@ -190,6 +190,17 @@ def test_config3_dit_block_forward(gpu, dgm, orc):
     assert np.allclose(probs.sum(-1), 1.0, atol=1e-5)
 
 
+@pytest.mark.parametrize("B,loops,bits", [(8, 4, 4), (3, 2, 8), (11, 1, 8), (1, 3, 4)])
+def test_dit_block_c3_shape_variants(gpu, dgm, orc, B, loops, bits):
+    """The c3 block shape (T 64, embd 192, 4 heads of 48, SwiGLU 768, group
+    32) at other batch sizes (sequences per XCD: none, one or two), loop
+    counts and int4 linears."""
+    cfg = dgm.DiTConfig(B=B, loops=loops, bits=bits)
+    w = _dit_weights(orc, cfg, seed=31 + B)
+    x0 = orc.RNG(1000 + B).randn(cfg.B * cfg.T * cfg.C, 1.0)
+    _check_block(gpu, dgm, orc, cfg, w, x0, 1e-5)
+
+
 @pytest.mark.parametrize("bits,group", [(4, 32), (32, 32)])
 def test_dit_block_other_widths(gpu, dgm, orc, bits, group):
     cfg = dgm.DiTConfig(B=2, T=16, C=64, F=128, H=4, D=16, loops=3, group=group, bits=bits)

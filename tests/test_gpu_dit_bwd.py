@@ -140,7 +140,7 @@ def test_c3_block_backward(gpu, dgm, orc):
     _check_block(blk, dgm, xg, gg, xo, gx, gw, gn)
 
 
-@pytest.mark.parametrize("bits,group", [(32, 8), (8, 16), (4, 16)])
+@pytest.mark.parametrize("bits,group", [(32, 8), (8, 16), (4, 16), (8, 32), (4, 32)])
 def test_small_block_backward(gpu, dgm, orc, bits, group):
     cfg = dgm.DiTConfig(B=2, T=16, C=64, F=128, H=4, D=16, loops=3, group=group, bits=bits)
     blk, xg, gg, xo, gx, gw, gn, _ = _run_block(gpu, dgm, orc, cfg, 900 + bits)
