@@ -720,6 +720,252 @@ __global__ __launch_bounds__(256) void loop_tail_kernel(LoopTailArgs a) {
     if (act) st4(a.x + row * C + c0, norm4(y, rs, w3));
 }
 
+// ---- loop_attn_bwd_kernel: the attention backward of one loop --------------------------
+// The reference's attention backward (metal/kernels.metal:508-612) followed by
+// the DiT's sum_heads of dk and dv, rope_bwd of dq and dk and the value
+// residual (src/DiT.swift:600-620), one launch. Per sequence b, 2 TT
+// workgroups of 16 waves: the query side (item < TT) owns query rows
+// 16 item .. and produces dq; the key side owns key rows and produces dk and
+// dv of the single KV head (summed over the query heads). Both form
+// dS = P * (dP - D) with D[h][t] = dO_h[t] . O_h[t], the row sum of dP * P
+// (sum_s P[t][s] dO[t].V[s] = dO[t].O[t]), from the attention output O. The
+// products run on fp32 MFMA.
+struct LoopAttnBwdArgs {
+    const float* q;          // [M, C] after RoPE
+    const float *k, *v;      // [M, C] repeated to every head: the KV head is columns 0 .. D-1
+    const float* probs;      // [B, H, T, T]
+    const float* o;          // [M, C] the attention output (av)
+    const float* dout;       // [M, C] dL/d(av)
+    const float *cosv, *sinv;
+    float* dq;               // rows of ldq floats: gradient of q before RoPE
+    int ldq;
+    float *dk, *dv;          // rows of ldkv floats: of k before RoPE, of v before the value mix
+    int ldkv;
+    float* dfirst;           // [M, D]: the value-residual source's gradient
+    int B, vmix;
+    float ca, mixc, scale;
+};
+
+template <int KS, int TT, int DT>
+struct AttnBwdShape {
+    static constexpr int C = 32 * KS, D = 16 * DT, H = C / D, T = 16 * TT, HT = H * T, C4 = C / 4, D4 = D / 4;
+    static constexpr int QLD = C + 4, KLD = D + 4, VLD = T + 4, SLD = HT + 4, XLD = 2 * D + 4;
+    // query side (floats): G [16][QLD] | Vf [T][KLD] | Kt [D][VLD] | Pm [16H][VLD] | Dq [16H] | dqs [16][QLD]
+    // (dqs first holds the [16][C4] partial dots of D)
+    static constexpr int QG = 0, QV = QG + 16 * QLD, QK = QV + T * KLD, QP = QK + D * VLD, QD = QP + 16 * H * VLD,
+                         QO = QD + 16 * H, QEND = QO + 16 * QLD;
+    // key side: G [T][QLD] | Qs [T][QLD] | Vs [16][KLD] | Ps [16][SLD] | dSs [16][SLD] | Dk [HT]
+    // (dSs first holds the [T][C4] partial dots; G | Qs last hold the [2][16][XLD] halves of dk | dv)
+    static constexpr int KG = 0, KQ = KG + T * QLD, KV = KQ + T * QLD, KP = KV + 16 * KLD, KS_ = KP + 16 * SLD,
+                         KD = KS_ + 16 * SLD, KEND = KD + HT;
+    static constexpr int BYTES = 4 * (QEND > KEND ? QEND : KEND);
+    static_assert(T * C4 <= 16 * SLD && 16 * C4 <= 16 * QLD && 2 * 16 * XLD <= 2 * T * QLD, "aliased LDS");
+    static_assert(BYTES <= 160 * 1024, "loop_attn_bwd LDS");
+    static_assert(H % 2 == 0, "two halves of the heads");
+};
+
+template <int KS, int TT, int DT>
+__global__ __launch_bounds__(1024) void loop_attn_bwd_kernel(LoopAttnBwdArgs a) {
+#pragma clang fp contract(off)
+    using S = AttnBwdShape<KS, TT, DT>;
+    constexpr int C = S::C, D = S::D, H = S::H, T = S::T, HT = S::HT, C4 = S::C4, D4 = S::D4;
+    constexpr int QLD = S::QLD, KLD = S::KLD, VLD = S::VLD, SLD = S::SLD, XLD = S::XLD, mid = D / 2;
+    extern __shared__ __align__(16) float lds_f[];
+    int b, item;
+    if (!seq_block(a.B, 2 * TT, b, item)) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const size_t seq0 = size_t(b) * T;
+
+    if (item < TT) {   // ---- query side: rows qt*16 ..
+        const int qt = item;
+        const size_t own0 = seq0 + size_t(qt) * 16;
+        float* G = lds_f + S::QG;
+        float* Vf = lds_f + S::QV;
+        float* Kt = lds_f + S::QK;
+        float* Pm = lds_f + S::QP;
+        float* Dq = lds_f + S::QD;
+        float* dqs = lds_f + S::QO;
+        {
+            constexpr int NG = 16 * C4, NV = T * D4, NP = 16 * H * (T / 4);
+            static_assert(NG <= 1024 && NV <= 1024 && NP <= 1024, "one chunk per thread");
+            float4 gv, ov, vv, kv, pv;
+            const int r = tid / C4, c4 = tid - r * C4;
+            const int t = tid / D4, d4 = tid - t * D4;
+            const int pr = tid / (T / 4), pc = tid - pr * (T / 4);   // pr = h * 16 + row
+            if (tid < NG) {
+                gv = ld4(a.dout + (own0 + r) * C + 4 * c4);
+                ov = ld4(a.o + (own0 + r) * C + 4 * c4);
+            }
+            if (tid < NV) {
+                vv = ld4(a.v + (seq0 + t) * C + 4 * d4);
+                kv = ld4(a.k + (seq0 + t) * C + 4 * d4);
+            }
+            if (tid < NP)
+                pv = ld4(a.probs + ((size_t(b) * H + pr / 16) * T + qt * 16 + pr % 16) * T + 4 * pc);
+            if (tid < NG) {
+                st4(G + r * QLD + 4 * c4, gv);
+                dqs[r * C4 + c4] = ((gv.x * ov.x + gv.y * ov.y) + gv.z * ov.z) + gv.w * ov.w;
+            }
+            if (tid < NV) {
+                st4(Vf + t * KLD + 4 * d4, vv);
+                Kt[(4 * d4 + 0) * VLD + t] = kv.x;
+                Kt[(4 * d4 + 1) * VLD + t] = kv.y;
+                Kt[(4 * d4 + 2) * VLD + t] = kv.z;
+                Kt[(4 * d4 + 3) * VLD + t] = kv.w;
+            }
+            if (tid < NP) st4(Pm + pr * VLD + 4 * pc, pv);
+        }
+        lds_barrier();
+        if (tid < 16 * H) {   // D[h][row] = sum of the head's partial dots, in chunk order
+            const int h = tid / 16, r = tid % 16;
+            float s = 0.0f;
+            for (int j = 0; j < D4; ++j) s += dqs[r * C4 + h * D4 + j];
+            Dq[tid] = s;
+        }
+        lds_barrier();
+        // dS = P * (dP - D), dP[t][s] = dO_h[t] . V[s], per (head, 16 keys).
+        for (int tile = wave; tile < H * TT; tile += 16) {
+            const int h = tile / TT, kt = tile - h * TT;
+            const f32x4 acc = dot_tile(G + r16 * QLD + h * D + 4 * q4, Vf + (kt * 16 + r16) * KLD + 4 * q4, D);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pr = h * 16 + 4 * q4 + e;
+                float* p = Pm + pr * VLD + kt * 16 + r16;
+                *p = *p * (acc[e] - Dq[pr]);
+            }
+        }
+        lds_barrier();
+        // dq_h = scale * dS_h . K, per (head, 16 columns).
+        for (int tile = wave; tile < H * DT; tile += 16) {
+            const int h = tile / DT, dt = tile - h * DT;
+            const f32x4 acc = dot_tile(Pm + (h * 16 + r16) * VLD + 4 * q4, Kt + (dt * 16 + r16) * VLD + 4 * q4, T);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dqs[(4 * q4 + e) * QLD + h * D + dt * 16 + r16] = acc[e] * a.scale;
+        }
+        lds_barrier();
+        // rope_bwd (metal/kernels.metal:891-909).
+        for (int e = tid; e < 16 * C; e += 1024) {
+            const int r = e / C, col = e - r * C, d = col % D, t = qt * 16 + r;
+            const float c = a.cosv[t * D + d], s = a.sinv[t * D + d];
+            const float* row = dqs + r * QLD;
+            a.dq[(own0 + r) * a.ldq + col] = d < mid ? row[col] * c + row[col + mid] * s : row[col] * c - row[col - mid] * s;
+        }
+        return;
+    }
+
+    // ---- key side: keys s0 ..
+    const int s0 = (item - TT) * 16;
+    float* G = lds_f + S::KG;
+    float* Qs = lds_f + S::KQ;
+    float* Vs = lds_f + S::KV;
+    float* Ps = lds_f + S::KP;
+    float* dSs = lds_f + S::KS_;
+    float* Dk = lds_f + S::KD;
+    {
+        constexpr int NG = T * C4, NV = 16 * D4, NP = HT * 4;   // P: (h, t) rows of 16 keys = 4 float4
+        constexpr int RG = (NG + 1023) / 1024;
+        float4 gv[RG], ov[RG], qv[RG], vv, pv;
+#pragma unroll
+        for (int i = 0; i < RG; ++i) {
+            const int e = min(tid + 1024 * i, NG - 1), t = e / C4, c4 = e - t * C4;
+            gv[i] = ld4(a.dout + (seq0 + t) * C + 4 * c4);
+            ov[i] = ld4(a.o + (seq0 + t) * C + 4 * c4);
+            qv[i] = ld4(a.q + (seq0 + t) * C + 4 * c4);
+        }
+        const int vr = tid / D4, vd = tid - vr * D4;
+        if (tid < NV) vv = ld4(a.v + (seq0 + s0 + vr) * C + 4 * vd);
+        const int ph = tid / 4, pc = tid - ph * 4;   // ph = h * T + t
+        if (tid < NP) pv = ld4(a.probs + ((size_t(b) * H + ph / T) * T + ph % T) * T + s0 + 4 * pc);
+#pragma unroll
+        for (int i = 0; i < RG; ++i) {
+            const int e = tid + 1024 * i, t = e / C4, c4 = e - t * C4;
+            if (e < NG) {
+                st4(G + t * QLD + 4 * c4, gv[i]);
+                st4(Qs + t * QLD + 4 * c4, qv[i]);
+                dSs[t * C4 + c4] = ((gv[i].x * ov[i].x + gv[i].y * ov[i].y) + gv[i].z * ov[i].z) + gv[i].w * ov[i].w;
+            }
+        }
+        if (tid < NV) st4(Vs + vr * KLD + 4 * vd, vv);
+        if (tid < NP) {
+            Ps[(4 * pc + 0) * SLD + ph] = pv.x;
+            Ps[(4 * pc + 1) * SLD + ph] = pv.y;
+            Ps[(4 * pc + 2) * SLD + ph] = pv.z;
+            Ps[(4 * pc + 3) * SLD + ph] = pv.w;
+        }
+    }
+    lds_barrier();
+    for (int e = tid; e < HT; e += 1024) {   // D[h][t], e = h * T + t
+        const int h = e / T, t = e - h * T;
+        float s = 0.0f;
+        for (int j = 0; j < D4; ++j) s += dSs[t * C4 + h * D4 + j];
+        Dk[e] = s;
+    }
+    lds_barrier();
+    // dS^T[s][(h, t)] = P * (dP - D), dP^T[s][t] = V[s] . dO_h[t], per (head, 16 queries).
+    for (int tile = wave; tile < H * TT; tile += 16) {
+        const int h = tile / TT, tt = tile - h * TT;
+        const f32x4 acc = dot_tile(Vs + r16 * KLD + 4 * q4, G + (tt * 16 + r16) * QLD + h * D + 4 * q4, D);
+        const int ht = h * T + tt * 16 + r16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int o = (4 * q4 + e) * SLD + ht;
+            dSs[o] = Ps[o] * (acc[e] - Dk[ht]);
+        }
+    }
+    lds_barrier();
+    // dk = sum_(h,t) dS^T[s][(h,t)] Q_h[t], dv = sum_(h,t) P^T[s][(h,t)] dO_h[t]:
+    // items (dk | dv, 16 columns, half of the heads).
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int item2 = wave;
+    const bool busy = item2 < 4 * DT;
+    const int which = item2 / (2 * DT), dt = (item2 / 2) % DT, half = item2 % 2;
+    if (busy) {
+        const float* A = (which == 0 ? dSs : Ps) + r16 * SLD;
+        const float* X = which == 0 ? Qs : G;
+        const int d = dt * 16 + r16;
+        for (int k0 = half * (HT / 2); k0 < (half + 1) * (HT / 2); k0 += 16) {
+            const float4 av = ld4(A + k0 + 4 * q4);
+            const int h = k0 / T, t = k0 - h * T + 4 * q4;
+            const float* xb = X + t * QLD + h * D + d;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, xb[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, xb[QLD], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, xb[2 * QLD], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, xb[3 * QLD], acc, 0, 0, 0);
+        }
+    }
+    lds_barrier();   // G and Qs are no longer read: the halves go where they were
+    float* st = G;   // [2][16][XLD]: columns 0 .. D-1 dk, D .. 2D-1 dv
+    if (busy) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[(half * 16 + 4 * q4 + e) * XLD + which * D + dt * 16 + r16] = acc[e];
+    }
+    lds_barrier();
+    // rope_bwd of dk (one head), the value residual of dv.
+    for (int e = tid; e < 16 * mid; e += 1024) {
+        const int s = e / mid, d = e - s * mid, t = s0 + s;
+        const float x0 = (st[s * XLD + d] + st[(16 + s) * XLD + d]) * a.scale;
+        const float x1 = (st[s * XLD + d + mid] + st[(16 + s) * XLD + d + mid]) * a.scale;
+        float* o = a.dk + (seq0 + t) * a.ldkv;
+        o[d] = x0 * a.cosv[t * D + d] + x1 * a.sinv[t * D + d];
+        o[d + mid] = x1 * a.cosv[t * D + d + mid] - x0 * a.sinv[t * D + d + mid];
+    }
+    for (int e = tid; e < 16 * D; e += 1024) {
+        const int s = e / D, d = e - s * D;
+        const size_t row = seq0 + s0 + s;
+        const float v = st[s * XLD + D + d] + st[(16 + s) * XLD + D + d];
+        float* f = a.dfirst + row * D + d;
+        if (a.vmix == 0) {
+            a.dv[row * a.ldkv + d] = v + *f;
+        } else {
+            const float p = a.ca * v;
+            const float r = 0.0f * v;
+            a.dv[row * a.ldkv + d] = p + r;
+            *f += a.mixc * v;
+        }
+    }
+}
+
 // ---- host side -------------------------------------------------------------------------
 template <int BITS, int KS, int TT, int DT, int NP>
 int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv, const float* sinv,
@@ -823,6 +1069,22 @@ bool shape_built(const dgm_dit_cfg* c) {
     return (ks == 6 && tt == 4 && dt == 3 && np == 6) || (ks == 2 && tt == 1 && dt == 1 && np == 1);
 }
 
+
+template <int KS, int TT, int DT>
+int run_attn_bwd(dgm_gpu* g, const LoopAttnBwdArgs& a) {
+    using S = AttnBwdShape<KS, TT, DT>;
+    auto k = loop_attn_bwd_kernel<KS, TT, DT>;
+    if (S::BYTES > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES);
+        if (e != hipSuccess)
+            return dgm::fail(g, DGM_ERR_HIP, "dit_backward: cannot reserve %d bytes of LDS: %s", S::BYTES,
+                             hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(k, dim3(unsigned(8 * ((a.B + 7) / 8) * 2 * TT)), dim3(1024), size_t(S::BYTES), g->stream, a);
+    return dgm::check_launch(g, "dit_backward loop_attn_bwd");
+}
+
 }  // namespace
 
 namespace dgm {
@@ -857,6 +1119,24 @@ int dit_forward_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w
                       const float* sinv, float* x, const DitLoopBufs& buf, const DitSaves* saves) {
     return c->bits == 8 ? dispatch<8>(g, c, w, cosv, sinv, x, buf, saves)
                         : dispatch<4>(g, c, w, cosv, sinv, x, buf, saves);
+}
+
+
+int dit_attn_bwd_loop(dgm_gpu* g, const dgm_dit_cfg* c, const float* q, const float* k, const float* v,
+                      const float* probs, const float* o, const float* dout, const float* cosv, const float* sinv,
+                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first) {
+    if (!dit_loop_shape_ok(c) || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(probs, 16) ||
+        !aligned(o, 16) || !aligned(dout, 16))
+        return kNotFused;
+    LoopAttnBwdArgs a{};
+    a.q = q; a.k = k; a.v = v; a.probs = probs; a.o = o; a.dout = dout; a.cosv = cosv; a.sinv = sinv;
+    a.dq = dq; a.ldq = ldq; a.dk = dk; a.dv = dv; a.ldkv = ldkv; a.dfirst = dfirst;
+    a.B = c->B; a.vmix = first ? 0 : 1; a.ca = 1.0f - c->mix; a.mixc = c->mix;
+    a.scale = 1.0f / sqrtf(float(c->D));
+    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16;
+    if (ks == 6 && tt == 4 && dt == 3) return run_attn_bwd<6, 4, 3>(g, a);
+    if (ks == 2 && tt == 1 && dt == 1) return run_attn_bwd<2, 1, 1>(g, a);
+    return kNotFused;
 }
 
 }  // namespace dgm

@@ -1251,17 +1251,24 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
         }
         DGM_TRY(bwd(w->wo, dattn, A(l, A_AV), S[B_DAV], gr->wo, C, C));
-        DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK], S[B_DV],
-                            S[B_DPROBS], S[B_DSCORES], B, T, H, D));
-        // sum_heads of dk and dv, rope_bwd of dq and dk, the value-residual
-        // copy + acc (loop 0) or mix + acc_scale in one launch.
+        // The attention backward with sum_heads of dk and dv, rope_bwd of dq
+        // and dk and the value residual: one launch for the built shapes,
+        // else attnBwd and the per-row gradient kernel.
+        float *oq = qkv1 ? qkvrow : S[B_QPRE], *ok = qkv1 ? qkvrow + C : S[B_KPRE];
+        float* ov = qkv1 ? qkvrow + C + KV : S[B_DVPRE];
+        const int ldq = qkv1 ? int(QKV) : int(C), ldkv = qkv1 ? int(QKV) : int(KV);
+        int ra = dgm::dit_attn_bwd_loop(g, c, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), A(l, A_AV), S[B_DAV],
+                                        cosv, sinv, oq, ldq, ok, ov, ldkv, S[B_DFIRST], l == 0);
+        if (ra == dgm::kNotFused) {
+            DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK],
+                                S[B_DV], S[B_DPROBS], S[B_DSCORES], B, T, H, D));
+            ra = launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, oq, ldq, ok, ldkv, ov, ldkv, S[B_DFIRST], B,
+                                 T, H, D, l == 0, mix);
+        }
+        DGM_TRY(ra);
         if (qkv1) {
-            DGM_TRY(launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, qkvrow, int(QKV), qkvrow + C, int(QKV),
-                                    qkvrow + C + KV, int(QKV), S[B_DFIRST], B, T, H, D, l == 0, mix));
             DGM_TRY(bwd(w->wq, qkvrow, A(l, A_LN1), t2, gr->wq, QKV, C));
         } else {
-            DGM_TRY(launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, S[B_QPRE], int(C), S[B_KPRE], int(KV),
-                                    S[B_DVPRE], int(KV), S[B_DFIRST], B, T, H, D, l == 0, mix));
             DGM_TRY(bwd(w->wq, S[B_QPRE], A(l, A_LN1), t2, gr->wq, C, C));
             DGM_TRY(bwd(w->wk, S[B_KPRE], A(l, A_LN1), dln, gr->wk, KV, C));
             DGM_TRY(dgm_acc(g, t2, dln, nC));
