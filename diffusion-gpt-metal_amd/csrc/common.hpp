@@ -107,10 +107,14 @@ int dit_forward_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w
 // the saved q, k, v ([B*T, C], k and v repeated to every head), probs and av
 // and dL/d(av): the gradients of q before RoPE, of k before RoPE and of v
 // before the value mix (summed over the heads), and dfirst updated (loop 0:
-// first = true). Returns kNotFused, launching nothing, for other shapes.
+// first = true; fresh = true when dfirst holds nothing yet, which the first
+// loop the backward runs then writes instead of adding to). Returns
+// kNotFused, launching nothing, unless dit_attn_bwd_loop_ok holds for the
+// activation and workspace buffers (16-byte aligned pieces).
+bool dit_attn_bwd_loop_ok(const dgm_dit_cfg* c, const float* acts, const float* ws);
 int dit_attn_bwd_loop(dgm_gpu* g, const dgm_dit_cfg* c, const float* q, const float* k, const float* v,
                       const float* probs, const float* o, const float* dout, const float* cosv, const float* sinv,
-                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first);
+                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first, bool fresh);
 // True when `next`'s weights (fp32 for bits 32, else codes and scales)
 // start where `first`'s `rows` x K end, so the two act as one [2 rows, K]
 // linear.

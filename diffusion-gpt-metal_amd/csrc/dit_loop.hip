@@ -39,6 +39,9 @@ namespace {
 
 using dgm_rows::add4;
 using dgm_rows::norm4;
+using dgm_rows::row16_max;
+using dgm_rows::row16_sum;
+using dgm_rows::wave64_sum;
 using dgm_rows::rstd16;
 using dgm_rows::silu_sigmoid;
 
@@ -147,40 +150,6 @@ __device__ __forceinline__ f32x4 dot_tile(const float* a, const float* b, int n)
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, y.w, acc, 0, 0, 0);
     }
     return acc;
-}
-
-// Cross-lane sums and maxima on DPP and permlane swaps (no LDS round trips).
-// Every lane of the reduced group gets the same bits: each step adds a value
-// and its partner's, and addition is commutative.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
-    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
-    v += dpp_f<0x141>(v);   // row_half_mirror: the other quad of the 8
-    v += dpp_f<0x140>(v);   // row_mirror: the other 8 of the 16
-    return v;
-}
-
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    v = fmaxf(v, dpp_f<0x140>(v));
-    return v;
-}
-
-__device__ __forceinline__ float wave64_sum(float v) {
-    v = row16_sum(v);
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                      false, false);   // rows 0 <-> 1, 2 <-> 3
-    v = __builtin_bit_cast(float, uint32_t(r16[0])) + __builtin_bit_cast(float, uint32_t(r16[1]));
-    const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                      false, false);   // lanes 0-31 <-> 32-63
-    return __builtin_bit_cast(float, uint32_t(r32[0])) + __builtin_bit_cast(float, uint32_t(r32[1]));
 }
 
 // rstd of one row held by a whole wave, one float4 per lane (columns 4 lane ..
@@ -743,6 +712,7 @@ struct LoopAttnBwdArgs {
     int ldkv;
     float* dfirst;           // [M, D]: the value-residual source's gradient
     int B, vmix;
+    int fresh;               // dfirst holds nothing yet (the first loop the backward runs)
     float ca, mixc, scale;
 };
 
@@ -955,13 +925,14 @@ __global__ __launch_bounds__(1024) void loop_attn_bwd_kernel(LoopAttnBwdArgs a) 
         const size_t row = seq0 + s0 + s;
         const float v = st[s * XLD + D + d] + st[(16 + s) * XLD + D + d];
         float* f = a.dfirst + row * D + d;
+        const float f0 = a.fresh ? 0.0f : *f;
         if (a.vmix == 0) {
-            a.dv[row * a.ldkv + d] = v + *f;
+            a.dv[row * a.ldkv + d] = v + f0;
         } else {
             const float p = a.ca * v;
             const float r = 0.0f * v;
             a.dv[row * a.ldkv + d] = p + r;
-            *f += a.mixc * v;
+            *f = f0 + a.mixc * v;
         }
     }
 }
@@ -1122,16 +1093,20 @@ int dit_forward_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w
 }
 
 
+bool dit_attn_bwd_loop_ok(const dgm_dit_cfg* c, const float* acts, const float* ws) {
+    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16;
+    return dit_loop_shape_ok(c) && ((ks == 6 && tt == 4 && dt == 3) || (ks == 2 && tt == 1 && dt == 1)) &&
+           aligned(acts, 16) && aligned(ws, 16);
+}
+
 int dit_attn_bwd_loop(dgm_gpu* g, const dgm_dit_cfg* c, const float* q, const float* k, const float* v,
                       const float* probs, const float* o, const float* dout, const float* cosv, const float* sinv,
-                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first) {
-    if (!dit_loop_shape_ok(c) || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(probs, 16) ||
-        !aligned(o, 16) || !aligned(dout, 16))
-        return kNotFused;
+                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first, bool fresh) {
+    if (!dit_attn_bwd_loop_ok(c, q, dout)) return kNotFused;
     LoopAttnBwdArgs a{};
     a.q = q; a.k = k; a.v = v; a.probs = probs; a.o = o; a.dout = dout; a.cosv = cosv; a.sinv = sinv;
     a.dq = dq; a.ldq = ldq; a.dk = dk; a.dv = dv; a.ldkv = ldkv; a.dfirst = dfirst;
-    a.B = c->B; a.vmix = first ? 0 : 1; a.ca = 1.0f - c->mix; a.mixc = c->mix;
+    a.B = c->B; a.vmix = first ? 0 : 1; a.fresh = fresh ? 1 : 0; a.ca = 1.0f - c->mix; a.mixc = c->mix;
     a.scale = 1.0f / sqrtf(float(c->D));
     const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16;
     if (ks == 6 && tt == 4 && dt == 3) return run_attn_bwd<6, 4, 3>(g, a);

@@ -53,4 +53,38 @@ __device__ __forceinline__ float silu_sigmoid(float z) {
     return e / (1.0f + e);
 }
 
+// Cross-lane sums and maxima on DPP and permlane swaps (no LDS round trips).
+// Every lane of the reduced group gets the same bits: each step adds a value
+// and its partner's, and addition is commutative.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    v += dpp_f<0x141>(v);   // row_half_mirror: the other quad of the 8
+    v += dpp_f<0x140>(v);   // row_mirror: the other 8 of the 16
+    return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+
+__device__ __forceinline__ float wave64_sum(float v) {
+    v = row16_sum(v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);   // rows 0 <-> 1, 2 <-> 3
+    v = __builtin_bit_cast(float, uint32_t(r16[0])) + __builtin_bit_cast(float, uint32_t(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                      false, false);   // lanes 0-31 <-> 32-63
+    return __builtin_bit_cast(float, uint32_t(r32[0])) + __builtin_bit_cast(float, uint32_t(r32[1]));
+}
+
 }  // namespace dgm_rows

@@ -32,6 +32,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "dit_rows.hpp"
 
 #pragma clang fp contract(off)
 
@@ -39,11 +40,8 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+// Sum over the wave on DPP and permlane swaps; every lane gets the same bits.
+__device__ __forceinline__ float wave_sum(float v) { return dgm_rows::wave64_sum(v); }
 
 constexpr int kDwWaves = 16;
 
@@ -226,15 +224,15 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainAr
             const float* x = a.st[0].x;
             const float* r1 = a.st[0].r;
             int r = wave;
-            for (; r + 7 * kDwWaves < rows; r += 8 * kDwWaves) {
-                float v[8];
+            for (; r + 15 * kDwWaves < rows; r += 16 * kDwWaves) {   // 16 rows' loads in flight
+                float v[16];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < 16; ++u) {
                     const int rr = r + u * kDwWaves;
                     v[u] = a.dy[size_t(rr) * cols + c] * x[size_t(rr) * cols + c] * r1[rr];
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc += v[u];
+                for (int u = 0; u < 16; ++u) acc += v[u];
             }
             for (; r < rows; r += kDwWaves) acc += a.dy[size_t(r) * cols + c] * x[size_t(r) * cols + c] * r1[r];
         } else {
@@ -1201,7 +1199,10 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         ra.npin = nrb; ra.rows = int(M); ra.cols = int(C);
         return launch_rms_chain(g, ra);
     };
-    DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
+    // The one-launch attention backward writes dfirst in the first loop it
+    // runs; the per-row gradient kernel adds to it, so it starts at zero.
+    const bool attn1 = dgm::dit_attn_bwd_loop_ok(c, acts, ws);
+    if (!attn1) DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
     const int L = c->loops;
     float* dmlp = t2;   // dL/dmlp of the loop about to run
     if (chain && L > 0) {
@@ -1257,15 +1258,19 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         float *oq = qkv1 ? qkvrow : S[B_QPRE], *ok = qkv1 ? qkvrow + C : S[B_KPRE];
         float* ov = qkv1 ? qkvrow + C + KV : S[B_DVPRE];
         const int ldq = qkv1 ? int(QKV) : int(C), ldkv = qkv1 ? int(QKV) : int(KV);
-        int ra = dgm::dit_attn_bwd_loop(g, c, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), A(l, A_AV), S[B_DAV],
-                                        cosv, sinv, oq, ldq, ok, ov, ldkv, S[B_DFIRST], l == 0);
-        if (ra == dgm::kNotFused) {
+        if (attn1) {
+            const int ra = dgm::dit_attn_bwd_loop(g, c, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), A(l, A_AV),
+                                                  S[B_DAV], cosv, sinv, oq, ldq, ok, ov, ldkv, S[B_DFIRST], l == 0,
+                                                  l == L - 1);
+            if (ra == dgm::kNotFused)
+                return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_backward: attention backward shape changed");
+            DGM_TRY(ra);
+        } else {
             DGM_TRY(dgm_attnBwd(g, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), S[B_DAV], S[B_DQ], S[B_DK],
                                 S[B_DV], S[B_DPROBS], S[B_DSCORES], B, T, H, D));
-            ra = launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, oq, ldq, ok, ldkv, ov, ldkv, S[B_DFIRST], B,
-                                 T, H, D, l == 0, mix);
+            DGM_TRY(launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, oq, ldq, ok, ldkv, ov, ldkv,
+                                    S[B_DFIRST], B, T, H, D, l == 0, mix));
         }
-        DGM_TRY(ra);
         if (qkv1) {
             DGM_TRY(bwd(w->wq, qkvrow, A(l, A_LN1), t2, gr->wq, QKV, C));
         } else {
