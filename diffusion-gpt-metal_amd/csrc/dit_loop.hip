@@ -27,8 +27,9 @@
 // (hi: the top 8 significand bits, mid: the next 8 of the remainder, lo: what
 // is left, at most 8 bits). Every product is exact; each 32-k group's sum is
 // accumulated in fp32 (lo, mid, then hi pieces) and multiplied by the group's
-// scale. The row chains, RoPE, softmax and SwiGLU use the standalone kernels'
-// formulas, so results agree with the oracle to fp32 rounding of the sums.
+// scale. RoPE, softmax, SwiGLU and the row chains use the standalone kernels'
+// formulas (the chains' rstd with the hardware inverse square root), so
+// results agree with the oracle to fp32 rounding of the sums.
 #include <algorithm>
 #include <cmath>
 
@@ -154,15 +155,20 @@ __device__ __forceinline__ f32x4 dot_tile(const float* a, const float* b, int n)
 
 // rstd of one row held by a whole wave, one float4 per lane (columns 4 lane ..
 // 4 lane + 3; lanes past the row's end hold zeros): 1 / sqrt(mean(x^2) + eps).
-__device__ __forceinline__ float rstd_row(float4 v, int cols, float eps) {
+// The mean is a product with 1/cols and the inverse square root the hardware
+// one (v_rsq_f32, within 1 ulp), not the IEEE divide and square root of the
+// standalone rmsnorm_fwd: the row chains here are VALU-bound, and the results
+// stay within a few ulp of the correctly rounded formula.
+template <int COLS>
+__device__ __forceinline__ float rstd_row(float4 v, float eps) {
 #pragma clang fp contract(off)
     float ss = v.x * v.x;
     ss += v.y * v.y;
     ss += v.z * v.z;
     ss += v.w * v.w;
     ss = wave64_sum(ss);
-    const float mean = ss / float(cols);
-    return 1.0f / sqrtf(mean + eps);
+    const float mean = ss * (1.0f / float(COLS));
+    return __builtin_amdgcn_rsqf(mean + eps);
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -276,17 +282,17 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
     const bool saver = g == 0;
     float rs;
     if (!a.first) {
-        rs = rstd_row(act ? y : z4, C, a.eps);   // rms(mlp)
+        rs = rstd_row<C>(act ? y : z4, a.eps);   // rms(mlp)
         if (saver && act && a.pmlp) st4(a.pmlp + row * C + c0, y);
         if (saver && a.pr2b && lane == 0) a.pr2b[row] = rs;
         y = add4(mp, norm4(y, rs, w2));          // pre = mid + rms(mlp) * n2b
         if (saver && act && a.ppre) st4(a.ppre + row * C + c0, y);
-        rs = rstd_row(act ? y : z4, C, a.eps);   // rms(pre)
+        rs = rstd_row<C>(act ? y : z4, a.eps);   // rms(pre)
         if (saver && a.prf && lane == 0) a.prf[row] = rs;
         y = norm4(y, rs, w3);                    // x = rms(pre) * nf
     }
     if (saver && act && a.xo) st4(a.xo + row * C + c0, y);
-    rs = rstd_row(act ? y : z4, C, a.eps);       // ln1 = rms(x) * n1
+    rs = rstd_row<C>(act ? y : z4, a.eps);       // ln1 = rms(x) * n1
     if (saver && a.sr1 && lane == 0) a.sr1[row] = rs;
     const float4 ln = norm4(y, rs, w1);
     if (saver && act && a.sln1) st4(a.sln1 + row * C + c0, ln);
@@ -537,11 +543,11 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
         const size_t o = (own0 + r) * C + c0;
         const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         float4 y = ld4(at + r * QLD + c0);
-        float rs = rstd_row(act ? y : z4, C, a.eps);
+        float rs = rstd_row<C>(act ? y : z4, a.eps);
         if (lane == 0 && a.sr1b) a.sr1b[own0 + r] = rs;
         y = add4(ld4(xs + r * QLD + c0), norm4(y, rs, ld4(nrm + c0)));
         if (act) st4(a.mid + o, y);
-        rs = rstd_row(act ? y : z4, C, a.eps);
+        rs = rstd_row<C>(act ? y : z4, a.eps);
         if (lane == 0 && a.sr2) a.sr2[own0 + r] = rs;
         if (act) st4(a.ln2 + o, norm4(y, rs, ld4(nrm + C + c0)));
     }
@@ -680,11 +686,11 @@ __global__ __launch_bounds__(256) void loop_tail_kernel(LoopTailArgs a) {
 #pragma unroll
     for (int p = 1; p < NP; ++p) y = add4(y, pp[p]);   // slab order
     if (act && a.pmlp) st4(a.pmlp + row * C + c0, y);
-    float rs = rstd_row(act ? y : z4, C, a.eps);
+    float rs = rstd_row<C>(act ? y : z4, a.eps);
     if (a.pr2b && lane == 0) a.pr2b[row] = rs;
     y = add4(m, norm4(y, rs, w2));
     if (act && a.ppre) st4(a.ppre + row * C + c0, y);
-    rs = rstd_row(act ? y : z4, C, a.eps);
+    rs = rstd_row<C>(act ? y : z4, a.eps);
     if (a.prf && lane == 0) a.prf[row] = rs;
     if (act) st4(a.x + row * C + c0, norm4(y, rs, w3));
 }
