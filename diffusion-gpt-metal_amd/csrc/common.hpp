@@ -64,7 +64,9 @@ constexpr int64_t kMaxIndex = (int64_t(1) << 31) - 1;
 
 // Where the DiT block's training forward stores one loop's activations (the
 // reference's Acts, src/DiT.swift:260-300): x, ln1 and its rstd, q / k / v
-// as the attention consumed them ([B*T, C], k and v repeated to every head),
+// as the attention consumed them ([B*T, C], k and v repeated to every head;
+// dit_forward_loops stores only the KV head, columns 0 .. D-1, which is all
+// dit_attn_bwd_loop reads),
 // probs, av, attn, rstd of rms(attn), mid, ln2 and its rstd, gate, up, sw,
 // mlp, rstd of rms(mlp), pre, rstd of rms(pre).
 struct DitSaves {

@@ -962,7 +962,8 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
     }
     // mid alternates between two buffers (a loop reads the previous loop's
     // mid while writing its own), or is saved per loop; q / k / v are the
-    // training saves ([M, C], k and v repeated to every head) or the
+    // training saves ([M, C] rows; k and v hold the KV head in columns
+    // 0 .. D-1, which is all the backward of these shapes reads) or the
     // inference buffers (k, v as [M, D]).
     auto mid_of = [&](int l) { return sv ? sv[l].mid : buf.mid[l & 1]; };
     auto ln2_of = [&](int l) { return sv ? sv[l].ln2 : buf.ln2; };
@@ -982,7 +983,7 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         ra.Wqkv = w->wq.q; ra.Sqkv = w->wq.scale;
         ra.cosv = cosv; ra.sinv = sinv;
         ra.vfirst = buf.vfirst;
-        ra.q = q; ra.k = k; ra.v = v; ra.kv_ld = kv_ld; ra.krep = sv ? H : 1;
+        ra.q = q; ra.k = k; ra.v = v; ra.kv_ld = kv_ld; ra.krep = 1;   // the KV head only (columns 0 .. D-1)
         ra.xo = (sv || l > 0) ? xl : nullptr;
         if (sv) {
             ra.sln1 = sv[l].ln1; ra.sr1 = sv[l].r1;

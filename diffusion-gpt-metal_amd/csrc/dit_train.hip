@@ -1138,6 +1138,10 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         if (!p) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: null norm gradient");
     if (acts_n < acts_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: activation buffer too small");
     if (ws_n < bwd_floats(c)) return dgm::fail(g, DGM_ERR_ARG, "dit_backward: workspace too small");
+    // The loop shapes' forward keeps k and v of the KV head only, which the
+    // one-launch attention backward reads; it needs 16-byte aligned buffers.
+    if (dgm::dit_loop_shape_ok(c) && !dgm::dit_attn_bwd_loop_ok(c, acts, ws))
+        return dgm::fail(g, DGM_ERR_ARG, "dit_backward: acts and ws must be 16-byte aligned");
     int64_t asz[A_COUNT], fsz[F_COUNT], bsz[B_COUNT];
     act_sizes(c, asz, fsz);
     bwd_sizes(c, bsz);
