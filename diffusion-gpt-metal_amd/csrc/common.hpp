@@ -150,6 +150,20 @@ int gemm_bwd_swiglu(dgm_gpu* g, int bits, const float* w, const void* q, const f
                     const float* x, const float* gate, const float* up, float* dgu, float* dw, int64_t M, int64_t N,
                     int64_t K, int64_t qGroup);
 
+// The STE backward of a quantized linear with dX on bf16 MFMA (gemm_f32.hip):
+// wt_prep writes the codes (int8, also for int4) and scales of up to 4
+// linears transposed, codesT [K][N] and scalesT [K/G][N], one launch;
+// gemm_bwd_fold then runs dX from them (the group scale folded into dY,
+// which is split into three bf16 pieces) beside the fp32 dW tiles
+// (dW += or = dY^T X), with the SwiGLU backward on dX when sg_gate is set.
+// gemm_bwd_fold returns kNotFused, launching nothing, unless bwd_fold_ok
+// holds and the buffers are aligned (dY and scalesT 16 bytes, codesT 8).
+int wt_prep(dgm_gpu* g, int bits, int nlin, const void* const* W, const float* const* S, const int* N, const int* K,
+            int G, int8_t* const* codesT, float* const* scalesT);
+bool bwd_fold_ok(int M, int N, int K, int G);
+int gemm_bwd_fold(dgm_gpu* g, const int8_t* codesT, const float* scalesT, const float* dY, const float* X, float* dX,
+                  float* dW, int M, int N, int K, int G, bool accumulate, const float* sg_gate, const float* sg_up);
+
 inline bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }

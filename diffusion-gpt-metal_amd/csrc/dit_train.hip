@@ -883,9 +883,38 @@ enum { F_QPRE, F_KPRE, F_VPRE, F_VFIRST, F_VMIX, F_KROT, F_SCORES, F_T1, F_PART,
 // backwards' later-stage weight gradients (n2b, n1b, nf), reduced by the next
 // chain launch.
 enum { B_T1, B_T2, B_DLN, B_DSW, B_DG, B_DU, B_DAV, B_DQ, B_DK, B_DV, B_DPROBS, B_DSCORES, B_DK1, B_DV1,
-       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_RPA, B_RPB, B_RPC, B_COUNT };
+       B_DFIRST, B_QPRE, B_KPRE, B_DVPRE, B_RPA, B_RPB, B_RPC, B_CT, B_ST, B_COUNT };
+// B_CT / B_ST: the four stacked linears' codes (int8) and scales transposed
+// for the bf16 dX of gemm_bwd_fold ([wq; wk; wv], wo, [wgate; wup], wdown in
+// that order), empty when the backward does not use it.
 
 inline int64_t pad64(int64_t n) { return (n + 63) & ~int64_t(63); }
+
+// The four stacked linears of the bf16-dX backward: (N, K) of [wq; wk; wv],
+// wo, [wgate; wup], wdown; false when the config does not take it.
+bool fold_shapes(const dgm_dit_cfg* c, int (*nk)[2]) {
+    if (!c || (c->bits != 8 && c->bits != 4) || c->B <= 0 || c->T <= 0) return false;
+    const int M = c->B * c->T, C = c->C, F = c->F, KV = c->D;
+    const int v[4][2] = {{C + 2 * KV, C}, {C, C}, {2 * F, C}, {C, F}};
+    for (int i = 0; i < 4; ++i) {
+        if (!dgm::bwd_fold_ok(M, v[i][0], v[i][1], c->group)) return false;
+        nk[i][0] = v[i][0];
+        nk[i][1] = v[i][1];
+    }
+    return true;
+}
+
+// Bytes of transposed codes and floats of transposed scales (each linear's
+// block padded to 256 bytes).
+void fold_sizes(const dgm_dit_cfg* c, int64_t* code_bytes, int64_t* scale_floats) {
+    int nk[4][2];
+    *code_bytes = *scale_floats = 0;
+    if (!fold_shapes(c, nk)) return;
+    for (int i = 0; i < 4; ++i) {
+        *code_bytes += (int64_t(nk[i][0]) * nk[i][1] + 255) & ~int64_t(255);
+        *scale_floats += pad64(int64_t(nk[i][0]) * (nk[i][1] / c->group));
+    }
+}
 
 void act_sizes(const dgm_dit_cfg* c, int64_t* a, int64_t* f) {
     const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
@@ -902,9 +931,11 @@ void bwd_sizes(const dgm_dit_cfg* c, int64_t* b) {
     const int64_t M = int64_t(c->B) * c->T, C = c->C, F = c->F, KV = c->D;
     const int64_t att = int64_t(c->B) * c->H * c->T * c->T;
     const int64_t RP = (M + kDwWaves - 1) / kDwWaves * C;
+    int64_t ct = 0, st = 0;
+    fold_sizes(c, &ct, &st);
     const int64_t bv[B_COUNT] = {M * C, M * C, M * C, M * F, M * F, M * F, M * C,  M * C,  M * C, M * C,
                                  att,   att,   M * KV, M * KV, M * KV, M * C, M * KV, M * KV, RP,    RP,
-                                 RP};
+                                 RP,    (ct + 3) / 4, st};
     for (int i = 0; i < B_COUNT; ++i) b[i] = pad64(bv[i]);
 }
 
@@ -1183,6 +1214,46 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     const bool gu1 = dgm::dit_linear_follows(w->wgate, w->wup, F, C, bits, G) && gr->wup == gr->wgate + F * C;
     const int64_t QKV = qkv1 ? C + 2 * KV : 0;
     float* const qkvrow = S[B_QPRE];   // [M, C + 2 KV] rows when qkv1
+    // dX on bf16 MFMA (gemm_bwd_fold) for the stacked linears: their codes
+    // and scales transposed once here.
+    int fnk[4][2];
+    const bool fold = qkv1 && gu1 && fold_shapes(c, fnk) && dgm::aligned(ws, 16);
+    const int8_t* fct[4] = {};
+    const float* fst[4] = {};
+    if (fold) {
+        const dgm_dit_linear* lins[4] = {&w->wq, &w->wo, &w->wgate, &w->wdown};
+        const void* Wp[4];
+        const float* Sp[4];
+        int8_t* ctp[4];
+        float* stp[4];
+        int Nn[4], Kk[4];
+        int8_t* cc = reinterpret_cast<int8_t*>(S[B_CT]);
+        float* sc = S[B_ST];
+        for (int i = 0; i < 4; ++i) {
+            Wp[i] = lins[i]->q;
+            Sp[i] = lins[i]->scale;
+            Nn[i] = fnk[i][0];
+            Kk[i] = fnk[i][1];
+            ctp[i] = cc;
+            stp[i] = sc;
+            fct[i] = cc;
+            fst[i] = sc;
+            cc += (int64_t(Nn[i]) * Kk[i] + 255) & ~int64_t(255);
+            sc += pad64(int64_t(Nn[i]) * (Kk[i] / G));
+        }
+        DGM_TRY(dgm::wt_prep(g, bits, 4, Wp, Sp, Nn, Kk, G, ctp, stp));
+    }
+    // gemmBwd of stacked linear li (0 [wq; wk; wv], 1 wo, 2 [wgate; wup],
+    // 3 wdown) on the bf16-dX pair when `fold`, else the fp32 pair.
+    auto bwdf = [&](int li, const dgm_dit_linear& Lw, const float* dy, const float* in, float* out, float* dW,
+                    int64_t N, int64_t K) -> int {
+        if (fold) {
+            const int r = dgm::gemm_bwd_fold(g, fct[li], fst[li], dy, in, out, dW, int(M), int(N), int(K), G, true,
+                                             nullptr, nullptr);
+            if (r != dgm::kNotFused) return r;
+        }
+        return bwd(Lw, dy, in, out, dW, N, K);
+    };
     // The RMSNorm backwards that follow each other run as one chained launch
     // when C <= 256: nf + n2b, n2 + n1b, and n1 together with the next loop's
     // nf + n2b. A later stage's weight gradient is summed per row block (RPA:
@@ -1222,9 +1293,11 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         if (gu1) {
             // wdown's backward with the SwiGLU backward in its dX epilogue,
             // else the two launches.
-            const int r = dgm::gemm_bwd_swiglu(g, bits, w->wdown.w, w->wdown.q, w->wdown.scale, dmlp, A(l, A_SW),
-                                               A(l, A_GATE), A(l, A_UP), S[B_DG], gr->wdown, M, C, F,
-                                               bits == 32 ? 8 : G);
+            const int r = fold ? dgm::gemm_bwd_fold(g, fct[3], fst[3], dmlp, A(l, A_SW), S[B_DG], gr->wdown, int(M),
+                                                    int(C), int(F), G, true, A(l, A_GATE), A(l, A_UP))
+                               : dgm::gemm_bwd_swiglu(g, bits, w->wdown.w, w->wdown.q, w->wdown.scale, dmlp,
+                                                      A(l, A_SW), A(l, A_GATE), A(l, A_UP), S[B_DG], gr->wdown, M, C,
+                                                      F, bits == 32 ? 8 : G);
             if (r == dgm::kNotFused) {
                 DGM_TRY(bwd(w->wdown, dmlp, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
                 DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F,
@@ -1232,7 +1305,7 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             } else {
                 DGM_TRY(r);
             }
-            DGM_TRY(bwd(w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, 2 * F, C));
+            DGM_TRY(bwdf(2, w->wgate, S[B_DG], A(l, A_LN2), t2, gr->wgate, 2 * F, C));
         } else {
             DGM_TRY(bwd(w->wdown, dmlp, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
             DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DU], M * F));
@@ -1255,7 +1328,7 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));
             DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
         }
-        DGM_TRY(bwd(w->wo, dattn, A(l, A_AV), S[B_DAV], gr->wo, C, C));
+        DGM_TRY(bwdf(1, w->wo, dattn, A(l, A_AV), S[B_DAV], gr->wo, C, C));
         // The attention backward with sum_heads of dk and dv, rope_bwd of dq
         // and dk and the value residual: one launch for the built shapes,
         // else attnBwd and the per-row gradient kernel.
@@ -1276,7 +1349,7 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
                                     S[B_DFIRST], B, T, H, D, l == 0, mix));
         }
         if (qkv1) {
-            DGM_TRY(bwd(w->wq, qkvrow, A(l, A_LN1), t2, gr->wq, QKV, C));
+            DGM_TRY(bwdf(0, w->wq, qkvrow, A(l, A_LN1), t2, gr->wq, QKV, C));
         } else {
             DGM_TRY(bwd(w->wq, S[B_QPRE], A(l, A_LN1), t2, gr->wq, C, C));
             DGM_TRY(bwd(w->wk, S[B_KPRE], A(l, A_LN1), dln, gr->wk, KV, C));

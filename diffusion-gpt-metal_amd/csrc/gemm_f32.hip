@@ -1322,6 +1322,215 @@ int check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits) {
     return DGM_OK;
 }
 
+
+// ---- dX on bf16 MFMA with the group scale folded into dY ---------------------------
+// dX[m,k] = sum_n dY[m,n] * code[n,k] * S[n, k/G]. For the columns of one
+// 32-wide block (inside one group g), A[m,n] = dY[m,n] * S[n,g] (one fp32
+// rounding, as the reference's code * scale) split into three bf16 pieces
+// hi + mid + lo that sum to it exactly, and B = the codes (integers of at most
+// 8 bits, exact in bf16): three v_mfma_f32_16x16x32_bf16 per 32-n step, the
+// products exact, the sum in fp32. The codes and scales come transposed
+// (codesT [K][N] int8, scalesT [K/G][N]), made once per weight by
+// wt_prep_kernel, so a lane's 8 consecutive n are one 8-byte load.
+// A workgroup owns 16 rows x 32 columns; its 4 waves take interleaved 32-n
+// steps and their partial tiles are added in wave order through LDS.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Three bf16 pieces of 8 values: v = hi + mid + lo exactly (truncation).
+__device__ __forceinline__ void pieces8(const float (&v)[8], bf16x8& hi, bf16x8& mi, bf16x8& lo) {
+    u32x4 h, m, l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float x0 = v[2 * i], x1 = v[2 * i + 1];
+        const float h0 = __uint_as_float(__float_as_uint(x0) & 0xFFFF0000u);
+        const float h1 = __uint_as_float(__float_as_uint(x1) & 0xFFFF0000u);
+        x0 = x0 - h0;
+        x1 = x1 - h1;
+        const float m0 = __uint_as_float(__float_as_uint(x0) & 0xFFFF0000u);
+        const float m1 = __uint_as_float(__float_as_uint(x1) & 0xFFFF0000u);
+        h[i] = pk_bf16(h0, h1);
+        m[i] = pk_bf16(m0, m1);
+        l[i] = pk_bf16(x0 - m0, x1 - m1);
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    mi = __builtin_bit_cast(bf16x8, m);
+    lo = __builtin_bit_cast(bf16x8, l);
+}
+
+__device__ __forceinline__ bf16x8 i8x8_bf16(uint2 w) {
+    u32x4 r;
+    r.x = pk_bf16(float(int8_t(w.x)), float(int8_t(w.x >> 8)));
+    r.y = pk_bf16(float(int8_t(w.x >> 16)), float(int8_t(w.x >> 24)));
+    r.z = pk_bf16(float(int8_t(w.y)), float(int8_t(w.y >> 8)));
+    r.w = pk_bf16(float(int8_t(w.y >> 16)), float(int8_t(w.y >> 24)));
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+struct DxFoldArgs {
+    const float* dY;          // [M, N]
+    const int8_t* codesT;     // [K][N]
+    const float* scalesT;     // [K/G][N]
+    float* out;               // [M, K], or [M, 2K] rows [dgate | dup] with the SwiGLU backward
+    const float *sg_gate, *sg_up;   // [M, K] or null
+    int M, N, K, G;
+};
+
+constexpr int kFoldSteps = 2;   // 32-n steps whose loads are in flight together per wave
+
+__device__ __forceinline__ void dx_fold_tile(const DxFoldArgs& a, int tiles_m, int tiles_k, int per_xcd, int blk,
+                                             float (*part)[2][16][16]) {
+#pragma clang fp contract(off)
+    const int t = (blk & 7) * per_xcd + (blk >> 3);
+    if (t >= tiles_m * tiles_k) return;
+    const int tk = t / tiles_m, tm = t - tk * tiles_m;   // consecutive tiles share a column block
+    const int m0 = tm * 16, k0 = tk * 32, g = k0 / a.G;
+    const int N = a.N, K = a.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const float* yrow = a.dY + size_t(min(m0 + r16, a.M - 1)) * N + 8 * q4;
+    const float* srow = a.scalesT + size_t(g) * N + 8 * q4;
+    const int8_t* c0 = a.codesT + size_t(k0 + r16) * N + 8 * q4;
+    const int8_t* c1 = c0 + size_t(16) * N;
+    f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    const int steps = N / 32;
+    for (int s0 = wave; s0 < steps; s0 += 4 * kFoldSteps) {
+        float4 yv[kFoldSteps][2], sv[kFoldSteps][2];
+        uint2 w0[kFoldSteps], w1[kFoldSteps];
+#pragma unroll
+        for (int u = 0; u < kFoldSteps; ++u) {
+            const int s = min(s0 + 4 * u, steps - 1);   // past the end: re-read, not computed
+            const int n = 32 * s;
+            yv[u][0] = *reinterpret_cast<const float4*>(yrow + n);
+            yv[u][1] = *reinterpret_cast<const float4*>(yrow + n + 4);
+            sv[u][0] = *reinterpret_cast<const float4*>(srow + n);
+            sv[u][1] = *reinterpret_cast<const float4*>(srow + n + 4);
+            w0[u] = *reinterpret_cast<const uint2*>(c0 + n);
+            w1[u] = *reinterpret_cast<const uint2*>(c1 + n);
+        }
+#pragma unroll
+        for (int u = 0; u < kFoldSteps; ++u) {
+            if (s0 + 4 * u >= steps) break;
+            const float v[8] = {yv[u][0].x * sv[u][0].x, yv[u][0].y * sv[u][0].y, yv[u][0].z * sv[u][0].z,
+                                yv[u][0].w * sv[u][0].w, yv[u][1].x * sv[u][1].x, yv[u][1].y * sv[u][1].y,
+                                yv[u][1].z * sv[u][1].z, yv[u][1].w * sv[u][1].w};
+            bf16x8 hi, mi, lo;
+            pieces8(v, hi, mi, lo);
+            const bf16x8 b0 = i8x8_bf16(w0[u]), b1 = i8x8_bf16(w1[u]);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b1, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mi, b0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mi, b1, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b1, acc1, 0, 0, 0);
+        }
+    }
+    // acc_t[r]: row m0 + 4 q4 + r, column k0 + 16 t + r16.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        part[wave][0][4 * q4 + r][r16] = acc0[r];
+        part[wave][1][4 * q4 + r][r16] = acc1[r];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * 32; e += kThreads) {
+        const int il = e >> 5, j = e & 31, tt = j >> 4, jj = j & 15;
+        const int i = m0 + il, k = k0 + j;
+        if (i >= a.M) continue;
+        float v = part[0][tt][il][jj];
+        v += part[1][tt][il][jj];
+        v += part[2][tt][il][jj];
+        v += part[3][tt][il][jj];
+        if (a.sg_gate) {
+            const size_t ei = size_t(i) * K + k;
+            float* o = a.out + size_t(i) * 2 * K + k;
+            dgm::swiglu_bwd_value(a.sg_gate[ei], a.sg_up[ei], v, o[0], o[K]);
+        } else {
+            a.out[size_t(i) * K + k] = v;
+        }
+    }
+}
+
+// dX tiles (dx_fold_tile) beside the paired-column dW tiles (dw_pair_tile).
+__global__ __launch_bounds__(kThreads) void gemm_bwd_fold_pair_kernel(DxFoldArgs ax, int tm, int tk, int per_x,
+                                                                      GemmArgs aw, int tn, int tkw, int per_w) {
+    __shared__ float part[4][2][16][16];
+    const int nx = 8 * per_x;
+    if (int(blockIdx.x) < nx) dx_fold_tile(ax, tm, tk, per_x, int(blockIdx.x), part);
+    else dw_pair_tile(aw, tn, tkw, per_w, int(blockIdx.x) - nx, part);
+}
+
+// codesT[k][n] = code[n][k] (int8, also for int4 codes) and scalesT[g][n] =
+// S[n][g] of one linear, through 64 x 64 LDS tiles. Linears li = 0 .. nlin-1
+// take consecutive runs of workgroups.
+struct WtPrepArgs {
+    const void* W[4];
+    const float* S[4];
+    int8_t* codesT[4];
+    float* scalesT[4];
+    int N[4], K[4], G[4];
+    int first[5];   // first workgroup of each linear
+    int nlin;
+};
+
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void wt_prep_kernel(WtPrepArgs a) {
+    __shared__ int8_t tile[64][64 + 4];
+    int li = 0;
+    while (li + 1 < a.nlin && int(blockIdx.x) >= a.first[li + 1]) ++li;
+    const int N = a.N[li], K = a.K[li], G = a.G[li];
+    const int tiles_n = (N + 63) / 64;
+    const int t = int(blockIdx.x) - a.first[li];
+    const int n0 = (t % tiles_n) * 64, k0 = (t / tiles_n) * 64;
+    const int tid = threadIdx.x;
+    // 64 rows x 64 codes: 16 codes per thread.
+    {
+        const int r = tid >> 2, c = (tid & 3) * 16;
+        const int n = n0 + r;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int k = k0 + c + i;
+            int8_t v = 0;
+            if (n < N && k < K) {
+                if constexpr (BITS == 8) {
+                    v = static_cast<const int8_t*>(a.W[li])[size_t(n) * K + k];
+                } else {
+                    const uint8_t b = static_cast<const uint8_t*>(a.W[li])[(size_t(n) * K + k) >> 1];
+                    const int nib = (k & 1) ? (b >> 4) : (b & 0xF);
+                    v = int8_t(nib >= 8 ? nib - 16 : nib);
+                }
+            }
+            tile[c + i][r] = v;
+        }
+    }
+    __syncthreads();
+    {
+        const int kr = tid >> 2, c = (tid & 3) * 16;
+        const int k = k0 + kr;
+        if (k < K) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int n = n0 + c + i;
+                if (n < N) a.codesT[li][size_t(k) * N + n] = tile[kr][c + i];
+            }
+        }
+    }
+    // scales: the workgroups of the first column block transpose their rows.
+    if (k0 == 0) {
+        const int groups = K / G;
+        for (int e = tid; e < 64 * groups; e += kThreads) {
+            const int gg = e / 64, n = n0 + e % 64;
+            if (n < N) a.scalesT[li][size_t(gg) * N + n] = a.S[li][size_t(n) * groups + gg];
+        }
+    }
+}
+
 }  // namespace
 
 namespace dgm {
@@ -1500,6 +1709,52 @@ int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, c
                            per_w);
     *fused = true;
     return DGM_OK;
+}
+
+// ---- dX on bf16 MFMA beside the fp32 dW tiles (the DiT backward's linears) ---------
+int wt_prep(dgm_gpu* g, int bits, int nlin, const void* const* W, const float* const* S, const int* N, const int* K,
+            int G, int8_t* const* codesT, float* const* scalesT) {
+    if (nlin <= 0 || nlin > 4) return fail(g, DGM_ERR_ARG, "wt_prep: %d linears", nlin);
+    WtPrepArgs a{};
+    a.nlin = nlin;
+    int blocks = 0;
+    for (int i = 0; i < nlin; ++i) {
+        a.W[i] = W[i]; a.S[i] = S[i]; a.codesT[i] = codesT[i]; a.scalesT[i] = scalesT[i];
+        a.N[i] = N[i]; a.K[i] = K[i]; a.G[i] = G;
+        a.first[i] = blocks;
+        blocks += int(ceil_div(N[i], 64) * ceil_div(K[i], 64));
+    }
+    a.first[nlin] = blocks;
+    if (bits == 8) hipLaunchKernelGGL(wt_prep_kernel<8>, dim3(unsigned(blocks)), dim3(kThreads), 0, g->stream, a);
+    else hipLaunchKernelGGL(wt_prep_kernel<4>, dim3(unsigned(blocks)), dim3(kThreads), 0, g->stream, a);
+    return check_launch(g, "wt_prep");
+}
+
+bool bwd_fold_ok(int M, int N, int K, int G) {
+    return M > 0 && M % 64 == 0 && N > 0 && N % 32 == 0 && K > 0 && K % 32 == 0 && G > 0 && G % 32 == 0 &&
+           K % G == 0;
+}
+
+int gemm_bwd_fold(dgm_gpu* g, const int8_t* codesT, const float* scalesT, const float* dY, const float* X, float* dX,
+                  float* dW, int M, int N, int K, int G, bool accumulate, const float* sg_gate, const float* sg_up) {
+    if (!bwd_fold_ok(M, N, K, G) || !aligned(dY, 16) || !aligned(codesT, 8) || !aligned(scalesT, 16))
+        return kNotFused;
+    DxFoldArgs ax{};
+    ax.dY = dY; ax.codesT = codesT; ax.scalesT = scalesT; ax.out = dX; ax.sg_gate = sg_gate; ax.sg_up = sg_up;
+    ax.M = M; ax.N = N; ax.K = K; ax.G = G;
+    GemmArgs aw{};
+    aw.A = dY; aw.B = X; aw.out = dW;
+    aw.M = M; aw.N = N; aw.K = K;
+    aw.rows = N; aw.cols = K; aw.red = M;
+    aw.G = 1; aw.groups = 0;
+    aw.accumulate = accumulate;
+    const int tm = M / 16, tk = K / 32;
+    const int per_x = (tm * tk + 7) / 8;
+    const int tn = int(ceil_div(N, 32)), tkw = int(ceil_div(K, 16));
+    const int per_w = (tn * tkw + 7) / 8;
+    hipLaunchKernelGGL(gemm_bwd_fold_pair_kernel, dim3(unsigned(per_x + per_w) * 8u), dim3(kThreads), 0, g->stream, ax,
+                       tm, tk, per_x, aw, tn, tkw, per_w);
+    return check_launch(g, "gemm_bwd_fold");
 }
 
 int gemm_check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits) {

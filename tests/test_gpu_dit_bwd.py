@@ -140,6 +140,16 @@ def test_c3_block_backward(gpu, dgm, orc):
     _check_block(blk, dgm, xg, gg, xo, gx, gw, gn)
 
 
+@pytest.mark.parametrize("B,bits,loops", [(2, 4, 2), (3, 8, 1)])
+def test_c3_shape_block_backward(gpu, dgm, orc, B, bits, loops):
+    """The c3 block shape at other batch sizes, loop counts and int4 linears
+    (the three-launch forward, the one-launch attention backward and the
+    bf16-dX weight backward)."""
+    cfg = dgm.DiTConfig(B=B, bits=bits, loops=loops)
+    blk, xg, gg, xo, gx, gw, gn, _ = _run_block(gpu, dgm, orc, cfg, 600 + B)
+    _check_block(blk, dgm, xg, gg, xo, gx, gw, gn)
+
+
 @pytest.mark.parametrize("bits,group", [(32, 8), (8, 16), (4, 16), (8, 32), (4, 32)])
 def test_small_block_backward(gpu, dgm, orc, bits, group):
     cfg = dgm.DiTConfig(B=2, T=16, C=64, F=128, H=4, D=16, loops=3, group=group, bits=bits)
