@@ -1217,7 +1217,10 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     // dX on bf16 MFMA (gemm_bwd_fold) for the stacked linears: their codes
     // and scales transposed once here.
     int fnk[4][2];
-    const bool fold = qkv1 && gu1 && fold_shapes(c, fnk) && dgm::aligned(ws, 16);
+    const size_t calign = bits == 8 ? 16 : 8;
+    const bool fold = qkv1 && gu1 && fold_shapes(c, fnk) && dgm::aligned(ws, 16) && dgm::aligned(w->wq.q, calign) &&
+                      dgm::aligned(w->wo.q, calign) && dgm::aligned(w->wgate.q, calign) &&
+                      dgm::aligned(w->wdown.q, calign);
     const int8_t* fct[4] = {};
     const float* fst[4] = {};
     if (fold) {

@@ -1481,7 +1481,7 @@ struct WtPrepArgs {
 
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void wt_prep_kernel(WtPrepArgs a) {
-    __shared__ int8_t tile[64][64 + 4];
+    __shared__ __align__(16) int8_t tile[64][64 + 16];
     int li = 0;
     while (li + 1 < a.nlin && int(blockIdx.x) >= a.first[li + 1]) ++li;
     const int N = a.N[li], K = a.K[li], G = a.G[li];
@@ -1489,37 +1489,38 @@ __global__ __launch_bounds__(kThreads) void wt_prep_kernel(WtPrepArgs a) {
     const int t = int(blockIdx.x) - a.first[li];
     const int n0 = (t % tiles_n) * 64, k0 = (t / tiles_n) * 64;
     const int tid = threadIdx.x;
-    // 64 rows x 64 codes: 16 codes per thread.
+    const int r = tid >> 2, c = (tid & 3) * 16;   // row r, codes c .. c+15 of the tile
+    // 64 rows x 64 codes: one 16-byte (int8) / 8-byte (int4) load per thread
+    // (K % 32 == 0: a run of 16 lies wholly inside or outside the matrix).
     {
-        const int r = tid >> 2, c = (tid & 3) * 16;
-        const int n = n0 + r;
+        const int n = n0 + r, k = k0 + c;
+        uint32_t wv[4] = {0u, 0u, 0u, 0u};
+        if (n < N && k < K) {
+            if constexpr (BITS == 8) {
+                const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.W[li]) + size_t(n) * K + k);
+                wv[0] = q.x; wv[1] = q.y; wv[2] = q.z; wv[3] = q.w;
+            } else {
+                const uint2 q =
+                    *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.W[li]) + ((size_t(n) * K + k) >> 1));
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int k = k0 + c + i;
-            int8_t v = 0;
-            if (n < N && k < K) {
-                if constexpr (BITS == 8) {
-                    v = static_cast<const int8_t*>(a.W[li])[size_t(n) * K + k];
-                } else {
-                    const uint8_t b = static_cast<const uint8_t*>(a.W[li])[(size_t(n) * K + k) >> 1];
-                    const int nib = (k & 1) ? (b >> 4) : (b & 0xF);
-                    v = int8_t(nib >= 8 ? nib - 16 : nib);
+                for (int h = 0; h < 2; ++h) {   // 8 nibbles (low first) -> 8 sign-extended bytes
+                    const uint32_t x = h ? q.y : q.x;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t b = uint32_t(int32_t(x << (28 - 4 * j)) >> 28) & 0xFFu;
+                        wv[2 * h + j / 4] |= b << (8 * (j % 4));
+                    }
                 }
             }
-            tile[c + i][r] = v;
         }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tile[c + i][r] = int8_t(wv[i / 4] >> (8 * (i % 4)));
     }
     __syncthreads();
     {
-        const int kr = tid >> 2, c = (tid & 3) * 16;
-        const int k = k0 + kr;
-        if (k < K) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int n = n0 + c + i;
-                if (n < N) a.codesT[li][size_t(k) * N + n] = tile[kr][c + i];
-            }
-        }
+        const int k = k0 + r, n = n0 + c;   // row k of the transpose, n .. n+15 (N % 32 == 0)
+        if (k < K && n < N)
+            *reinterpret_cast<uint4*>(a.codesT[li] + size_t(k) * N + n) = *reinterpret_cast<const uint4*>(&tile[r][c]);
     }
     // scales: the workgroups of the first column block transpose their rows.
     if (k0 == 0) {
@@ -1715,6 +1716,9 @@ int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, c
 int wt_prep(dgm_gpu* g, int bits, int nlin, const void* const* W, const float* const* S, const int* N, const int* K,
             int G, int8_t* const* codesT, float* const* scalesT) {
     if (nlin <= 0 || nlin > 4) return fail(g, DGM_ERR_ARG, "wt_prep: %d linears", nlin);
+    for (int i = 0; i < nlin; ++i)
+        if (N[i] % 32 != 0 || K[i] % 32 != 0 || !aligned(W[i], bits == 8 ? 16 : 8) || !aligned(codesT[i], 16))
+            return fail(g, DGM_ERR_UNSUPPORTED, "wt_prep: sizes or alignment");
     WtPrepArgs a{};
     a.nlin = nlin;
     int blocks = 0;
