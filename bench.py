@@ -199,16 +199,27 @@ def load_traffic() -> dict:
     return {}
 
 
-def traffic_for(workload: str, kernel_keys) -> object:
+def traffic_for(workload: str, kernel_keys, per_call: str = "") -> object:
     """Counted HBM bytes per call: the sum over the call's kernels (names
-    matched by substring), or None when the workload was not profiled."""
+    matched by substring), or None when the workload was not profiled. With
+    per_call naming a kernel that runs exactly once per call, each kernel's
+    bytes per launch are weighted by its launches per call (its dispatches
+    over that kernel's); without it every matched kernel counts once."""
     ent = load_traffic().get(workload, {})
-    total, found = 0, False
-    for name, rec in ent.items():   # every kernel of the call once
-        if name != "_calibration" and any(key in name for key in kernel_keys):
-            total += rec.get("total_bytes", 0)
-            found = True
-    return total if found else None
+    kern = {n: r for n, r in ent.items() if n != "_calibration" and any(key in n for key in kernel_keys)}
+    if not kern:
+        return None
+    calls = None
+    if per_call:
+        once = [r for n, r in kern.items() if per_call in n]
+        if len(once) != 1 or not once[0].get("dispatches"):
+            return None
+        calls = once[0]["dispatches"]
+    total = 0.0
+    for rec in kern.values():
+        weight = rec.get("dispatches", 0) / calls if calls else 1.0
+        total += rec.get("total_bytes", 0) * weight
+    return round(total)
 
 
 # ---- the reference's scalar CPU path, one core ---------------------------------
@@ -433,6 +444,11 @@ def bench_c1(b: Bench, reps: int, cpu: bool) -> dict:
     return out
 
 
+# Kernels of one c3 forward (dit_loop.hip) and of the block backward.
+C3_FWD_KERNELS = ["loop_row_kernel", "loop_attn_kernel", "loop_mlp_kernel", "loop_tail_kernel"]
+C3_BWD_KERNELS = ["rms_bwd", "gemm_bwd", "loop_attn_bwd_kernel", "wt_prep_kernel", "acc_kernel"]
+
+
 def c3_flops(cfg) -> int:
     """Linear + attention flop of the looped block forward (src/DiT.swift:520-550)."""
     M, C, F, KV, T, H, D = cfg.B * cfg.T, cfg.C, cfg.F, cfg.D, cfg.T, cfg.H, cfg.D
@@ -493,9 +509,9 @@ def bench_c3(b: Bench, reps: int, cpu: bool) -> dict:
            "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
            "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
            "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
-                                traffic_for("c3", ["dit_gemm_kernel", "attn_mfma_kernel", "gemm_fwd", "row_fuse"])),
-           "note": "launch/latency-bound: ~2.3 GFLOP and ~0.6 MB of weights per forward; traffic = sum over "
-                   "the forward's kernels"}
+                                traffic_for("c3", C3_FWD_KERNELS, "loop_tail_kernel")),
+           "note": "launch/latency-bound: ~2.3 GFLOP and ~0.6 MB of weights per forward; traffic = the "
+                   "forward's 13 launches (three per loop and the tail), each at its counted bytes"}
     if cpu:
         out["cpu_baseline"] = _cpu_dit(cfg, False, 3.0)
     return out
@@ -525,8 +541,10 @@ def bench_c3_train(b: Bench, reps: int, cpu: bool) -> dict:
            "shape": "B=8 T=64 C=192 F=768 H=4 D=48 int8 G=32",
            "us": round(ms * 1e3, 3), "tokens_per_s": round(tokens / (ms * 1e-3), 1),
            "TFLOPs": round(flops / ms / 1e9, 3), "flop": flops,
-           "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma"),
-           "note": "launch/latency-bound; x and dL/dx are reused in place across the timed steps"}
+           "roofline": roofline(flops / ms / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
+                                traffic_for("c3_train", C3_FWD_KERNELS + C3_BWD_KERNELS, "wt_prep_kernel")),
+           "note": "launch/latency-bound; x and dL/dx are reused in place across the timed steps; traffic = "
+                   "every launch of one step at its counted bytes"}
     if cpu:
         out["cpu_baseline"] = _cpu_dit(cfg, True, 4.0)
     return out
@@ -763,7 +781,8 @@ def traffic(name: str, fetch_dir: str, write_dir: str) -> dict:
             continue
         fb = fetch[k] * 1024.0 * f_scale
         wb = write.get(k, 0.0) * 1024.0 * w_scale
-        rec[k] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "total_bytes": round(fb + wb)}
+        rec[k] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "total_bytes": round(fb + wb),
+                  "dispatches": len(fv[k])}
     allt = load_traffic()
     allt[name] = rec
     os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
