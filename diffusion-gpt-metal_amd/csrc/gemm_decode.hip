@@ -19,6 +19,10 @@
 // MFMA's fp32 accumulation; the block partial is rescaled exactly by 2^-e
 // before the group scale.
 //
+// Reduced-precision int4 instead takes bf16(x) with its own exponent (no
+// factor) against the codes entered as 128 + (code + 8), exact in bf16; the
+// offset 136 leaves inside each block's fp32 partial (see below).
+//
 // Two kernels:
 //  * M <= 16 (decode_small_kernel, further down): one launch; every
 //    workgroup converts the activations it needs in registers.
@@ -26,7 +30,12 @@
 //    fragment-major: for each MFMA step (32 k), row tile and piece, the 64
 //    lanes' 16-byte A fragments form one contiguous 1 KB, so every activation
 //    load is a whole-line 1 KB read. A row block holding a non-finite value
-//    is stored as NaN, so that output row is NaN.
+//    is stored as NaN, so that output row is NaN (bf16: the value itself;
+//    an infinity meets the offset term's opposite infinity and gives NaN).
+//    For bf16 the prepare pass also writes, per (block, row), the fp32 term
+//    -136 * sum of the block's bf16(x); a block's MFMA chain starts from it,
+//    so the offset is removed before the group scale, exactly whenever the
+//    sums are exact (one-hot or small-integer activations).
 //
 // Weights (both kernels). A workgroup owns 64 whole rows of W (64 output
 // columns) and all of K; its compute waves split K, so each weight is
@@ -67,7 +76,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int DEC_COLS = 64;                 // W rows (output columns) per workgroup
 constexpr int DEC_SLOTS = 4;                 // intervals (4 chunks each) in the weight ring
 constexpr int DEC_CHUNK = DEC_COLS * 128;    // bytes of one chunk (64 rows x 128 B)
-constexpr int DEC_THREADS = 320;             // 4 compute waves + the weight-stream wave
+constexpr int DEC_KW = 4;                    // compute waves splitting K
 constexpr int DEC_LDS = DEC_SLOTS * 4 * DEC_CHUNK;   // 128 KB
 
 template <int BITS>
@@ -97,9 +106,16 @@ __host__ __device__ constexpr int frag_k(int q, int kk, int t) {
 // One wave per (row tile, block): lane (q = lane / 16, c = lane % 16) owns
 // row 16 mt + c and the KL consecutive k of lane group q, i.e. exactly the
 // elements of its own fragments for the SPB steps of the block.
+//
+// Reduced-precision int4 (BITS 4, one piece) takes bf16 instead: the
+// fragments hold bf16(x) (own exponent, no block factor), and in place of
+// the exponents the prepare pass writes, per (block, row), the fp32 term
+// -136 * sum over the block of bf16(x): the GEMM feeds the codes as
+// 128 + (code + 8), exact in bf16, and this term removes the offset 136.
 template <int BITS, int P>
 __global__ __launch_bounds__(256) void decode_prep_kernel(const float* __restrict__ X, _Float16* __restrict__ XP,
-                                                          int8_t* __restrict__ ex, int M, int K, int MT) {
+                                                          int8_t* __restrict__ ex, float* __restrict__ corr, int M,
+                                                          int K, int MT) {
     using SH = DecShape<BITS>;
     const int nblk = K / SH::KB;
     const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -118,6 +134,30 @@ __global__ __launch_bounds__(256) void decode_prep_kernel(const float* __restric
     } else {
 #pragma unroll
         for (int i = 0; i < SH::KL; ++i) v[i] = 0.0f;
+    }
+    if constexpr (BITS == 4 && P == 1) {
+        // bf16 fragments and the offset term. The sum runs in k order within
+        // a lane, then over the four lane groups in a fixed tree: every lane
+        // of the row gets the same bits.
+        float sum = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < SH::SPB; ++kk) {
+            uint32_t o[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const __bf16 lo = __bf16(v[frag_k<BITS>(0, kk, 2 * d)]);
+                const __bf16 hi = __bf16(v[frag_k<BITS>(0, kk, 2 * d + 1)]);
+                o[d] = uint32_t(__builtin_bit_cast(uint16_t, lo)) | (uint32_t(__builtin_bit_cast(uint16_t, hi)) << 16);
+            }
+            const int s = blk * SH::SPB + kk;
+            *reinterpret_cast<u32x4*>(XP + (size_t(s) * MT + mt) * 512 + lane * 8) = u32x4{o[0], o[1], o[2], o[3]};
+        }
+#pragma unroll
+        for (int i = 0; i < SH::KL; ++i) sum += float(__bf16(v[i]));
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        if (q == 0) corr[size_t(blk) * (16 * MT) + row] = -136.0f * sum;
+        return;
     }
     // Block maximum of the row: the four lanes q share row c.
     float mx = 0.0f;
@@ -176,7 +216,8 @@ struct DecArgs {
     const uint8_t* W;      // codes; row stride rowb bytes
     const float* S;        // scales [N, groups]
     const _Float16* XP;    // fragment-major pieces
-    const int8_t* ex;      // exponents [blocks][16 MT]
+    const int8_t* ex;      // exponents [blocks][16 MT] (f16 pieces)
+    const float* corr;     // offset terms [blocks][16 MT] (bf16 path)
     const float* bias;
     float* Y;
     int M, N, K, groups, gshift, rowb, nchunk, has_bias;
@@ -193,7 +234,8 @@ struct DecArgs {
 template <int BITS, int MT, int P, int D>
 struct Schedule {
     using SH = DecShape<BITS>;
-    static constexpr int NA = 4 + MT;    // block loads
+    static constexpr bool BF = BITS == 4 && P == 1;
+    static constexpr int NA = 4 + MT;    // block loads: 4 scales, MT exponent or offset-term loads
     static constexpr int issued(int i) { return MT * P + ((i + D) % SH::SPB == 0 ? NA : 0); }
     static constexpr int wait(int i) {     // vmcnt before computing step position i
         int n = 0;
@@ -248,15 +290,21 @@ __device__ __forceinline__ bf16x8 codes_to_bf16_off(uint32_t dw) {
     return __builtin_bit_cast(bf16x8, o);
 }
 
-// Five waves: waves 0-3 compute (wave w takes chunks w, w + 4, ...: interval
-// t holds chunks 4t .. 4t + 3), wave 4 streams the weight chunks into a ring
-// of DEC_SLOTS intervals (DEC_SLOTS - 1 intervals ahead). One barrier per
-// interval: interval t is in LDS and every compute wave is done with
-// interval t - 1, whose slot the producer then refills.
-template <int BITS, int MT, int P, int D>
-__global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
+// 4 MW + 1 waves: compute wave w takes chunks kw, kw + 4, ... (kw = w % 4;
+// interval t holds chunks 4t .. 4t + 3) for row tiles MT mh .. MT mh + MT - 1
+// (mh = w / 4); wave 4 MW streams the weight chunks into a ring of DEC_SLOTS
+// intervals (DEC_SLOTS - 1 intervals ahead). With MW = 2 two compute waves
+// share each SIMD and convert the same codes for different rows: one wave's
+// conversions and waits run beside the other's MFMAs, and each wave keeps
+// half the accumulators, which leaves registers for a deeper activation
+// prefetch. One barrier per interval: interval t is in LDS and every compute
+// wave is done with interval t - 1, whose slot the producer then refills.
+template <int BITS, int MT, int P, int D, int MW>
+__global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecArgs a) {
     using SH = DecShape<BITS>;
     using SC = Schedule<BITS, MT, P, D>;
+    constexpr bool BF = SC::BF;   // reduced-precision int4: bf16 fragments, offset codes
+    using XF = std::conditional_t<BF, bf16x8, f16x8>;
     static_assert(D >= 1 && D <= SH::SPB, "prefetch depth: at most one block ahead");
     // Activation ring: XR step slots, a power of two above D dividing SPC, so
     // that the slot of step s0 + i (s0 a chunk start) is i % XR.
@@ -275,7 +323,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
     const int rot = a.nchunk % 4 == 0 ? int(blockIdx.x % unsigned(T)) : 0;
     auto iv = [&](int t) { return (t + rot) % T; };
 
-    if (w == 4) {
+    if (w == DEC_KW * MW) {
         // ---- producer. Instruction i of a chunk covers rows 8i .. 8i+7;
         // lane l lands at slot l % 8 of row 8i + l / 8 and fetches the
         // piece that belongs there. Rows past N re-read row N - 1; chunks
@@ -307,16 +355,22 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
 #pragma clang diagnostic pop
             }
         };
-#pragma unroll
-        for (int t = 0; t < DEC_SLOTS - 1; ++t) dma_interval(t);
+        static_assert(DEC_SLOTS == 4, "the waits below count at most two intervals ahead");
+        for (int t = 0; t < DEC_SLOTS - 1 && t < T; ++t) dma_interval(t);
         for (int t = 0; t < T; ++t) {
-            // Interval t has landed: DEC_SLOTS - 2 newer intervals (64 loads)
-            // may be in flight; the counter holds at most 63, so this also
-            // waits for the first load of interval t + 1.
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(32 * (DEC_SLOTS - 2) < 63 ? 32 * (DEC_SLOTS - 2) : 63)
-                         : "memory");
+            // Interval t has landed once at most `ahead` newer intervals (32
+            // loads each, issued after it) are in flight; no interval past T
+            // is ever issued. The counter holds at most 63, so with two ahead
+            // this also waits for the first load of interval t + 1.
+            const int ahead = min(T - 1 - t, DEC_SLOTS - 2);
+            if (ahead >= 2)
+                asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
+            else if (ahead == 1)
+                asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            dma_interval(t + DEC_SLOTS - 1);
+            if (t + DEC_SLOTS - 1 < T) dma_interval(t + DEC_SLOTS - 1);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();   // the ring is quiet: the partials may overwrite it
@@ -324,43 +378,56 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
         return;
     }
 
-    // ---- compute wave w: chunks w + 4t, SPC steps each.
-    const int cnt = a.nchunk > w ? (a.nchunk - w + 3) / 4 : 0;
+    // ---- compute wave w: chunks kw + 4t, SPC steps each, row tiles
+    // tile0 .. tile0 + MT - 1 of the prepared pieces.
+    const int kw = w % DEC_KW, mh = w / DEC_KW;
+    const int tile0 = a.mt0 + mh * MT;
+    const int cnt = a.nchunk > kw ? (a.nchunk - kw + 3) / 4 : 0;
     const int nsteps = cnt * SH::SPC;
 
-    f16x8 xa[XR][MT][P];
+    XF xa[XR][MT][P];
     const uint32_t xlane = uint32_t(lane) * 16u;
     auto load_x = [&](int s, int slot) {   // this wave's step s (clamped)
         const int ss = s < nsteps ? s : nsteps - 1;
-        const int gstep = (w + 4 * iv(ss / SH::SPC)) * SH::SPC + ss % SH::SPC;
+        const int gstep = (kw + 4 * iv(ss / SH::SPC)) * SH::SPC + ss % SH::SPC;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int p = 0; p < P; ++p)
                 asm volatile("global_load_dwordx4 %0, %1, %2"
                              : "=v"(xa[slot][mt][p])
-                             : "v"(((uint32_t(gstep) * a.mtp + a.mt0 + mt) * P + p) * 1024u + xlane), "s"(a.XP));
+                             : "v"(((uint32_t(gstep) * a.mtp + tile0 + mt) * P + p) * 1024u + xlane), "s"(a.XP));
     };
-    // Block loads: scales of the lane's 4 columns and exponents of its rows
-    // 16 mt + 4 q .. +3 (one dword per row tile). With D <= SPB at most the
-    // next block is in flight, so two slots (block b in slot b & 1; a chunk
-    // holds blocks 2j and 2j + 1).
+    // Block loads: scales of the lane's 4 columns, and for its rows
+    // 16 mt + 4 q .. +3 the exponents (f16 pieces: one dword per row tile) or
+    // the offset terms (bf16: one 16-byte load per row tile). With D <= SPB
+    // at most the next block is in flight, so two slots (block b in slot
+    // b & 1; a chunk holds blocks 2j and 2j + 1).
     float bs[2][4];
-    uint32_t be[2][MT];
+    uint32_t be[2][BF ? 1 : MT];
+    f32x4 bc[2][BF ? MT : 1];
     auto load_blk = [&](int b, int slot) {   // this wave's block b (clamped)
         const int bb = b < 2 * cnt ? b : 2 * cnt - 1;
-        const int gblk = 2 * (w + 4 * iv(bb >> 1)) + (bb & 1);
+        const int gblk = 2 * (kw + 4 * iv(bb >> 1)) + (bb & 1);
         const uint32_t g = uint32_t(gblk) >> a.gshift;
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
             const uint32_t n = uint32_t(min(n0 + 16 * ct + c, a.N - 1));
             asm volatile("global_load_dword %0, %1, %2" : "=v"(bs[slot][ct]) : "v"((n * a.groups + g) * 4u), "s"(a.S));
         }
+        if constexpr (BF) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            asm volatile("global_load_dword %0, %1, %2"
-                         : "=v"(be[slot][mt])
-                         : "v"(uint32_t(gblk) * (16u * a.mtp) + 16u * (a.mt0 + mt) + 4u * q), "s"(a.ex));
+            for (int mt = 0; mt < MT; ++mt)
+                asm volatile("global_load_dwordx4 %0, %1, %2"
+                             : "=v"(bc[slot][mt])
+                             : "v"((uint32_t(gblk) * (16u * a.mtp) + 16u * (tile0 + mt) + 4u * q) * 4u), "s"(a.corr));
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                asm volatile("global_load_dword %0, %1, %2"
+                             : "=v"(be[slot][mt])
+                             : "v"(uint32_t(gblk) * (16u * a.mtp) + 16u * (tile0 + mt) + 4u * q), "s"(a.ex));
+        }
     };
 
     f32x4 acc[MT][4], tmp[MT][4];
@@ -381,7 +448,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
     for (int j = 0; j < T; ++j) {
         __syncthreads();   // interval j is in LDS
         if (j >= cnt) continue;
-        const uint8_t* cs = smem + ((j % DEC_SLOTS) * 4 + w) * DEC_CHUNK;
+        const uint8_t* cs = smem + ((j % DEC_SLOTS) * 4 + kw) * DEC_CHUNK;
         const int s0 = j * SH::SPC;
 #pragma unroll
         for (int i = 0; i < SH::SPC; ++i) {
@@ -397,6 +464,12 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
                 for (int p = 0; p < P; ++p) asm volatile("" : "+v"(xa[slot][mt][p]));
 
             const int kk = i % SH::SPB, hb = i / SH::SPB;   // step in block, block in chunk
+            if constexpr (BF) {
+                if (kk == 0) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) asm volatile("" : "+v"(bc[hb][mt]));
+                }
+            }
             if (kk == 0) {
                 // The block's code pieces: row 16 ct + c, piece 4 hb + q.
 #pragma unroll
@@ -409,38 +482,62 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
             // B fragments of this step and the MFMAs.
 #pragma unroll
             for (int ct = 0; ct < 4; ++ct) {
-                f16x2 h[4];
-                if constexpr (BITS == 4) {
-                    codes_to_f16<4>(wc[ct][kk], h);
+                if constexpr (BF) {
+                    // A block's partial starts from its offset term: the
+                    // offset leaves inside the fp32 accumulation, before the
+                    // scale (exact when the activations are small integers).
+                    const bf16x8 b = codes_to_bf16_off(wc[ct][kk]);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const f32x4 t0 = kk == 0 ? bc[hb][mt] : tmp[mt][ct];
+                        tmp[mt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[slot][mt][0], b, t0, 0, 0, 0);
+                    }
                 } else {
-                    codes_to_f16<8>(wc[ct][2 * kk], h);
-                    codes_to_f16<8>(wc[ct][2 * kk + 1], h + 2);
-                }
-                const f16x8 b = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+                    f16x2 h[4];
+                    if constexpr (BITS == 4) {
+                        codes_to_f16<4>(wc[ct][kk], h);
+                    } else {
+                        codes_to_f16<8>(wc[ct][2 * kk], h);
+                        codes_to_f16<8>(wc[ct][2 * kk + 1], h + 2);
+                    }
+                    const f16x8 b = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    f32x4 t0 = kk == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : tmp[mt][ct];
+                    for (int mt = 0; mt < MT; ++mt) {
+                        f32x4 t0 = kk == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : tmp[mt][ct];
 #pragma unroll
-                    for (int p = 0; p < P; ++p)
-                        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[slot][mt][p], b, t0, 0, 0, 0);
-                    tmp[mt][ct] = t0;
+                        for (int p = 0; p < P; ++p)
+                            t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[slot][mt][p], b, t0, 0, 0, 0);
+                        tmp[mt][ct] = t0;
+                    }
                 }
             }
             if (kk == SH::SPB - 1) {
-                // Block done: acc += (partial * 2^-e) * scale, per row.
                 const int bslot = (i / SH::SPB) & 1;
                 asm volatile("" : "+v"(bs[bslot][0]), "+v"(bs[bslot][1]), "+v"(bs[bslot][2]), "+v"(bs[bslot][3]));
+                if constexpr (BF) {
+                    // Block done: acc += partial * scale.
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    asm volatile("" : "+v"(be[bslot][mt]));
-                    const uint32_t e4 = be[bslot][mt];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        // 2^-e as an fp32 bit pattern (|e| <= 127: a normal power of two).
-                        const float inv = __builtin_bit_cast(float, uint32_t(127 - int(int8_t(e4 >> (8 * r)))) << 23);
+                    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                         for (int ct = 0; ct < 4; ++ct)
-                            acc[mt][ct][r] = __builtin_fmaf(tmp[mt][ct][r] * inv, bs[bslot][ct], acc[mt][ct][r]);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                acc[mt][ct][r] = __builtin_fmaf(tmp[mt][ct][r], bs[bslot][ct], acc[mt][ct][r]);
+                } else {
+                    // Block done: acc += (partial * 2^-e) * scale, per row.
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        asm volatile("" : "+v"(be[bslot][mt]));
+                        const uint32_t e4 = be[bslot][mt];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            // 2^-e as an fp32 bit pattern (|e| <= 127: a normal power of two).
+                            const float inv =
+                                __builtin_bit_cast(float, uint32_t(127 - int(int8_t(e4 >> (8 * r)))) << 23);
+#pragma unroll
+                            for (int ct = 0; ct < 4; ++ct)
+                                acc[mt][ct][r] = __builtin_fmaf(tmp[mt][ct][r] * inv, bs[bslot][ct], acc[mt][ct][r]);
+                        }
                     }
                 }
             }
@@ -459,30 +556,41 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void decode_kernel(DecArgs a) {
     for (int sl = 0; sl < 2; ++sl) {
         asm volatile("" : "+v"(bs[sl][0]), "+v"(bs[sl][1]), "+v"(bs[sl][2]), "+v"(bs[sl][3]));
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) asm volatile("" : "+v"(be[sl][mt]));
+        for (int mt = 0; mt < MT; ++mt) {
+            if constexpr (BF)
+                asm volatile("" : "+v"(bc[sl][mt]));
+            else
+                asm volatile("" : "+v"(be[sl][mt]));
+        }
     }
-
-    // ---- the four waves' partials, summed in a fixed order.
+    // ---- the four K parts' partials, summed in a fixed order. Layout
+    // [kw][column][16 MT MW rows + 4 pad]: a lane's four rows of one column
+    // are one 16-byte store, and the padded column stride (16 MT MW + 4
+    // floats) puts 16 consecutive columns on 16 distinct 16-byte bank groups.
+    constexpr int RP = 16 * MT * MW + 4;
+    static_assert(DEC_KW * 64 * RP * 4 <= DEC_LDS, "partials fit the ring");
     __syncthreads();   // the producer's last loads have landed
-    float* red = reinterpret_cast<float*>(smem);   // [4][16 MT][64]
+    float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) red[(w * 16 * MT + 16 * mt + 4 * q + r) * 64 + 16 * ct + c] = acc[mt][ct][r];
+            *reinterpret_cast<f32x4*>(red + (kw * 64 + 16 * ct + c) * RP + 16 * (mh * MT + mt) + 4 * q) = acc[mt][ct];
     __syncthreads();
-    const int rows = min(a.M - 16 * a.mt0, 16 * MT);
-    for (int idx = threadIdx.x; idx < rows * 64; idx += 256) {
-        const int m = idx >> 6, col = idx & 63;
+    const int rows = min(a.M - 16 * a.mt0, 16 * MT * MW);
+    for (int idx = threadIdx.x; idx < ((rows + 3) / 4) * 64; idx += 64 * DEC_KW * MW) {
+        const int m4 = idx >> 6, col = idx & 63;
         const int n = n0 + col;
         if (n >= a.N) continue;
-        float y = red[(0 * 16 * MT + m) * 64 + col];
-        y += red[(1 * 16 * MT + m) * 64 + col];
-        y += red[(2 * 16 * MT + m) * 64 + col];
-        y += red[(3 * 16 * MT + m) * 64 + col];
-        if (a.has_bias) y += a.bias[n];
-        a.Y[size_t(16 * a.mt0 + m) * a.N + n] = y;
+        f32x4 y = *reinterpret_cast<const f32x4*>(red + (0 * 64 + col) * RP + 4 * m4);
+#pragma unroll
+        for (int v = 1; v < 4; ++v) y += *reinterpret_cast<const f32x4*>(red + (v * 64 + col) * RP + 4 * m4);
+        const float bv = a.has_bias ? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * m4 + r;
+            if (m < rows) a.Y[size_t(16 * a.mt0 + m) * a.N + n] = a.has_bias ? y[r] + bv : y[r];
+        }
     }
 }
 
@@ -841,15 +949,15 @@ int launch_decode_small(dgm_gpu* g, const DecArgs& a, const float* X) {
     return DGM_OK;
 }
 
-template <int BITS, int MT, int P, int D>
+template <int BITS, int MT, int P, int D, int MW = 1>
 int launch_decode(dgm_gpu* g, const DecArgs& a) {
-    auto kern = decode_kernel<BITS, MT, P, D>;
+    auto kern = decode_kernel<BITS, MT, P, D, MW>;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, DEC_LDS);
     if (e != hipSuccess)
         return dgm::fail(g, DGM_ERR_HIP, "decode: cannot reserve %d bytes of LDS: %s", DEC_LDS, hipGetErrorString(e));
-    hipLaunchKernelGGL(kern, dim3(unsigned((a.N + DEC_COLS - 1) / DEC_COLS)), dim3(DEC_THREADS), DEC_LDS, g->stream,
-                       a);
+    hipLaunchKernelGGL(kern, dim3(unsigned((a.N + DEC_COLS - 1) / DEC_COLS)), dim3(64 * (DEC_KW * MW + 1)), DEC_LDS,
+                       g->stream, a);
     return DGM_OK;
 }
 
@@ -859,30 +967,43 @@ bool small_ok(int M, int K, int groups) {
     return M <= 16 && groups <= DS_SMAX / 256 && int64_t(M) * K * 4 < (int64_t(1) << 32);
 }
 
+// Reduced-precision int4 (bf16 fragments) keeps up to four row tiles in one
+// group of compute waves; the other modes take three or four row tiles as two
+// groups of two (two compute waves per SIMD), with the prefetch depth each
+// fits in its register budget.
+template <int BITS, int P>
+constexpr bool DEC_ONE_GROUP = BITS == 4 && P == 1;
+template <int BITS, int P>
+constexpr int DEC_D2 = P == 2 ? 1 : 2;
+
 template <int BITS, int P>
 int decode_dispatch(dgm_gpu* g, DecArgs& a, const float* X) {
     using SH = DecShape<BITS>;
     if (small_ok(a.M, a.K, a.groups)) return launch_decode_small<BITS, P>(g, a, X);
-    const int MT = (a.M + 15) / 16;
+    // Row tiles of the prepared pieces: for the two-group kernel three are
+    // padded to four (zero rows), which it covers as 2 x 2.
+    const int MT = (a.M <= 32 || DEC_ONE_GROUP<BITS, P>) ? (a.M + 15) / 16 : 4;
     const int nblk = a.K / SH::KB;
     const size_t xp_bytes = size_t(nblk) * SH::SPB * MT * P * 1024;
-    const size_t ex_bytes = size_t(nblk) * 16 * MT;
+    // Exponents (int8) or, on the bf16 path, offset terms (fp32) per (block, row).
+    const size_t ex_bytes = size_t(nblk) * 16 * MT * ((BITS == 4 && P == 1) ? 4 : 1);
     uint8_t* ws = static_cast<uint8_t*>(dgm::workspace(g, xp_bytes + ex_bytes + 256));
     if (!ws) return dgm::ws_error(g);
     _Float16* xp = reinterpret_cast<_Float16*>(ws);
     int8_t* ex = reinterpret_cast<int8_t*>(ws + xp_bytes);
+    float* corr = reinterpret_cast<float*>(ws + xp_bytes);
     const unsigned jobs = unsigned(MT * nblk);
-    hipLaunchKernelGGL((decode_prep_kernel<BITS, P>), dim3((jobs + 3) / 4), dim3(256), 0, g->stream, X, xp, ex, a.M,
-                       a.K, MT);
+    hipLaunchKernelGGL((decode_prep_kernel<BITS, P>), dim3((jobs + 3) / 4), dim3(256), 0, g->stream, X, xp, ex, corr,
+                       a.M, a.K, MT);
     a.XP = xp;
     a.ex = ex;
+    a.corr = corr;
     a.mtp = MT;
     a.mt0 = 0;
-    // Prefetch depth: as many activation steps in flight as the block
-    // registers allow (at most one block ahead); fewer for the larger row
-    // counts, whose steps are longer and whose fragments take more registers.
-    // Every variant must fit 256 registers without spilling (two waves share
-    // a SIMD): a spilled register whose hand-waited load is still in flight
+    // Prefetch depth: as many activation steps in flight as the registers
+    // allow (at most one block ahead). Every variant must fit its register
+    // budget without spilling (256 with one compute wave per SIMD, 168 with
+    // two): a spilled register whose hand-waited load is still in flight
     // would be copied before it holds the data. build.py checks this.
     constexpr int SPB = SH::SPB;
     switch (MT) {
@@ -890,17 +1011,10 @@ int decode_dispatch(dgm_gpu* g, DecArgs& a, const float* X) {
         case 2: return launch_decode<BITS, 2, P, (SPB > 2 ? SPB / 2 : 1)>(g, a);
         default: break;
     }
-    if constexpr (P == 1 && BITS == 4) {
-        return MT == 3 ? launch_decode<BITS, 3, 1, 2>(g, a) : launch_decode<BITS, 4, 1, 2>(g, a);
-    } else {
-        // Three or four row tiles with two pieces (or int8 codes) do not fit
-        // the registers: two launches of two tiles each over the same pieces
-        // (W streams twice).
-        int rc = launch_decode<BITS, 2, P, (SPB > 2 ? SPB / 2 : 1)>(g, a);
-        if (rc) return rc;
-        a.mt0 = 2;
-        return MT == 3 ? launch_decode<BITS, 1, P, SPB>(g, a) : launch_decode<BITS, 2, P, (SPB > 2 ? SPB / 2 : 1)>(g, a);
-    }
+    if constexpr (DEC_ONE_GROUP<BITS, P>)
+        return MT == 3 ? launch_decode<BITS, 3, P, 2>(g, a) : launch_decode<BITS, 4, P, 1>(g, a);
+    else
+        return launch_decode<BITS, 2, P, DEC_D2<BITS, P>, 2>(g, a);
 }
 
 }  // namespace

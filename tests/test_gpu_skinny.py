@@ -111,6 +111,47 @@ def test_tiled_decode_many_chunks(gpu, dgm, orc, bits, G, K, M):
     assert worst <= 1e-2, worst
 
 
+@pytest.mark.parametrize("M,N,K,G", [(17, 70, 512, 128), (40, 300, 4096, 128), (64, 129, 1024, 256),
+                                     (64, 14336, 4096, 128)])
+def test_tiled_decode_bf16_arithmetic(gpu, dgm, orc, M, N, K, G):
+    """Reduced mode, int4, 16 < M <= 64: the tiled kernel takes bf16(x) against
+    the exact codes (offset by 136, removed by an fp32 term per block) and
+    applies the group scale in fp32, so it agrees with float64 products of
+    bf16(X) and the dequantized weights to 1e-5 per row; rows 1e-20 and 1e20
+    of the others keep that accuracy."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[1] *= np.float32(1e-20)
+    x[2] *= np.float32(1e20)
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if M % 2 == 0 else None
+    q, s = _quantize(gpu, to_dev(w), N, K, G, 4)
+    wd = orc.dequant(from_dev(q), from_dev(s), N, K, G, 4).reshape(N, K).astype(np.float64)
+    ref = _bf16_round(x) @ wd.T
+    if bias is not None:
+        ref = ref + bias.astype(np.float64)
+    y = _forward(gpu, dgm, 4, q, s, x.ravel(), bias, M, N, K, G, dgm.DGM_MATH_BF16).reshape(M, N)
+    worst = max(rel_err(y[m], ref[m]) for m in range(M))
+    assert worst <= 1e-5, worst
+
+
+def test_tiled_decode_bf16_non_finite(gpu, dgm, orc):
+    """Reduced mode, M > 16: a NaN or an infinity in a row makes that row NaN;
+    the other rows are unaffected."""
+    M, N, K, G = 20, 64, 512, 128
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[3, 7] = np.inf
+    x[5, 300] = np.nan
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    q, s = _quantize(gpu, to_dev(w), N, K, G, 4)
+    y = _forward(gpu, dgm, 4, q, s, x.ravel(), None, M, N, K, G, dgm.DGM_MATH_BF16).reshape(M, N)
+    ref = _ref(orc, q, s, x.ravel(), None, M, N, K, G, 4).reshape(M, N)
+    assert np.all(np.isnan(y[3])) and np.all(np.isnan(y[5]))
+    for m in (0, 1, 2, 4, 6, M - 1):
+        assert rel_err(y[m], ref[m]) <= 1e-2, m
+
+
 def test_rows_of_very_different_magnitude(gpu, dgm, orc):
     """Each row carries its own power-of-two scale: a tiny row next to a huge
     one keeps its own relative accuracy."""
