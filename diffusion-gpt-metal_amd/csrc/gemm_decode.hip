@@ -46,8 +46,8 @@
 // in issue order, so one wave issuing both would make every activation wait
 // for the younger weight loads. One barrier per interval hands the weights
 // from the stream wave to the compute waves. 16-byte slots are XOR-swizzled
-// by row, which keeps the fragment reads free of bank conflicts on the
-// 64-bank LDS.
+// by row (slot = piece ^ (row & 7)), which keeps the fragment reads free of
+// bank conflicts.
 //
 // Code -> f16 without a convert instruction: offset-binary codes (sign bit
 // flipped) are placed under the exponent of 1024.0 (0x6400) by one v_bitop3,
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int r = 8 * i + drow;
-            const int piece = dslot ^ (r & 7) ^ ((r >> 3) & 1);
+            const int piece = dslot ^ (r & 7);
             doff[i] = uint32_t(min(n0 + r, a.N - 1)) * uint32_t(a.rowb) + 16u * uint32_t(piece);
         }
         const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
@@ -475,7 +475,7 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct) {
                     const int r = 16 * ct + c;
-                    const int sl = (4 * hb + q) ^ (r & 7) ^ ((r >> 3) & 1);
+                    const int sl = (4 * hb + q) ^ (r & 7);
                     wc[ct] = *reinterpret_cast<const u32x4*>(cs + r * 128 + sl * 16);
                 }
             }
