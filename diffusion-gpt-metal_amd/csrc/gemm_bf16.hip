@@ -49,6 +49,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int RS = BK * 2;        // LDS row stride in bytes (chunks swizzled, no pad)
@@ -139,42 +140,63 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
 
     if (wave >= 8) {
         // ---- producer p: X rows 64p .. 64p+63 (8 per instruction), W row 64p + lane.
-        const int p = wave - 8;
+        // Every global load is inline asm and waited for by count: step ks
+        // issues X of step ks + 2 (8 direct-to-LDS loads) and then the codes
+        // and scales of step ks + 3 (NW loads) into the code buffer it has
+        // just dequantized, so codes have two steps to arrive and X stays
+        // two steps ahead. (With compiler-visible direct-to-LDS loads the
+        // compiler waits for all of them before any LDS store.)
+        constexpr int NW = CB + 2;
+        const int p = __builtin_amdgcn_readfirstlane(wave - 8);
         const int arl = lane >> 3, aslot = lane & 7;
-        uint32_t aoff[8];
+        uint32_t aoff[8];   // byte offsets into Xb
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int r = p * 64 + j * 8 + arl;
-            aoff[j] = uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8);
+            aoff[j] = (uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8)) * 2u;
         }
         const int brow = p * 64 + lane;
         const int bn = min(n0 + brow, N - 1);
-        const uint8_t* bptr = a.W + size_t(bn) * (BITS == 4 ? K / 2 : K);
-        const float* sptr = a.S + size_t(bn) * a.groups;
+        const uint32_t boff = uint32_t(bn) * uint32_t(BITS == 4 ? K / 2 : K);
+        const uint32_t soff = uint32_t(bn) * uint32_t(a.groups) * 4u;
+        const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
         auto xdma = [&](int ks, int st) {
-            uint8_t* As = smem + st * TILE + p * 64 * RS;
+            const uint32_t lds = lds0 + uint32_t(st * TILE + p * 64 * RS);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                __builtin_amdgcn_global_load_lds((global_cvoid*)(a.Xb + aoff[j] + ks * BK),
-                                                 (lds_void*)(As + j * 8 * RS), 16, 0, 0);
+                asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds + j * 8 * RS),
+                             "v"(aoff[j] + uint32_t(ks * BK * 2)), "s"(a.Xb)
+                             : "memory", "m0");
         };
-        auto wload = [&](uint4 (&c)[CB], float (&s)[2], int ks) {
-            const int k0 = ks * BK;
+#pragma clang diagnostic pop
+        auto wload = [&](u32x4 (&c)[CB], float (&s)[2], int ks) {
+            const uint32_t k0 = uint32_t(ks * BK);
 #pragma unroll
             for (int j = 0; j < CB; ++j)
-                c[j] = *reinterpret_cast<const uint4*>(bptr + (BITS == 4 ? k0 / 2 : k0) + 16 * j);
-            s[0] = sptr[k0 / a.G];
-            s[1] = sptr[(k0 + 32) / a.G];
+                asm volatile("global_load_dwordx4 %0, %1, %2"
+                             : "=v"(c[j])
+                             : "v"(boff + (BITS == 4 ? k0 / 2 : k0) + 16u * j), "s"(a.W));
+            asm volatile("global_load_dword %0, %1, %2" : "=v"(s[0]) : "v"(soff + (k0 / a.G) * 4u), "s"(a.S));
+            asm volatile("global_load_dword %0, %1, %2" : "=v"(s[1]) : "v"(soff + ((k0 + 32) / a.G) * 4u), "s"(a.S));
+        };
+        // The loaded registers become visible to the compiler only here,
+        // after the wait that covers them.
+        auto pin = [](u32x4 (&c)[CB], float (&s)[2]) {
+#pragma unroll
+            for (int j = 0; j < CB; ++j) asm volatile("" : "+v"(c[j]));
+            asm volatile("" : "+v"(s[0]), "+v"(s[1]));
         };
         // k half h (32 k) of the step: chunks 4h .. 4h+3 of the row.
-        auto dequant_store = [&](const uint4 (&c)[CB], const float (&sc)[2], int st) {
+        auto dequant_store = [&](const u32x4 (&c)[CB], const float (&sc)[2], int st) {
             uint8_t* Bs = smem + (3 + st) * TILE;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const float s = sc[h];
                 if constexpr (BITS == 4) {
                     const float s16 = s * 0.0625f, off = -8.0f * s;
-                    const uint32_t w4[4] = {c[h].x, c[h].y, c[h].z, c[h].w};
+                    const uint32_t w4[4] = {c[h][0], c[h][1], c[h][2], c[h][3]};
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
                         const uint32_t x = w4[d] ^ 0x88888888u;
@@ -194,8 +216,8 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
                     }
                 } else {
                     const float off = -128.0f * s;
-                    const uint32_t w8[8] = {c[2 * h].x, c[2 * h].y, c[2 * h].z, c[2 * h].w,
-                                            c[2 * h + 1].x, c[2 * h + 1].y, c[2 * h + 1].z, c[2 * h + 1].w};
+                    const uint32_t w8[8] = {c[2 * h][0], c[2 * h][1], c[2 * h][2], c[2 * h][3],
+                                            c[2 * h + 1][0], c[2 * h + 1][1], c[2 * h + 1][2], c[2 * h + 1][3]};
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
                         uint32_t o[4];
@@ -212,33 +234,45 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
                 }
             }
         };
-        uint4 cr[CB];
-        float sr[2];
+        u32x4 c0[CB], c1[CB];
+        float s0[2], s1[2];
         auto clampk = [&](int ks) { return ks < nk ? ks : nk - 1; };
         // X stage i at i * TILE, weight stage i at (3 + i) * TILE.
+        wload(c0, s0, 0);
         xdma(0, 0);
+        wload(c1, s1, clampk(1));
         xdma(clampk(1), 1);
-        wload(cr, sr, 0);
-        dequant_store(cr, sr, 0);
-        wload(cr, sr, clampk(1));
-        __syncthreads();
-        for (int ks = 0; ks < nk; ++ks) {
-            // Weights of step ks+1 (codes loaded during the previous step; the
-            // compiler waits for every outstanding load before the LDS stores,
-            // which also completes X of step ks+1), then the loads of step ks+2.
-            dequant_store(cr, sr, (ks + 1) & 1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + NW) : "memory");   // codes of step 0
+        pin(c0, s0);
+        dequant_store(c0, s0, 0);
+        wload(c0, s0, clampk(2));
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + 2 * NW) : "memory");   // X of step 0
+        // Step ks: codes of step ks + 1 are in (cc, cs), issued two steps ago;
+        // X of step ks + 1 landed by the barrier.
+        auto step = [&](int ks, u32x4 (&cc)[CB], float (&cs)[2]) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 + NW) : "memory");
+            pin(cc, cs);
+            dequant_store(cc, cs, (ks + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
             xdma(clampk(ks + 2), (ks + 2) % 3);
-            wload(cr, sr, clampk(ks + 2));
+            wload(cc, cs, clampk(ks + 3));
             __builtin_amdgcn_sched_barrier(0);
-            // Barrier once everything but this step's loads has completed
-            // (a __syncthreads here would also wait for those).
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + CB + 2) : "memory");
+            // Barrier once X of step ks + 1 has landed (the newer loads stay in
+            // flight) and every weight store of this wave is done.
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + 2 * NW) : "memory");
+        };
+        int ks = 0;
+        for (; ks + 1 < nk; ks += 2) {
+            step(ks, c1, s1);
+            step(ks + 1, c0, s0);
         }
+        if (ks < nk) step(ks, c1, s1);
         // The last steps' clamped loads (re-reads of the last step, never
         // consumed) land before the wave ends: no direct-to-LDS write may
         // outlive the workgroup's LDS.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        pin(c0, s0);
+        pin(c1, s1);
         return;
     }
 
