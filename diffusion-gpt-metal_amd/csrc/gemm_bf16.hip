@@ -9,16 +9,19 @@
 //
 // Design (prefill shapes, MFMA-bound):
 //  * X is converted to bf16 once by a pre-pass (it is re-read by every tile
-//    column, so converting it inside the GEMM would repeat the work N/256
+//    column, so converting it inside the GEMM would repeat the work N/128
 //    times).
-//  * A workgroup computes a 256 x 256 tile of Y with twelve waves in two
-//    roles. Eight MFMA waves each own a 64 x 128 block = 4 x 8
+//  * A workgroup computes a 512 x 128 tile of Y with twelve waves in two
+//    roles. Eight MFMA waves each own a 128 x 64 block = 8 x 4
 //    v_mfma_f32_16x16x32_bf16 tiles (128 fp32 accumulators) and only read LDS
 //    and issue MFMAs. Four producer waves load the X tile (global -> LDS with
 //    global_load_lds_dwordx4, no VGPR staging) and the weight codes, and
-//    dequantize the codes into the bf16 weight tile in LDS, one weight row
-//    per lane. Each SIMD holds two MFMA waves and one producer, so the
+//    dequantize the codes into the bf16 weight tile in LDS, half a weight row
+//    (32 k) per lane. Each SIMD holds two MFMA waves and one producer, so the
 //    dequantization's VALU work runs beside the MFMAs. K advances 64 per step.
+//    The tall tile halves the weights dequantized per step against the
+//    256 x 256 tile with the same MFMA work (the producers' dequantization
+//    sets the step time): int8 gains ~5%, int4 is unchanged.
 //  * A wave instruction of the X load fills 1 KB of LDS in lane order, so rows
 //    are unpadded (128 B) and the 16-byte chunks of row r sit at slot
 //    c ^ (r & 7): each lane fetches the global chunk that belongs in its slot.
@@ -27,11 +30,12 @@
 //    cycles per wave instruction with this map, as with contiguous lanes, and
 //    32 when rows 8-15 are further XOR-ed by 1. The weight tile uses the same
 //    swizzle (its one-row-per-lane stores cost the same either way).
-//  * Stages: three for X, two for the weights (160 KB of LDS). During step k
-//    the MFMA waves read stage k; the producers store the weights of step k+1
-//    (codes loaded during step k-1) and then issue the loads of step k+2, and
-//    enter the step's barrier once everything but those loads has landed, so
-//    every load has a whole step to arrive. One barrier per step.
+//  * Stages: two for X, two for the weights (160 KB of LDS). During step k
+//    the MFMA waves read stage k; the producers first issue X of step k+1,
+//    then store the weights of step k+1 (codes loaded two steps earlier),
+//    then issue the codes of step k+3, and enter the step's barrier once X of
+//    step k+1 has landed. All producer loads are inline asm with counted
+//    waits. One barrier per step.
 //  * Dequant: int4 bytes are flipped to offset binary and masked into the
 //    high nibble, so each byte is 16*(code+8) as an unsigned value and
 //    converts with one v_cvt_f32_ubyte; fma(f, s/16, -8s) then yields
@@ -41,7 +45,7 @@
 //  * Tile order is XCD-aware: workgroups are dealt round-robin to the 8 XCDs,
 //    so the logical tile index is remapped to give each XCD a contiguous range,
 //    walked in groups of 4 tile rows; the ~32 tiles an XCD runs at once then
-//    share A and B rows in its L2.
+//    share X and weight rows in its L2.
 #include "common.hpp"
 
 namespace {
@@ -51,9 +55,8 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 512, BN = 128, BK = 64;
 constexpr int RS = BK * 2;        // LDS row stride in bytes (chunks swizzled, no pad)
-constexpr int TILE = BM * RS;     // one operand tile (BM == BN)
 constexpr int GROUP_M = 4;        // tile rows per group of the XCD-local order
 
 struct Bf16Args {
@@ -107,20 +110,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ int swz(int r, int c) { return r * RS + ((c ^ (r & 7)) << 4); }
 
 // ---- the kernel ------------------------------------------------------------------
-// Twelve waves: waves 0-7 only read LDS and issue MFMAs (a 64 x 128 block
+// Twelve waves: waves 0-7 only read LDS and issue MFMAs (a 128 x 64 block
 // each); waves 8-11 are producers: they issue the X tile's direct-to-LDS loads
 // and load, dequantize and store the weight tile of the next step while the
 // MFMA waves work on the current one. Waves are dealt to the SIMDs round
 // robin, so each SIMD holds two MFMA waves and one producer and the
 // dequantization's VALU work overlaps MFMA issue instead of following it.
-// LDS: three X stages (the X tile of step k+2 is loaded during step k) and two
-// weight stages, 5 x 32 KB.
+// The tile is 512 rows of X by 128 weight rows: per 64-k step the producers
+// dequantize 128 x 64 weights (each W element is dequantized once per 512
+// rows of Y) and move 512 x 64 of X. LDS: two X stages (the X tile of step
+// k+1 is loaded at the start of step k) and two weight stages, 2 x 64 + 2 x 16
+// KB.
 constexpr int NTW = 768;
-constexpr int LDS_WS = 5 * TILE;
+constexpr int TILE_X = BM * RS;
+constexpr int TILE_W = BN * RS;
+constexpr int LDS_WS = 2 * TILE_X + 2 * TILE_W;
 
 template <int BITS>
 __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
-    constexpr int CB = BITS == 4 ? 2 : 4;   // 16-byte code loads per producer lane per 64-k step
+    constexpr int CB = BITS == 4 ? 1 : 2;   // 16-byte code loads per producer lane per 64-k step (32 k)
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -139,127 +147,121 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
     const int nk = K / BK;
 
     if (wave >= 8) {
-        // ---- producer p: X rows 64p .. 64p+63 (8 per instruction), W row 64p + lane.
+        // ---- producer p: X rows 128p .. 128p+127 (8 per instruction); W row
+        // 32p + lane % 32, k half lane / 32 (32 k, one group).
         // Every global load is inline asm and waited for by count: step ks
-        // issues X of step ks + 2 (8 direct-to-LDS loads) and then the codes
-        // and scales of step ks + 3 (NW loads) into the code buffer it has
-        // just dequantized, so codes have two steps to arrive and X stays
-        // two steps ahead. (With compiler-visible direct-to-LDS loads the
+        // issues X of step ks + 1 (16 direct-to-LDS loads) first and, after
+        // the weight stores, the codes and scale of step ks + 3 (NW loads)
+        // into the code buffer it has just dequantized, so codes have two
+        // steps to arrive. (With compiler-visible direct-to-LDS loads the
         // compiler waits for all of them before any LDS store.)
-        constexpr int NW = CB + 2;
+        constexpr int NW = CB + 1;
         const int p = __builtin_amdgcn_readfirstlane(wave - 8);
         const int arl = lane >> 3, aslot = lane & 7;
-        uint32_t aoff[8];   // byte offsets into Xb
+        uint32_t aoff[16];   // byte offsets into Xb
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = p * 64 + j * 8 + arl;
+        for (int j = 0; j < 16; ++j) {
+            const int r = p * 128 + j * 8 + arl;
             aoff[j] = (uint32_t(min(m0 + r, M - 1)) * uint32_t(K) + ((aslot ^ (r & 7)) * 8)) * 2u;
         }
-        const int brow = p * 64 + lane;
+        const int brow = p * 32 + (lane & 31), hh = lane >> 5;
         const int bn = min(n0 + brow, N - 1);
-        const uint32_t boff = uint32_t(bn) * uint32_t(BITS == 4 ? K / 2 : K);
+        const uint32_t boff = uint32_t(bn) * uint32_t(BITS == 4 ? K / 2 : K) + uint32_t(hh) * (BITS == 4 ? 16u : 32u);
         const uint32_t soff = uint32_t(bn) * uint32_t(a.groups) * 4u;
         const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
         auto xdma = [&](int ks, int st) {
-            const uint32_t lds = lds0 + uint32_t(st * TILE + p * 64 * RS);
+            const uint32_t lds = lds0 + uint32_t(st * TILE_X + p * 128 * RS);
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 16; ++j)
                 asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds + j * 8 * RS),
                              "v"(aoff[j] + uint32_t(ks * BK * 2)), "s"(a.Xb)
                              : "memory", "m0");
         };
 #pragma clang diagnostic pop
-        auto wload = [&](u32x4 (&c)[CB], float (&s)[2], int ks) {
+        auto wload = [&](u32x4 (&c)[CB], float& s, int ks) {
             const uint32_t k0 = uint32_t(ks * BK);
 #pragma unroll
             for (int j = 0; j < CB; ++j)
                 asm volatile("global_load_dwordx4 %0, %1, %2"
                              : "=v"(c[j])
                              : "v"(boff + (BITS == 4 ? k0 / 2 : k0) + 16u * j), "s"(a.W));
-            asm volatile("global_load_dword %0, %1, %2" : "=v"(s[0]) : "v"(soff + (k0 / a.G) * 4u), "s"(a.S));
-            asm volatile("global_load_dword %0, %1, %2" : "=v"(s[1]) : "v"(soff + ((k0 + 32) / a.G) * 4u), "s"(a.S));
+            asm volatile("global_load_dword %0, %1, %2"
+                         : "=v"(s)
+                         : "v"(soff + ((k0 + 32u * hh) / a.G) * 4u), "s"(a.S));
         };
         // The loaded registers become visible to the compiler only here,
         // after the wait that covers them.
-        auto pin = [](u32x4 (&c)[CB], float (&s)[2]) {
+        auto pin = [](u32x4 (&c)[CB], float& s) {
 #pragma unroll
             for (int j = 0; j < CB; ++j) asm volatile("" : "+v"(c[j]));
-            asm volatile("" : "+v"(s[0]), "+v"(s[1]));
+            asm volatile("" : "+v"(s));
         };
-        // k half h (32 k) of the step: chunks 4h .. 4h+3 of the row.
-        auto dequant_store = [&](const u32x4 (&c)[CB], const float (&sc)[2], int st) {
-            uint8_t* Bs = smem + (3 + st) * TILE;
+        // The lane's 32 k: chunks 4 hh .. 4 hh + 3 of its weight row.
+        auto dequant_store = [&](const u32x4 (&c)[CB], float s, int st) {
+            uint8_t* Bs = smem + 2 * TILE_X + st * TILE_W;
+            if constexpr (BITS == 4) {
+                const float s16 = s * 0.0625f, off = -8.0f * s;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const float s = sc[h];
-                if constexpr (BITS == 4) {
-                    const float s16 = s * 0.0625f, off = -8.0f * s;
-                    const uint32_t w4[4] = {c[h][0], c[h][1], c[h][2], c[h][3]};
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t x = c[0][d] ^ 0x88888888u;
+                    uint32_t lo = (x << 4) & 0xF0F0F0F0u;
+                    uint32_t hi = x & 0xF0F0F0F0u;
+                    asm("" : "+v"(lo));
+                    asm("" : "+v"(hi));
+                    const float fe[4] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
+                                         float(lo >> 24)};
+                    const float fo[4] = {float(hi & 0xFFu), float((hi >> 8) & 0xFFu), float((hi >> 16) & 0xFFu),
+                                         float(hi >> 24)};
+                    uint32_t o[4];
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        const uint32_t x = w4[d] ^ 0x88888888u;
-                        uint32_t lo = (x << 4) & 0xF0F0F0F0u;
-                        uint32_t hi = x & 0xF0F0F0F0u;
-                        asm("" : "+v"(lo));
-                        asm("" : "+v"(hi));
-                        const float fe[4] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
-                                             float(lo >> 24)};
-                        const float fo[4] = {float(hi & 0xFFu), float((hi >> 8) & 0xFFu), float((hi >> 16) & 0xFFu),
-                                             float(hi >> 24)};
-                        uint32_t o[4];
+                    for (int i = 0; i < 4; ++i)
+                        o[i] = pack_bf16(__builtin_fmaf(fe[i], s16, off), __builtin_fmaf(fo[i], s16, off));
+                    *reinterpret_cast<u32x4*>(Bs + swz(brow, hh * 4 + d)) = u32x4{o[0], o[1], o[2], o[3]};
+                }
+            } else {
+                const float off = -128.0f * s;
+                const uint32_t w8[8] = {c[0][0], c[0][1], c[0][2], c[0][3], c[1][0], c[1][1], c[1][2], c[1][3]};
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            o[i] = pack_bf16(__builtin_fmaf(fe[i], s16, off), __builtin_fmaf(fo[i], s16, off));
-                        *reinterpret_cast<uint4*>(Bs + swz(brow, h * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
+                for (int d = 0; d < 4; ++d) {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const uint32_t x = w8[2 * d + e] ^ 0x80808080u;
+                        const float f0 = float(x & 0xFFu), f1 = float((x >> 8) & 0xFFu);
+                        const float f2 = float((x >> 16) & 0xFFu), f3 = float(x >> 24);
+                        o[2 * e] = pack_bf16(__builtin_fmaf(f0, s, off), __builtin_fmaf(f1, s, off));
+                        o[2 * e + 1] = pack_bf16(__builtin_fmaf(f2, s, off), __builtin_fmaf(f3, s, off));
                     }
-                } else {
-                    const float off = -128.0f * s;
-                    const uint32_t w8[8] = {c[2 * h][0], c[2 * h][1], c[2 * h][2], c[2 * h][3],
-                                            c[2 * h + 1][0], c[2 * h + 1][1], c[2 * h + 1][2], c[2 * h + 1][3]};
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        uint32_t o[4];
-#pragma unroll
-                        for (int e = 0; e < 2; ++e) {
-                            const uint32_t x = w8[2 * d + e] ^ 0x80808080u;
-                            const float f0 = float(x & 0xFFu), f1 = float((x >> 8) & 0xFFu);
-                            const float f2 = float((x >> 16) & 0xFFu), f3 = float(x >> 24);
-                            o[2 * e] = pack_bf16(__builtin_fmaf(f0, s, off), __builtin_fmaf(f1, s, off));
-                            o[2 * e + 1] = pack_bf16(__builtin_fmaf(f2, s, off), __builtin_fmaf(f3, s, off));
-                        }
-                        *reinterpret_cast<uint4*>(Bs + swz(brow, h * 4 + d)) = make_uint4(o[0], o[1], o[2], o[3]);
-                    }
+                    *reinterpret_cast<u32x4*>(Bs + swz(brow, hh * 4 + d)) = u32x4{o[0], o[1], o[2], o[3]};
                 }
             }
         };
         u32x4 c0[CB], c1[CB];
-        float s0[2], s1[2];
+        float s0, s1;
         auto clampk = [&](int ks) { return ks < nk ? ks : nk - 1; };
-        // X stage i at i * TILE, weight stage i at (3 + i) * TILE.
+        // X stage i at i * TILE_X, weight stage i at 2 * TILE_X + i * TILE_W.
         wload(c0, s0, 0);
-        xdma(0, 0);
         wload(c1, s1, clampk(1));
-        xdma(clampk(1), 1);
+        xdma(0, 0);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + NW) : "memory");   // codes of step 0
         pin(c0, s0);
         dequant_store(c0, s0, 0);
         wload(c0, s0, clampk(2));
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + 2 * NW) : "memory");   // X of step 0
-        // Step ks: codes of step ks + 1 are in (cc, cs), issued two steps ago;
-        // X of step ks + 1 landed by the barrier.
-        auto step = [&](int ks, u32x4 (&cc)[CB], float (&cs)[2]) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 + NW) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(NW) : "memory");   // X of step 0
+        // Step ks: codes of step ks + 1 are in (cc, cs), issued two steps ago.
+        auto step = [&](int ks, u32x4 (&cc)[CB], float& cs) {
+            xdma(clampk(ks + 1), (ks + 1) & 1);   // stage of step ks - 1, free since the last barrier
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(32 + NW) : "memory");
             pin(cc, cs);
             dequant_store(cc, cs, (ks + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
-            xdma(clampk(ks + 2), (ks + 2) % 3);
             wload(cc, cs, clampk(ks + 3));
             __builtin_amdgcn_sched_barrier(0);
-            // Barrier once X of step ks + 1 has landed (the newer loads stay in
+            // Barrier once X of step ks + 1 has landed (the codes stay in
             // flight) and every weight store of this wave is done.
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(8 + 2 * NW) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(NW) : "memory");
         };
         int ks = 0;
         for (; ks + 1 < nk; ks += 2) {
@@ -276,47 +278,47 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
         return;
     }
 
-    // ---- MFMA waves
+    // ---- MFMA waves: rows wm*128 .. +127, columns wn*64 .. +63.
     const int wm = wave >> 1, wn = wave & 1;
-    f32x4 acc[4][8];
+    f32x4 acc[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int cw0 = ((0 * 4 + q) ^ (l16 & 7)) << 4, cw1 = ((1 * 4 + q) ^ (l16 & 7)) << 4;
     auto compute = [&](int xs, int ws) {
-        const uint8_t* As = smem + xs * TILE + (wm * 64 + l16) * RS;
-        const uint8_t* Bs = smem + (3 + ws) * TILE + (wn * 128 + l16) * RS;
+        const uint8_t* As = smem + xs * TILE_X + (wm * 128 + l16) * RS;
+        const uint8_t* Bs = smem + 2 * TILE_X + ws * TILE_W + (wn * 64 + l16) * RS;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             const int cw = kk ? cw1 : cw0;
-            bf16x8 af[4];
+            bf16x8 bf[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(As + i * 16 * RS + cw);
+            for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(Bs + j * 16 * RS + cw);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const bf16x8 bfj = *reinterpret_cast<const bf16x8*>(Bs + j * 16 * RS + cw);
+            for (int i = 0; i < 8; ++i) {
+                const bf16x8 afi = *reinterpret_cast<const bf16x8*>(As + i * 16 * RS + cw);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfj, acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afi, bf[j], acc[i][j], 0, 0, 0);
             }
         }
     };
     __syncthreads();
     for (int ks = 0; ks < nk; ++ks) {
-        compute(ks % 3, ks & 1);
+        compute(ks & 1, ks & 1);
         __syncthreads();
     }
 
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int col = n0 + wn * 128 + j * 16 + l16;
+    for (int j = 0; j < 4; ++j) {
+        const int col = n0 + wn * 64 + j * 16 + l16;
         const float bv = (a.has_bias && col < N) ? a.bias[col] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm * 64 + i * 16 + 4 * q + r;
+                const int row = m0 + wm * 128 + i * 16 + 4 * q + r;
                 if (row < M && col < N) __builtin_nontemporal_store(acc[i][j][r] + bv, a.Y + size_t(row) * N + col);
             }
     }
