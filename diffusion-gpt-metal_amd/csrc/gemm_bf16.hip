@@ -310,17 +310,38 @@ __global__ __launch_bounds__(NTW) void gemm_bf16_kernel(Bf16Args a) {
         __syncthreads();
     }
 
+    // Epilogue. The bias is added to the accumulators before any store, so
+    // no store depends on a load: a bias load that only some paths issue
+    // makes the compiler wait for every outstanding memory operation
+    // (vmcnt(0)) before each dependent store, i.e. for all earlier stores,
+    // which serializes the 128 stores of a wave on the write latency.
+    if (a.has_bias) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = n0 + wn * 64 + j * 16 + l16;
-        const float bv = (a.has_bias && col < N) ? a.bias[col] : 0.0f;
+        for (int j = 0; j < 4; ++j) {
+            const float bv = a.bias[min(n0 + wn * 64 + j * 16 + l16, N - 1)];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i][j] += bv;
+        }
+    }
+    float* yb = a.Y + size_t(m0 + wm * 128 + 4 * q) * N + (n0 + wn * 64 + l16);
+    if (m0 + BM <= M && n0 + BN <= N) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm * 128 + i * 16 + 4 * q + r;
-                if (row < M && col < N) __builtin_nontemporal_store(acc[i][j][r] + bv, a.Y + size_t(row) * N + col);
-            }
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    yb[size_t(i * 16 + r) * N + j * 16] = acc[i][j][r];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int row = m0 + wm * 128 + i * 16 + 4 * q + r, col = n0 + wn * 64 + j * 16 + l16;
+                    if (row < M && col < N) yb[size_t(i * 16 + r) * N + j * 16] = acc[i][j][r];
+                }
     }
 }
 

@@ -578,18 +578,23 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
             *reinterpret_cast<f32x4*>(red + (kw * 64 + 16 * ct + c) * RP + 16 * (mh * MT + mt) + 4 * q) = acc[mt][ct];
     __syncthreads();
     const int rows = min(a.M - 16 * a.mt0, 16 * MT * MW);
-    for (int idx = threadIdx.x; idx < ((rows + 3) / 4) * 64; idx += 64 * DEC_KW * MW) {
-        const int m4 = idx >> 6, col = idx & 63;
-        const int n = n0 + col;
-        if (n >= a.N) continue;
+    // A thread keeps one column (the stride is a multiple of 64). Its bias is
+    // loaded and waited for before the first store: a load used only inside
+    // the conditional stores makes the compiler wait for all outstanding
+    // memory operations, earlier stores included, before each store.
+    const int col = threadIdx.x & 63, n = n0 + col;
+    if (n >= a.N || w >= DEC_KW * MW) return;   // the stream wave stores nothing
+    float bv = a.has_bias ? a.bias[n] : 0.0f;
+    asm volatile("" : "+v"(bv));
+    for (int m4 = w; m4 < (rows + 3) / 4; m4 += DEC_KW * MW) {
         f32x4 y = *reinterpret_cast<const f32x4*>(red + (0 * 64 + col) * RP + 4 * m4);
 #pragma unroll
         for (int v = 1; v < 4; ++v) y += *reinterpret_cast<const f32x4*>(red + (v * 64 + col) * RP + 4 * m4);
-        const float bv = a.has_bias ? a.bias[n] : 0.0f;
+        if (a.has_bias) y += bv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = 4 * m4 + r;
-            if (m < rows) a.Y[size_t(16 * a.mt0 + m) * a.N + n] = a.has_bias ? y[r] + bv : y[r];
+            if (m < rows) a.Y[size_t(16 * a.mt0 + m) * a.N + n] = y[r];
         }
     }
 }
@@ -925,14 +930,17 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) *reinterpret_cast<f32x4*>(red + (w * 16 + c) * 64 + 16 * ct + 4 * q) = acc[ct];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < a.M * 64; idx += 64 * DS_CW) {
-        const int m = idx >> 6, col = idx & 63;
-        const int n = n0 + col;
-        if (n >= a.N) continue;
+    // One column per thread (the stride is a multiple of 64); its bias is
+    // waited for before the first store, as in decode_kernel.
+    const int col = threadIdx.x & 63, n = n0 + col;
+    if (n >= a.N || w >= DS_CW) return;   // the stream wave stores nothing
+    float bv = a.has_bias ? a.bias[n] : 0.0f;
+    asm volatile("" : "+v"(bv));
+    for (int m = w; m < a.M; m += DS_CW) {
         float y = red[m * 64 + col];
 #pragma unroll
         for (int v = 1; v < DS_CW; ++v) y += red[(v * 16 + m) * 64 + col];
-        if (a.has_bias) y += a.bias[n];
+        if (a.has_bias) y += bv;
         a.Y[size_t(m) * a.N + n] = y;
     }
 }

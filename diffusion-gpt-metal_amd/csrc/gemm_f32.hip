@@ -563,18 +563,17 @@ __global__ __launch_bounds__(kThreads) void gemm_fwd_lds_kernel(GemmArgs a, int 
     }
 
     // -- reduce contraction parts in order and store. acc: rows 4*q4 + r, column r16.
+    // The bias is added before the first store: a load whose value only the
+    // conditional stores use makes the compiler wait for every outstanding
+    // memory operation, the earlier stores included, before each store.
     if constexpr (KS == 1) {
         const int j = j0 + wn * 16 + r16;
         if (j < a.cols) {
-            const float bb = a.has_bias ? a.bias[j] : 0.0f;
+            if (a.has_bias) acc += a.bias[j];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = i0 + 4 * q4 + r;
-                if (i < a.rows) {
-                    float v = acc[r];
-                    if (a.has_bias) v += bb;
-                    a.out[size_t(i) * a.cols + j] = v;
-                }
+                if (i < a.rows) a.out[size_t(i) * a.cols + j] = acc[r];
             }
         }
     } else {
@@ -583,13 +582,18 @@ __global__ __launch_bounds__(kThreads) void gemm_fwd_lds_kernel(GemmArgs a, int 
 #pragma unroll
         for (int r = 0; r < 4; ++r) part[(wk * 16 + 4 * q4 + r) * TN + wn * 16 + r16] = acc[r];
         __syncthreads();
+        static_assert(kThreads % TN == 0, "a thread keeps one column");
+        const int j = j0 + threadIdx.x % TN;
+        if (j >= a.cols) return;
+        float bb = a.has_bias ? a.bias[j] : 0.0f;
+        asm volatile("" : "+v"(bb));
         for (int e = threadIdx.x; e < 16 * TN; e += kThreads) {
-            const int i = i0 + e / TN, j = j0 + e % TN;
-            if (i >= a.rows || j >= a.cols) continue;
+            const int i = i0 + e / TN;
+            if (i >= a.rows) break;
             float v = part[e];
 #pragma unroll
             for (int p2 = 1; p2 < KS; ++p2) v += part[p2 * 16 * TN + e];
-            if (a.has_bias) v += a.bias[j];
+            if (a.has_bias) v += bb;
             a.out[size_t(i) * a.cols + j] = v;
         }
     }
@@ -1103,13 +1107,21 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     const int k = k0 + wave * 16 + r16;
     if (k < K) {
         if (a.sg_gate) {
+            // All four rows' gate and up values are loaded before the first
+            // store, so no store waits on a later row's loads.
+            float gv[4], uv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const size_t e = size_t(min(i0 + 4 * q4 + r, a.rows - 1)) * K + k;
+                gv[r] = a.sg_gate[e];
+                uv[r] = a.sg_up[e];
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = i0 + 4 * q4 + r;
                 if (i < a.rows) {
-                    const size_t e = size_t(i) * K + k;
                     float* o = a.out + size_t(i) * 2 * K + k;
-                    dgm::swiglu_bwd_value(a.sg_gate[e], a.sg_up[e], acc[r], o[0], o[K]);
+                    dgm::swiglu_bwd_value(gv[r], uv[r], acc[r], o[0], o[K]);
                 }
             }
         } else {
