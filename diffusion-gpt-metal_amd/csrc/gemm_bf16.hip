@@ -355,7 +355,10 @@ bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_
     if (bits != 4 && bits != 8) return false;
     if (p->M <= 64 || p->K == 0 || (p->K % (2 * BK)) != 0) return false;
     if (p->qGroup == 0 || (p->qGroup % 32) != 0) return false;   // a thread's 32 k share a group
-    if (int64_t(p->M) * p->K >= (int64_t(1) << 32)) return false;   // 32-bit element offsets
+    // The kernel addresses X (bf16), the codes and the scales with 32-bit byte offsets.
+    if (int64_t(p->M) * p->K * 2 >= (int64_t(1) << 32)) return false;
+    if (int64_t(p->N) * p->K * bits / 8 >= (int64_t(1) << 32)) return false;
+    if (int64_t(p->N) * (p->K / p->qGroup) * 4 >= (int64_t(1) << 32)) return false;
     (void)S;
     return aligned(W, 16) && aligned(X, 16);
 }
