@@ -51,10 +51,11 @@ def hipcc() -> str:
 
 
 # Sources whose kernels issue loads as inline asm and wait for them by hand
-# (gemm_decode.hip): a register spilled or copied while such a load is in
-# flight would be read before the load fills it, so these kernels must not
-# use scratch. The build checks the compiler's resource-usage remarks.
-NO_SCRATCH = {"gemm_decode.hip"}
+# (gemm_decode.hip, gemm_stream.hip, and the prefill producers of
+# gemm_bf16.hip): a register spilled while such a load is in flight would be
+# read before the load fills it, so these kernels must not use scratch. The
+# build checks the compiler's resource-usage remarks.
+NO_SCRATCH = {"gemm_decode.hip", "gemm_stream.hip", "gemm_bf16.hip"}
 REMARK = "-Rpass-analysis=kernel-resource-usage"
 
 

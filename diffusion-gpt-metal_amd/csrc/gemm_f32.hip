@@ -1556,6 +1556,9 @@ int decode_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const fl
 int skinny_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
                const float* bias, float* Y, const dgm_GemmP* p);
 bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
+bool stream_ok(dgm_gpu* g, int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
+int stream_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X, const float* bias, float* Y,
+               const dgm_GemmP* p);
 int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
              const float* bias, float* Y, const dgm_GemmP* p);
 
@@ -1567,6 +1570,7 @@ int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const 
     // operations per 8 weights and whose activation pieces fill spare MFMA
     // rows; more rows take f16 MFMA over exact f16 activation pieces
     // (gemm_decode.hip), or the int8-MFMA kernel outside that domain.
+    if (stream_ok(g, bits, W, X, scale, p)) return stream_fwd(g, bits, W, scale, X, bias, Y, p);
     if (skinny_fused_ok(g, bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
     if (decode_ok(bits, W, X, scale, p)) return decode_fwd(g, bits, W, scale, X, bias, Y, p);
     if (skinny_ok(bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
