@@ -359,10 +359,11 @@ int launch_p(dgm_gpu* g, const StreamArgs& a, const StPlan& pl) {
 namespace dgm {
 
 // The streaming kernel's domain: quantized weights, 1 <= M <= 4, whole
-// 128-byte chunks (int4: K % 256 == 0; int8: K % 128 == 0), at most one chunk
-// per wave (K <= 4096 int4, 2048 int8), blocks inside groups, at most 64
-// groups, the pieces in LDS (the fp32 mode: M = 1 at K = 4096), 16-byte
-// aligned codes and X, 32-bit byte offsets.
+// 128-byte chunks (int4: K % 256 == 0; int8: K % 128 == 0), at most 16
+// chunks per row (K <= 4096 int4, 2048 int8), blocks inside groups, at most
+// 64 groups (4 scale loads per wave), the pieces in LDS (the fp32 mode: M = 1
+// at K = 4096; the reduced mode: M <= 2), 16-byte aligned codes and X,
+// 32-bit byte offsets.
 bool stream_ok(dgm_gpu* g, int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p) {
     if (bits != 4 && bits != 8) return false;
     if (p->M < 1 || p->M > 4 || p->K == 0 || p->N == 0) return false;
@@ -374,7 +375,6 @@ bool stream_ok(dgm_gpu* g, int bits, const void* W, const float* X, const float*
     const int64_t groups = p->K / p->qGroup;
     if (int64_t(p->N) * rowb >= (int64_t(1) << 32)) return false;
     if (int64_t(p->N) * groups * 4 >= (int64_t(1) << 32)) return false;
-    if (int64_t(p->M) * p->K * 4 >= (int64_t(1) << 31)) return false;
     if (st_plan(bits, g->math == DGM_MATH_FP32, int(p->M), int(groups), int(rowb / 128)).lds == 0) return false;
     return aligned(W, 16) && aligned(X, 16) && aligned(S, 4);
 }
@@ -395,10 +395,10 @@ int stream_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const fl
     a.rowb = bits == 4 ? a.K / 2 : a.K;
     a.nchunk = a.rowb / 128;
     a.has_bias = p->hasBias != 0;
+    a.ns = a.groups;
     const bool exact = g->math == DGM_MATH_FP32;
     const StPlan pl = st_plan(bits, exact, a.M, a.groups, a.nchunk);
-    if (pl.lds == 0) return dgm::fail(g, DGM_ERR_UNSUPPORTED, "stream: the call does not fit LDS");
-    a.ns = a.groups;
+    if (pl.lds == 0) return fail(g, DGM_ERR_UNSUPPORTED, "stream: the call does not fit LDS");
     a.s_off = pl.s_off;
     a.x_off = pl.x_off;
     if (bits == 4) return exact ? launch_p<4, 4>(g, a, pl) : launch_p<4, 2>(g, a, pl);
