@@ -88,6 +88,7 @@ class Bench:
         self.stream = torch.cuda.Stream()
         self.gpu = dgm.GPU(stream=self.stream)
         self.gen = torch.Generator(device="cpu").manual_seed(1234)
+        self.read_ceiling_c4 = None   # GB/s, set by hbm_read_ceiling
 
     def randn(self, n: int, std: float):
         t = self.torch.randn(n, generator=self.gen, dtype=self.torch.float32) * std
@@ -359,7 +360,9 @@ def bench_c4(b: Bench, reps: int, M: int, math_mode: int, cpu: bool) -> dict:
            "TFLOPs": round(flops / ms / 1e9, 3), "weight_copies_rotated": copies,
            "algorithmic_bytes": nbytes,
            "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
-                                traffic_for(name, ["skinny", "tiled", "decode", "gemv"]))}
+                                traffic_for(name, ["skinny", "tiled", "decode", "stream"]))}
+    if b.read_ceiling_c4:
+        out["frac_of_read_ceiling"] = round(nbytes / ms / 1e6 / b.read_ceiling_c4, 4)
     if cpu:
         # The reference's CPU path does the same work at any M per output
         # column; time a slice of N sized to about a second.
@@ -551,14 +554,20 @@ def bench_c3_train(b: Bench, reps: int, cpu: bool) -> dict:
 
 
 def bench_quant(b: Bench, reps: int, bits: int, cpu: bool) -> dict:
+    """quantize of the c4/c5 weight, W[14336,4096] G=128. Successive launches
+    rotate over distinct (W, codes, scales) sets totalling at least 768 MiB,
+    so that no launch finds its operands in the 256 MB Infinity Cache."""
     N, K, G = C4["N"], C4["K"], C4["G"]
-    w = b.randn(N * K, 0.02)
-    q = b.zeros(N * K // (2 if bits == 4 else 1), b.torch.uint8)
-    s = b.zeros(N * (K // G))
-    ms = b.time_launches(lambda i: b.gpu.quantize(w, q, s, N, K, bits, G), reps)
     nbytes = 4 * N * K + (N * K // (2 if bits == 4 else 1)) + 4 * N * (K // G)
+    sets = max(2, -(-768 * 2 ** 20 // nbytes))
+    w0 = b.randn(N * K, 0.02)
+    W = [w0] + [w0.clone() for _ in range(sets - 1)]
+    Q = [b.zeros(N * K // (2 if bits == 4 else 1), b.torch.uint8) for _ in range(sets)]
+    S = [b.zeros(N * (K // G)) for _ in range(sets)]
+    ms = b.time_launches(lambda i: b.gpu.quantize(W[i % sets], Q[i % sets], S[i % sets], N, K, bits, G), reps)
+    del W, Q, S
     out = {"kernel": f"quant_i{bits}", "shape": "W[14336,4096] G=128", "us": round(ms * 1e3, 3),
-           "GBps": round(nbytes / ms / 1e6, 2),
+           "GBps": round(nbytes / ms / 1e6, 2), "operand_sets_rotated": sets,
            "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
                                 traffic_for(f"quant_i{bits}", ["quant_vec_kernel"]))}
     if cpu:
@@ -670,6 +679,40 @@ def hbm_ceiling(b: Bench) -> dict:
             "GBps": round(gbps, 1), "frac_of_8TBps": round(gbps / PEAK["hbm_GBps"], 4)}
 
 
+def hbm_read_ceiling(b: Bench) -> dict:
+    """The box's measured read ceiling for one launch: this library's read-only
+    probe (dgm_probe_read) over (i) one c4 weight copy (codes + scales,
+    31,195,136 bytes), rotated over as many copies as bench_c4 uses so that no
+    launch finds it in the 256 MB Infinity Cache, and (ii) 512 MiB (two
+    buffers, alternated); 16-byte register loads and direct-to-LDS loads, one
+    workgroup per CU and more. Graph replays, as for the c4 lines, so the
+    per-launch cost is included the same way."""
+    t = b.torch
+    N, K, G = C4["N"], C4["K"], C4["G"]
+    wq = N * K // 2 + N * (K // G) * 4
+    copies = max(2, -(-512 * 2 ** 20 // wq))
+    sink = b.zeros(1 << 16, t.int32)
+    out = {}
+    big = 512 * 2 ** 20
+    for name, nbytes, nbuf, reps in (("c4_weight_copy", wq, copies, 72), ("512MiB", big, 2, 10)):
+        buf = t.ones(nbytes * nbuf, dtype=t.uint8, device="cuda")
+        rows = []
+        for mode in (0, 1):
+            for wgs in (256, 512, 1024):
+                ms = b.time_launches(
+                    lambda i: b.gpu.probeRead(buf[(i % nbuf) * nbytes:], nbytes, mode, wgs, sink), reps)
+                rows.append({"mode": ("registers", "direct-to-LDS")[mode], "workgroups": wgs,
+                             "us": round(ms * 1e3, 3), "GBps": round(nbytes / ms / 1e6, 1)})
+        best = max(rows, key=lambda r: r["GBps"])
+        out[name] = {"bytes": nbytes, "buffers_rotated": nbuf, "launches_per_graph": reps, "results": rows,
+                     "best_GBps": best["GBps"], "best": f"{best['mode']}, {best['workgroups']} workgroups",
+                     "frac_of_8TBps": round(best["GBps"] / PEAK["hbm_GBps"], 4)}
+        del buf
+        t.cuda.empty_cache()
+    b.read_ceiling_c4 = out["c4_weight_copy"]["best_GBps"]
+    return out
+
+
 def calib_copy(b: Bench) -> dict:
     """A plain device copy of CALIB_BYTES, for scaling the --pmc traffic
     counters (its algorithmic traffic is CALIB_BYTES read + CALIB_BYTES written)."""
@@ -689,10 +732,11 @@ def workload_table(b, args, cpu: bool):
     return [
         ("c5_int8", lambda: bench_c5(b, 8, max(args.steps, 20), max(args.warmup, 3), cpu)),
         ("c4_int4_m1_fp32", lambda: bench_c4(b, 72, 1, F, cpu)),
+        ("c4_int4_m1_bf16", lambda: bench_c4(b, 72, 1, H, cpu)),
         ("c4_int4_m16_fp32", lambda: bench_c4(b, 72, 16, F, cpu)),
-        ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, H, False)),
+        ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, H, cpu)),
         ("c4_int4_m64_fp32", lambda: bench_c4(b, 72, 64, F, cpu)),
-        ("c4_int4_m64_bf16", lambda: bench_c4(b, 72, 64, H, False)),
+        ("c4_int4_m64_bf16", lambda: bench_c4(b, 72, 64, H, cpu)),
         ("c1", lambda: bench_c1(b, args.reps, cpu)),
         ("c2", lambda: bench_c2(b, args.reps, cpu)),
         ("c3", lambda: bench_c3(b, 50, cpu)),
@@ -824,7 +868,8 @@ def main() -> int:
         return 2
 
     if args.list:
-        print("\n".join(["c5_int4 (headline)", "hbm_ceiling"] + [n for n, _ in workload_table(None, args, False)]))
+        print("\n".join(["c5_int4 (headline)", "hbm_ceiling", "hbm_read_ceiling"] +
+                        [n for n, _ in workload_table(None, args, False)]))
         return 0
     import torch
     if not torch.cuda.is_available():
@@ -872,6 +917,10 @@ def main() -> int:
     if want("hbm_ceiling") or not only:
         log("[bench] hbm ceiling (stream copy)")
         out["hbm_ceiling"] = hbm_ceiling(b)
+        torch.cuda.empty_cache()
+    if want("hbm_read_ceiling") or not only or any(n.startswith("c4_") for n in only):
+        log("[bench] hbm read ceiling (read-only probe)")
+        out["hbm_read_ceiling"] = hbm_read_ceiling(b)
         torch.cuda.empty_cache()
 
     if not args.skip_extra:

@@ -1,7 +1,9 @@
 // C-ABI entry points of the GEMM family and the GPU.swift-style wrappers
-// (src/GPU.swift:227-272). Validates the reference's preconditions, then picks
-// the kernel: fp32 MFMA tiles (default), the fp32 GEMV for M <= 4 quantized
-// forwards, or the bf16 MFMA kernels when the context's math mode is BF16.
+// (src/GPU.swift:227-272). Validates the reference's preconditions, then hands
+// the call to the router of its direction (gemm_f32.hip): for quantized
+// forwards the few-row and decode-shaped kernels (int8 / f16 / bf16 MFMA over
+// exact activation pieces), the bf16 prefill kernel in the reduced-precision
+// mode, else the fp32 MFMA tiles; dX and dW always on the fp32 tiles.
 #include "common.hpp"
 
 namespace dgm {

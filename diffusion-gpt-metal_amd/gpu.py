@@ -117,6 +117,12 @@ class GPU:
         self._check(self.lib.dgm_gemmNT_noalloc(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(x),
                                                  _ptr(bias), _ptr(y), M, N, K, qGroup))
 
+    def probeRead(self, src, nbytes: int, mode: int, workgroups: int, sink) -> None:
+        """The bench's read-rate probe (no counterpart in the reference): mode 0
+        16-byte register loads, mode 1 direct-to-LDS loads, `workgroups` 0 = one
+        per CU; `sink` gets one u32 per workgroup."""
+        self._check(self.lib.dgm_probe_read(self.h, _ptr(src), nbytes, mode, workgroups, _ptr(sink)))
+
     def gemmDX(self, bits: int, w, q, scale, dy, dx, M: int, N: int, K: int, qGroup: int) -> None:
         self._check(self.lib.dgm_gemmDX(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(dy),
                                         _ptr(dx), M, N, K, qGroup))

@@ -42,13 +42,17 @@ extern "C" {
 
 /* ---- math modes (dgm_set_math) ------------------------------------------ */
 /* FP32 (default): every result is within max relative error 1e-5 of the
- * float64 product. Quantized forwards with M <= 64 run on int8 MFMA over an
- * exact three-piece int8 split of each activation row; the rest accumulate
- * fp32 products of fp32 operands.
- * BF16: quantized forwards with M <= 64 use a two-piece split; larger M (with
- * K % 128 == 0 and qGroup % 32 == 0) runs on bf16 MFMA with activations
- * rounded to bf16 and weights dequantized to bf16 in LDS, fp32 accumulate.
- * Max relative error <= 1e-2. Backward kernels are fp32 in both modes. */
+ * float64 product. Quantized forwards of a few rows (M <= 4) run on int8
+ * MFMA over an exact split of the activations into four int8 pieces against
+ * a power of two per row and k-range (2^-27 of its maximum); up to M = 64 on
+ * f16 MFMA over two f16 pieces per activation against a power of two per
+ * (row, 128-k block) (2^-22 of each element); the rest accumulate fp32
+ * products of fp32 operands.
+ * BF16: the few-row kernels take two int8 pieces; up to M = 64, int4 codes
+ * meet bf16(x) and int8 codes one f16 piece; larger M (with K % 128 == 0 and
+ * qGroup % 32 == 0) runs on bf16 MFMA with activations rounded to bf16 and
+ * weights dequantized to bf16 in LDS, fp32 accumulate. Max relative error
+ * <= 1e-2. dX and dW are fp32 in both modes. */
 #define DGM_MATH_FP32 0
 #define DGM_MATH_BF16 1
 
@@ -441,6 +445,16 @@ int dgm_tgmt_param(const dgm_tgmt_header* hdr, int64_t i, dgm_param_info* out);
  * (src/DiT.swift:233-250). */
 int dgm_tdit_parse(const void* data, int64_t len, dgm_tdit_header* hdr, int64_t* nparams);
 int dgm_tdit_param(const dgm_tdit_header* hdr, int64_t i, dgm_param_info* out);
+
+/* ---- measurement ----------------------------------------------------------
+ * No counterpart in the reference: the achievable HBM read rate of one
+ * launch, for the bench's roofline. Reads `bytes` (a multiple of 1024) from
+ * `src` (16-byte aligned) in contiguous shares over `workgroups` workgroups
+ * (0: one per CU), mode 0 with 16-byte loads into registers, mode 1 with
+ * 16-byte direct-to-LDS loads, and stores one word per workgroup to `sink`
+ * (device memory of at least 4 * workgroups bytes). */
+int dgm_probe_read(dgm_gpu* g, const void* src, int64_t bytes, int64_t mode, int64_t workgroups,
+                   uint32_t* sink);
 
 #ifdef __cplusplus
 }

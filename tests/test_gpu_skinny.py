@@ -1,12 +1,16 @@
 """GPU parity of the decode-shaped (M <= 64) quantized forward: gemm_nt_i4 /
-gemm_nt_i8 (metal/kernels.metal:152-209) on the int8-MFMA skinny kernel.
+gemm_nt_i8 (metal/kernels.metal:152-209) through dgm_gemmNT, whichever kernel
+the library routes the shape to: the streaming int8-MFMA kernel (a few rows
+whose activation pieces fit LDS, gemm_stream.hip), the int8-MFMA skinny
+kernel (other shapes of up to 3 rows, and shapes outside the decode kernels'
+domain, gemm_skinny.hip), or the f16 / bf16 decode kernels (4 <= M <= 64,
+gemm_decode.hip).
 
 Bars (max|got - ref| / max|ref|, ref = float64 product of the oracle's
 dequantized weights, Check.swift:433-458):
   * fp32 math mode (the default): <= 1e-5;
   * reduced-precision mode (DGM_MATH_BF16): <= 1e-2.
-Every shape here has G % 128 == 0 (int4) or G % 64 == 0 (int8) and M <= 64,
-which is the domain the library routes to the skinny kernel.
+Every shape here has G % 128 == 0 (int4) or G % 64 == 0 (int8) and M <= 64.
 """
 from __future__ import annotations
 
