@@ -36,6 +36,14 @@ struct dgm_gpu {
     // whether the current call draws its workspace from it instead.
     void* scratch = nullptr;
     bool use_scratch = false;
+    // Streams the context was set to (dgm_gpu_set_stream), synchronized by
+    // dgm_gpu_destroy; and whether a kernel with bounded in-workgroup waits
+    // ran since the last dgm_end (which then checks their give-up flag).
+    static constexpr int kMaxStreams = 16;
+    hipStream_t streams[kMaxStreams] = {};
+    int n_streams = 0;
+    bool many_streams = false;   // more than kMaxStreams: destroy waits for the device
+    bool spin_waits = false;
 };
 
 namespace dgm {
@@ -57,6 +65,10 @@ int check_launch(dgm_gpu* g, const char* name);
 void* workspace(dgm_gpu* g, size_t bytes);
 // The status a caller returns when workspace() gave nullptr.
 int ws_error(dgm_gpu* g);
+// After a synchronize: records an error on g if a decode kernel gave up a
+// bounded in-workgroup wait since the last check (gemm_decode.hip), and
+// clears the device's flag.
+void decode_wait_check(dgm_gpu* g);
 // Bytes of the static device scratch behind dgm_gemmNT_noalloc.
 constexpr size_t kScratchBytes = size_t(8) << 20;
 

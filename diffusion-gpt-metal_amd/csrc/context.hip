@@ -146,8 +146,14 @@ int dgm_gpu_create(dgm_gpu** out) {
 
 void dgm_gpu_destroy(dgm_gpu* g) {
     if (!g) return;
+    // Work queued by this context may still use its workspace: wait for the
+    // streams it launched on (not the whole device, where another thread may
+    // be capturing a graph).
     if (g->stream) (void)hipStreamSynchronize(g->stream);
-    (void)hipDeviceSynchronize();   // any stream or graph may still use a workspace
+    if (g->own_stream && g->own_stream != g->stream) (void)hipStreamSynchronize(g->own_stream);
+    for (int i = 0; i < g->n_streams; ++i)
+        if (g->streams[i] != g->stream) (void)hipStreamSynchronize(g->streams[i]);
+    if (g->many_streams) (void)hipDeviceSynchronize();
     if (g->ws) (void)hipFree(g->ws);
     for (int i = 0; i < g->n_retired; ++i) (void)hipFree(g->retired[i]);
     if (g->own_stream) (void)hipStreamDestroy(g->own_stream);
@@ -156,7 +162,16 @@ void dgm_gpu_destroy(dgm_gpu* g) {
 
 int dgm_gpu_set_stream(dgm_gpu* g, void* hip_stream) {
     if (!g) return DGM_ERR_ARG;
-    g->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : g->own_stream;
+    hipStream_t s = hip_stream ? static_cast<hipStream_t>(hip_stream) : g->own_stream;
+    if (s != g->own_stream) {
+        bool known = false;
+        for (int i = 0; i < g->n_streams; ++i) known = known || g->streams[i] == s;
+        if (!known) {
+            if (g->n_streams < dgm_gpu::kMaxStreams) g->streams[g->n_streams++] = s;
+            else g->many_streams = true;   // destroy then waits for the whole device
+        }
+    }
+    g->stream = s;
     return DGM_OK;
 }
 
@@ -186,6 +201,8 @@ int dgm_end(dgm_gpu* g) {
     if (e == hipSuccess) e = hipGetLastError();
     if (e != hipSuccess)
         dgm::fail(g, DGM_ERR_HIP, "HIP error after %s: %s", g->last_kernel, hipGetErrorString(e));
+    else if (g->spin_waits)
+        dgm::decode_wait_check(g);
     return g->first_err;
 }
 

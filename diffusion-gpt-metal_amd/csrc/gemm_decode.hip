@@ -63,7 +63,12 @@
 #include "common.hpp"
 #include "decode_codes.hpp"
 
+#include <atomic>
 #include <type_traits>
+
+// Set (to 1) by a decode workgroup whose bounded hand-over wait gave up;
+// read and cleared by dgm_end (decode_wait_check). One per device.
+__device__ uint32_t g_wait_gave_up;
 
 namespace {
 
@@ -209,6 +214,7 @@ struct DecArgs {
     int M, N, K, groups, gshift, rowb, nchunk, has_bias;
     int mtp;     // row tiles of the prepared pieces and exponents
     int mt0;     // first row tile this launch handles (its MT tiles)
+    int spin;    // rounds of every bounded hand-over wait (decode_small_kernel)
 };
 
 // The load schedule of a compute wave. Step s (one MFMA step of 32 k)
@@ -563,7 +569,8 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
 // its slot's count when it has read an interval, and the stream wave refills
 // a slot only when all eight waves have read it. A wave's LDS operations are
 // performed in issue order, so a count raised after a wave's reads is seen
-// only after those reads. Every wait is bounded (DS_SPIN rounds of s_sleep):
+// only after those reads. Every wait is bounded (DS_SPIN rounds of s_sleep,
+// unless the test hook dgm_debug_wait_limit sets fewer):
 // a fault in this protocol gives wrong results, never a hang.
 //
 // Reduced-precision int4 (one piece) runs on bf16 instead: x rounded to bf16
@@ -623,11 +630,19 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
     if (threadIdx.x < 4) cnt[threadIdx.x] = 0u;
     __syncthreads();
     auto wait_for = [&](int i, uint32_t want) {
+        bool met = false;
 #pragma nounroll
-        for (int spin = 0; spin < DS_SPIN; ++spin) {
-            if (__builtin_amdgcn_readfirstlane(cnt[i]) >= want) break;
+        for (int spin = 0; spin < a.spin; ++spin) {
+            if (__builtin_amdgcn_readfirstlane(cnt[i]) >= want) {
+                met = true;
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
+        // A wait that gave up is reported (dgm_end returns an error): the
+        // flag is set by a vector atomic, one lane's value non-zero.
+        if (!met) __hip_atomic_fetch_or(&g_wait_gave_up, uint32_t(lane == 0), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("" ::: "memory");
     };
 
@@ -886,9 +901,16 @@ __global__ __launch_bounds__(DS_THREADS, 1) void decode_small_kernel(DecArgs a, 
     }
 }
 
+// Rounds of every bounded hand-over wait; the test hook dgm_debug_wait_limit
+// lowers it to force a give-up (the kernels still end normally).
+std::atomic<int> g_wait_limit{DS_SPIN};
+
 template <int BITS, int P>
-int launch_decode_small(dgm_gpu* g, const DecArgs& a, const float* X) {
+int launch_decode_small(dgm_gpu* g, const DecArgs& a0, const float* X) {
     auto kern = decode_small_kernel<BITS, P>;
+    DecArgs a = a0;
+    a.spin = g_wait_limit.load();
+    g->spin_waits = true;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, DS_LDS);
     if (e != hipSuccess)
@@ -970,6 +992,20 @@ int decode_dispatch(dgm_gpu* g, DecArgs& a, const float* X) {
 
 namespace dgm {
 
+void decode_wait_check(dgm_gpu* g) {
+    g->spin_waits = false;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return;
+    if (cur != g->device && hipSetDevice(g->device) != hipSuccess) return;
+    uint32_t flag = 0;
+    if (hipMemcpyFromSymbol(&flag, HIP_SYMBOL(g_wait_gave_up), sizeof(flag)) == hipSuccess && flag != 0) {
+        const uint32_t zero = 0;
+        (void)hipMemcpyToSymbol(HIP_SYMBOL(g_wait_gave_up), &zero, sizeof(zero));
+        fail(g, DGM_ERR_HIP, "a decode kernel gave up a bounded in-workgroup wait: its results are not valid");
+    }
+    if (cur != g->device) (void)hipSetDevice(cur);
+}
+
 // The decode kernel's domain: quantized weights, 1 <= M <= 64, blocks inside
 // groups (G a multiple of 128 for int4, 64 for int8), whole chunks (K a
 // multiple of 256 / 128), 32-bit byte offsets, aligned buffers.
@@ -1011,3 +1047,11 @@ int decode_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const fl
 }
 
 }  // namespace dgm
+
+// Test hook (no counterpart in the reference): bounds every hand-over wait of
+// the decode kernels to `spins` rounds; 0 restores the default bound.
+extern "C" int dgm_debug_wait_limit(int64_t spins) {
+    if (spins < 0 || spins > DS_SPIN) return DGM_ERR_ARG;
+    g_wait_limit.store(spins ? int(spins) : DS_SPIN);
+    return DGM_OK;
+}

@@ -73,6 +73,12 @@ typedef struct dgm_gpu dgm_gpu;
 /* GPU.init (src/GPU.swift:118-156): binds the current HIP device and creates
  * the context's own stream. */
 int dgm_gpu_create(dgm_gpu** out);
+/* Waits for the work queued on the context's own stream and on every stream
+ * it was set to (so those must still exist; after more than 16 distinct
+ * streams, for the whole device), then frees its workspace. Graphs captured
+ * from calls on the context read that workspace: they must not be replayed
+ * after the context is destroyed. Other streams are not synchronized, so a
+ * capture in progress elsewhere is undisturbed. */
 void dgm_gpu_destroy(dgm_gpu* g);
 /* Use a caller-owned stream (e.g. a framework's current stream) instead of the
  * context's own; NULL restores the context's stream. */
@@ -85,7 +91,11 @@ int dgm_get_math(const dgm_gpu* g);
 int dgm_begin(dgm_gpu* g);
 /* GPU.end (src/GPU.swift:168-180): waits for the region's work and returns the
  * first error of the region (the reference prints it with lastKernel and
- * exits; callers turn a nonzero status into their own fatal error). */
+ * exits; callers turn a nonzero status into their own fatal error). This
+ * includes DGM_ERR_HIP when a decode kernel of the region gave up one of its
+ * bounded in-workgroup waits, whose results are then not valid (the flag is
+ * per device: with several contexts on one device, the first end() that
+ * follows reports it). */
 int dgm_end(dgm_gpu* g);
 /* GPU.lastKernel (src/GPU.swift:99): name of the last dispatched kernel. */
 const char* dgm_last_kernel(const dgm_gpu* g);
@@ -455,6 +465,13 @@ int dgm_tdit_param(const dgm_tdit_header* hdr, int64_t i, dgm_param_info* out);
  * (device memory of at least 4 * workgroups bytes). */
 int dgm_probe_read(dgm_gpu* g, const void* src, int64_t bytes, int64_t mode, int64_t workgroups,
                    uint32_t* sink);
+
+/* ---- test hook -------------------------------------------------------------
+ * No counterpart in the reference: bounds every in-workgroup hand-over wait of
+ * the decode kernels to `spins` rounds (0 restores the default), so that a
+ * test can force a wait to give up and check that dgm_end reports it. The
+ * kernels still run to their end; only their results are invalid. */
+int dgm_debug_wait_limit(int64_t spins);
 
 #ifdef __cplusplus
 }

@@ -44,3 +44,34 @@ def test_one_launch_repeatable(gpu, dgm, orc):
     for _ in range(3):
         y1 = _forward(gpu, dgm, 4, q, s, x, None, M, N, K, G, dgm.DGM_MATH_FP32)
         assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+
+
+def test_wait_give_up_is_reported(gpu, dgm, orc):
+    """A bounded in-workgroup hand-over wait that gives up (forced by the test
+    hook: one round per wait) makes dgm_end fail instead of handing back
+    invalid results as if they were good; the kernel itself still ends. With
+    the default bound restored the same call is exact again and dgm_end
+    succeeds (the device flag was cleared by the failing end)."""
+    M, N, K, G = 16, 4096, 4096, 128
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    q, s = _quantize(gpu, to_dev(w), N, K, G, 4)
+    ref = _ref(orc, q, s, x, None, M, N, K, G, 4)
+    lib = dgm.load_library()
+    reported = False
+    try:
+        assert lib.dgm_debug_wait_limit(1) == dgm.DGM_OK
+        for _ in range(5):   # one round per wait: some wait gives up in practice on the first call
+            try:
+                _forward(gpu, dgm, 4, q, s, x, None, M, N, K, G, dgm.DGM_MATH_FP32)
+            except dgm.DgmError as e:
+                assert e.code == dgm.DGM_ERR_HIP
+                assert "gave up" in gpu.lastError
+                reported = True
+                break
+    finally:
+        assert lib.dgm_debug_wait_limit(0) == dgm.DGM_OK
+    assert reported
+    y = _forward(gpu, dgm, 4, q, s, x, None, M, N, K, G, dgm.DGM_MATH_FP32)
+    assert rel_err(y, ref) <= 1e-5

@@ -6,8 +6,9 @@ static device scratch, called through the C ABI.
   nothing (fp32 tiles), two calls in a row, the second with a smaller input,
   return exactly dgm_gemmNT's bytes.
 * On a fresh context the call can be captured in a HIP graph (nothing to
-  allocate), and every replay, with eager work between replays, matches the
-  eager result.
+  allocate) on the staging paths (M = 64 decode pieces, bf16 prefill), and
+  every replay, with eager work between replays, matches the eager result;
+  under the same capture the regular entry point refuses.
 * A call that needs more scratch than the library holds fails with
   DGM_ERR_UNSUPPORTED and leaves its output untouched.
 """
@@ -72,25 +73,49 @@ def test_matches_gemmNT_twice(gpu, dgm, math, bits, first, second):
         assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (math, bits, M, N, K, G)
 
 
-def test_captured_on_a_fresh_context(dgm, orc, torch_cuda):
+# Shapes whose forward stages data: the decode kernels' prepared activation
+# pieces (16 < M <= 64) and the bf16 prefill path's bf16 copy of X.
+CAPTURED = [
+    ("fp32", 4, (64, 512, 2048, 128)),
+    ("bf16", 4, (512, 512, 1024, 128)),
+]
+
+
+@pytest.mark.parametrize("math,bits,shape", CAPTURED)
+def test_captured_on_a_fresh_context(dgm, orc, torch_cuda, math, bits, shape):
+    """On a fresh context (empty workspace) the call is captured in a HIP
+    graph and every replay, with eager work between replays, matches the
+    eager dgm_gemmNT result bitwise; under the same capture, dgm_gemmNT on a
+    second fresh context refuses (its workspace would have to grow), which is
+    what the static scratch makes unnecessary."""
     torch = torch_cuda
+    mode = dgm.DGM_MATH_FP32 if math == "fp32" else dgm.DGM_MATH_BF16
+    M, N, K, G = shape
     stream = torch.cuda.Stream()
-    g = dgm.GPU(stream=stream)   # empty workspace: the regular entry would have to allocate
+    g = dgm.GPU(stream=stream)
+    g2 = dgm.GPU(stream=stream)
+    ref_ctx = dgm.GPU(stream=stream)
     try:
-        M, N, K, G = 16, 512, 2048, 128
-        x, q, s, _ = _case(g, M, N, K, G, 4, 5)
+        for c in (g, g2, ref_ctx):
+            c.set_math(mode)
+        x, q, s, bias = _case(ref_ctx, M, N, K, G, bits, 5)
         y = torch.zeros(M * N, device="cuda")
         ref = torch.zeros(M * N, device="cuda")
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             g.begin()
-            g.gemmNT_noalloc(4, None, q, s, x, None, y, M, N, K, G)
+            g.gemmNT_noalloc(bits, None, q, s, x, bias, y, M, N, K, G)
+            g2.begin()
+            with pytest.raises(dgm.DgmError) as e:
+                g2.gemmNT(bits, None, q, s, x, bias, y, M, N, K, G)
+            assert e.value.code == dgm.DGM_ERR_UNSUPPORTED
         with torch.cuda.stream(stream):
-            g.begin()
-            g.gemmNT(4, None, q, s, x, None, ref, M, N, K, G)
-            g.end()
+            ref_ctx.begin()
+            ref_ctx.gemmNT(bits, None, q, s, x, bias, ref, M, N, K, G)
+            ref_ctx.end()
         want = from_dev(ref)
+        assert np.all(np.isfinite(want))
         for _ in range(3):
             y.fill_(float("nan"))
             torch.cuda.synchronize()
@@ -101,7 +126,8 @@ def test_captured_on_a_fresh_context(dgm, orc, torch_cuda):
         del graph
     finally:
         torch.cuda.synchronize()
-        g.close()
+        for c in (g, g2, ref_ctx):
+            c.close()
 
 
 def test_too_large_is_refused(gpu, dgm):
