@@ -219,15 +219,15 @@ struct DecArgs {
 
 // The load schedule of a compute wave. Step s (one MFMA step of 32 k)
 // issues, in this order: the MT * P activation fragments of step s + D;
-// when step s + D starts a block, the block's 4 scale loads and MT exponent
-// loads. Then it waits for everything issued at step s - D. The prologue
+// when step s + D starts a block, the block's 4 scale loads (none when the
+// scales are in LDS) and MT exponent loads. Then it waits for everything issued at step s - D. The prologue
 // issues steps -D .. -1's loads, so the count depends only on s % SPC. The
 // weight stream is issued by another wave, whose counter it does not share.
-template <int BITS, int MT, int P, int D>
+template <int BITS, int MT, int P, int D, bool SL>
 struct Schedule {
     using SH = DecShape<BITS>;
     static constexpr bool BF = BITS == 4 && P == 1;
-    static constexpr int NA = 4 + MT;    // block loads: 4 scales, MT exponent or offset-term loads
+    static constexpr int NA = (SL ? 0 : 4) + MT;   // block loads: 4 scales (unless in LDS), MT exponent or offset-term loads
     static constexpr int issued(int i) { return MT * P + ((i + D) % SH::SPB == 0 ? NA : 0); }
     static constexpr int wait(int i) {     // vmcnt before computing step position i
         int n = 0;
@@ -246,10 +246,14 @@ struct Schedule {
 // half the accumulators, which leaves registers for a deeper activation
 // prefetch. One barrier per interval: interval t is in LDS and every compute
 // wave is done with interval t - 1, whose slot the producer then refills.
-template <int BITS, int MT, int P, int D, int MW>
+// With SL the producer also moves the workgroup's scales once (after interval
+// 0), transposed to [group][64 columns] behind the ring: a compute wave then
+// reads a block's 16 columns from LDS (16 consecutive words: no bank
+// conflict) instead of gathering them from 16 rows in HBM.
+template <int BITS, int MT, int P, int D, int MW, bool SL>
 __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecArgs a) {
     using SH = DecShape<BITS>;
-    using SC = Schedule<BITS, MT, P, D>;
+    using SC = Schedule<BITS, MT, P, D, SL>;
     constexpr bool BF = SC::BF;   // reduced-precision int4: bf16 fragments, offset codes
     using XF = std::conditional_t<BF, bf16x8, f16x8>;
     static_assert(D >= 1 && D <= SH::SPB, "prefetch depth: at most one block ahead");
@@ -303,12 +307,26 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
             }
         };
         static_assert(DEC_SLOTS == 4, "the waits below count at most two intervals ahead");
-        for (int t = 0; t < DEC_SLOTS - 1 && t < T; ++t) dma_interval(t);
+        dma_interval(0);
+        if constexpr (SL) {
+            // Scales: one 4-byte gather per group, lane l = row n0 + l
+            // (rows past N re-read row N - 1).
+            const uint32_t srow = uint32_t(min(n0 + lane, a.N - 1)) * uint32_t(a.groups) * 4u;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+            for (int g = 0; g < a.groups; ++g)
+                asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds0 + DEC_LDS + g * 256),
+                             "v"(srow + 4u * uint32_t(g)), "s"(a.S)
+                             : "memory", "m0");
+#pragma clang diagnostic pop
+        }
+        for (int t = 1; t < DEC_SLOTS - 1 && t < T; ++t) dma_interval(t);
         for (int t = 0; t < T; ++t) {
             // Interval t has landed once at most `ahead` newer intervals (32
             // loads each, issued after it) are in flight; no interval past T
             // is ever issued. The counter holds at most 63, so with two ahead
-            // this also waits for the first load of interval t + 1.
+            // this also waits for the first load of interval t + 1. The
+            // scales, issued between intervals 0 and 1, have landed at t = 0.
             const int ahead = min(T - 1 - t, DEC_SLOTS - 2);
             if (ahead >= 2)
                 asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
@@ -356,11 +374,15 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
     auto load_blk = [&](int b, int slot) {   // this wave's block b (clamped)
         const int bb = b < 2 * cnt ? b : 2 * cnt - 1;
         const int gblk = 2 * (kw + 4 * iv(bb >> 1)) + (bb & 1);
-        const uint32_t g = uint32_t(gblk) >> a.gshift;
+        if constexpr (!SL) {
+            const uint32_t g = uint32_t(gblk) >> a.gshift;
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            const uint32_t n = uint32_t(min(n0 + 16 * ct + c, a.N - 1));
-            asm volatile("global_load_dword %0, %1, %2" : "=v"(bs[slot][ct]) : "v"((n * a.groups + g) * 4u), "s"(a.S));
+            for (int ct = 0; ct < 4; ++ct) {
+                const uint32_t n = uint32_t(min(n0 + 16 * ct + c, a.N - 1));
+                asm volatile("global_load_dword %0, %1, %2"
+                             : "=v"(bs[slot][ct])
+                             : "v"((n * a.groups + g) * 4u), "s"(a.S));
+            }
         }
         if constexpr (BF) {
 #pragma unroll
@@ -424,6 +446,12 @@ __global__ __launch_bounds__(64 * (DEC_KW * MW + 1), 1) void decode_kernel(DecAr
                     const int r = 16 * ct + c;
                     const int sl = (4 * hb + q) ^ (r & 7);
                     wc[ct] = *reinterpret_cast<const u32x4*>(cs + r * 128 + sl * 16);
+                }
+                if constexpr (SL) {
+                    const int g = (2 * (kw + 4 * iv(j)) + hb) >> a.gshift;
+                    const float* sc = reinterpret_cast<const float*>(smem + DEC_LDS) + g * 64 + c;
+#pragma unroll
+                    for (int ct = 0; ct < 4; ++ct) bs[hb][ct] = sc[16 * ct];
                 }
             }
             // B fragments of this step and the MFMAs.
@@ -920,16 +948,27 @@ int launch_decode_small(dgm_gpu* g, const DecArgs& a0, const float* X) {
     return DGM_OK;
 }
 
-template <int BITS, int MT, int P, int D, int MW = 1>
-int launch_decode(dgm_gpu* g, const DecArgs& a) {
-    auto kern = decode_kernel<BITS, MT, P, D, MW>;
+// Scales of the workgroup's 64 rows behind the weight ring: at most
+// (160 KB - DEC_LDS) / 256 = 128 groups; more keep the per-block gathers.
+constexpr int DEC_SL_MAX = (160 * 1024 - DEC_LDS) / 256;
+
+template <int BITS, int MT, int P, int D, int MW, bool SL>
+int launch_decode_sl(dgm_gpu* g, const DecArgs& a) {
+    auto kern = decode_kernel<BITS, MT, P, D, MW, SL>;
+    const int lds = DEC_LDS + (SL ? 256 * a.groups : 0);
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, DEC_LDS);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess)
-        return dgm::fail(g, DGM_ERR_HIP, "decode: cannot reserve %d bytes of LDS: %s", DEC_LDS, hipGetErrorString(e));
-    hipLaunchKernelGGL(kern, dim3(unsigned((a.N + DEC_COLS - 1) / DEC_COLS)), dim3(64 * (DEC_KW * MW + 1)), DEC_LDS,
+        return dgm::fail(g, DGM_ERR_HIP, "decode: cannot reserve %d bytes of LDS: %s", lds, hipGetErrorString(e));
+    hipLaunchKernelGGL(kern, dim3(unsigned((a.N + DEC_COLS - 1) / DEC_COLS)), dim3(64 * (DEC_KW * MW + 1)), lds,
                        g->stream, a);
     return DGM_OK;
+}
+
+template <int BITS, int MT, int P, int D, int MW = 1>
+int launch_decode(dgm_gpu* g, const DecArgs& a) {
+    return a.groups <= DEC_SL_MAX ? launch_decode_sl<BITS, MT, P, D, MW, true>(g, a)
+                                  : launch_decode_sl<BITS, MT, P, D, MW, false>(g, a);
 }
 
 // The one-launch kernel's domain: M <= 16, the scales of 64 rows in LDS (at

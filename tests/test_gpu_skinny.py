@@ -115,6 +115,26 @@ def test_tiled_decode_many_chunks(gpu, dgm, orc, bits, G, K, M):
     assert worst <= 1e-2, worst
 
 
+@pytest.mark.parametrize("bits,G,K,M", [(4, 128, 8192, 5), (4, 128, 16384, 33), (8, 64, 8192, 64),
+                                        (8, 64, 8704, 20), (4, 128, 16640, 17)])
+def test_tiled_decode_scale_staging(gpu, dgm, orc, bits, G, K, M):
+    """Long K around the limits of the tiled kernel's scale staging: up to 128
+    groups the workgroup's scales sit in LDS, more (136, 130 groups) keep the
+    per-block gathers; M <= 16 with more than 63 groups also lands here."""
+    N = 70
+    rng = np.random.default_rng(M * 13 + K + bits)
+    x = rng.standard_normal(M * K).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    w[5 * K: 6 * K] *= np.float32(40.0)            # one row with much larger scales
+    bias = rng.standard_normal(N).astype(np.float32)
+    q, s = _quantize(gpu, to_dev(w), N, K, G, bits)
+    ref = _ref(orc, q, s, x, bias, M, N, K, G, bits)
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_FP32)
+    assert rel_err(y, ref) <= 1e-5
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16)
+    assert rel_err(y, ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M,N,K,G", [(17, 70, 512, 128), (40, 300, 4096, 128), (64, 129, 1024, 256),
                                      (64, 14336, 4096, 128)])
 def test_tiled_decode_bf16_arithmetic(gpu, dgm, orc, M, N, K, G):
