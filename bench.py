@@ -360,7 +360,7 @@ def bench_c4(b: Bench, reps: int, M: int, math_mode: int, cpu: bool) -> dict:
            "TFLOPs": round(flops / ms / 1e9, 3), "weight_copies_rotated": copies,
            "algorithmic_bytes": nbytes,
            "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
-                                traffic_for(name, ["skinny", "tiled", "decode", "stream"]))}
+                                traffic_for(name, ["skinny", "tiled", "decode", "stream", "slab"]))}
     if b.read_ceiling_c4:
         out["frac_of_read_ceiling"] = round(nbytes / ms / 1e6 / b.read_ceiling_c4, 4)
     if cpu:

@@ -55,7 +55,7 @@ def hipcc() -> str:
 # gemm_bf16.hip): a register spilled while such a load is in flight would be
 # read before the load fills it, so these kernels must not use scratch. The
 # build checks the compiler's resource-usage remarks.
-NO_SCRATCH = {"gemm_decode.hip", "gemm_stream.hip", "gemm_bf16.hip"}
+NO_SCRATCH = {"gemm_decode.hip", "gemm_stream.hip", "gemm_bf16.hip", "gemm_slab.hip"}
 REMARK = "-Rpass-analysis=kernel-resource-usage"
 
 

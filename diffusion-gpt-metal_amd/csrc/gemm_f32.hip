@@ -1557,6 +1557,9 @@ int skinny_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const fl
                const float* bias, float* Y, const dgm_GemmP* p);
 bool bf16_ok(int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
 bool stream_ok(dgm_gpu* g, int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
+bool slab_ok(dgm_gpu* g, int bits, const void* W, const float* X, const float* S, const dgm_GemmP* p);
+int slab_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X, const float* bias, float* Y,
+             const dgm_GemmP* p);
 int stream_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X, const float* bias, float* Y,
                const dgm_GemmP* p);
 int bf16_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
@@ -1568,9 +1571,12 @@ int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const 
     // Decode-shaped quantized forwards stream W once. GEMV-like calls (a few
     // rows) take the int8-MFMA kernel, whose weight unpack is three bit
     // operations per 8 weights and whose activation pieces fill spare MFMA
-    // rows; more rows take f16 MFMA over exact f16 activation pieces
-    // (gemm_decode.hip), or the int8-MFMA kernel outside that domain.
+    // rows; up to 16 rows (8 in the reduced mode) split K over workgroups on
+    // the same arithmetic when the weights are large (gemm_slab.hip); more
+    // rows take f16 MFMA over exact f16 activation pieces (gemm_decode.hip),
+    // or the int8-MFMA kernel outside those domains.
     if (stream_ok(g, bits, W, X, scale, p)) return stream_fwd(g, bits, W, scale, X, bias, Y, p);
+    if (slab_ok(g, bits, W, X, scale, p)) return slab_fwd(g, bits, W, scale, X, bias, Y, p);
     if (skinny_fused_ok(g, bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);
     if (decode_ok(bits, W, X, scale, p)) return decode_fwd(g, bits, W, scale, X, bias, Y, p);
     if (skinny_ok(bits, W, X, p)) return skinny_fwd(g, bits, W, scale, X, bias, Y, p);

@@ -52,7 +52,9 @@ def test_wait_give_up_is_reported(gpu, dgm, orc):
     invalid results as if they were good; the kernel itself still ends. With
     the default bound restored the same call is exact again and dgm_end
     succeeds (the device flag was cleared by the failing end)."""
-    M, N, K, G = 16, 4096, 4096, 128
+    # A shape the one-launch kernel takes (40 workgroups: too few for the
+    # K-sliced kernel).
+    M, N, K, G = 16, 4096, 2048, 128
     rng = np.random.default_rng(11)
     x = rng.standard_normal(M * K).astype(np.float32)
     w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)

@@ -2,7 +2,8 @@
 static device scratch, called through the C ABI.
 
 * On each forward path that stages data (decode pieces at M <= 64 in both
-  math modes, the bf16 prefill path's bf16 copy of X) and on one that stages
+  math modes, the K-sliced kernel's partial sums, the bf16 prefill path's
+  bf16 copy of X) and on one that stages
   nothing (fp32 tiles), two calls in a row, the second with a smaller input,
   return exactly dgm_gemmNT's bytes.
 * On a fresh context the call can be captured in a HIP graph (nothing to
@@ -53,7 +54,7 @@ def _both(gpu, dgm, math, bits, M, N, K, G, seed):
 
 
 # (math, bits, first shape, second shape): decode pieces (fused, prepared,
-# tiled), bf16 prefill, fp32 tiles (no staging).
+# tiled), bf16 prefill, fp32 tiles (no staging), K-sliced partial sums.
 CASES = [
     ("fp32", 4, (16, 1024, 4096, 128), (3, 520, 2048, 128)),
     ("fp32", 8, (64, 700, 2048, 64), (7, 300, 1024, 64)),
@@ -61,6 +62,8 @@ CASES = [
     ("bf16", 4, (1024, 768, 2048, 128), (300, 500, 1024, 32)),
     ("bf16", 8, (512, 512, 1024, 64), (130, 260, 512, 32)),
     ("fp32", 4, (512, 192, 768, 32), (100, 64, 256, 32)),
+    ("fp32", 4, (16, 3600, 4096, 128), (5, 7200, 2048, 128)),
+    ("bf16", 8, (8, 3600, 2048, 64), (4, 3600, 2048, 128)),
 ]
 
 
