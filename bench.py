@@ -334,9 +334,12 @@ def bench_c5(b: Bench, bits: int, steps: int, warmup: int, cpu: bool) -> dict:
     return out
 
 
-def bench_c4(b: Bench, reps: int, M: int, math_mode: int, cpu: bool) -> dict:
+def bench_c4(b: Bench, reps: int, M: int, math_mode: int, cpu: bool, valu: bool = False) -> dict:
     """Decode-shaped int4: K=4096, N=14336, G=128. Weight copies are rotated so
-    that successive launches never find W in the 256 MB Infinity Cache."""
+    that successive launches never find W in the 256 MB Infinity Cache. With
+    valu, the same call on the wave-reduction VALU GEMV probe
+    (dgm_probe_gemv_valu, no bias), the design the MFMA kernels are measured
+    against."""
     N, K, G = C4["N"], C4["K"], C4["G"]
     wq_bytes = N * K // 2 + N * (K // G) * 4
     copies = max(2, -(-512 * 2 ** 20 // wq_bytes))
@@ -347,20 +350,25 @@ def bench_c4(b: Bench, reps: int, M: int, math_mode: int, cpu: bool) -> dict:
     S = [s0] + [s0.clone() for _ in range(copies - 1)]
     x = b.randn(M * K, 1.0)
     y = b.zeros(M * N)
+    if valu:
+        call = lambda i: b.gpu.probeGemvValu(Q[i % copies], S[i % copies], x, y, M, N, K, G)
+    else:
+        call = lambda i: b.gpu.gemmNT(4, None, Q[i % copies], S[i % copies], x, None, y, M, N, K, G)
     with b.math(math_mode):
-        ms = b.time_launches(lambda i: b.gpu.gemmNT(4, None, Q[i % copies], S[i % copies], x, None, y,
-                                                    M, N, K, G), reps)
+        ms = b.time_launches(call, reps)
     flops = 2 * M * N * K
     nbytes = wq_bytes + 4 * (M * K + M * N)
     mode = "fp32" if math_mode == b.dgm.DGM_MATH_FP32 else "bf16"
     del Q, S
-    name = f"c4_int4_m{M}_{mode}"
-    out = {"kernel": "gemm_nt_i4", "math": mode, "shape": f"M={M} K=4096 N=14336 int4 G=128",
+    name = f"c4_valu_gemv_m{M}" if valu else f"c4_int4_m{M}_{mode}"
+    keys = ["gemv_valu"] if valu else ["skinny", "tiled", "decode", "stream", "slab"]
+    out = {"kernel": "probe_gemv_valu" if valu else "gemm_nt_i4", "math": mode,
+           "shape": f"M={M} K=4096 N=14336 int4 G=128",
            "us": round(ms * 1e3, 3), "GBps": round(nbytes / ms / 1e6, 2),
            "TFLOPs": round(flops / ms / 1e9, 3), "weight_copies_rotated": copies,
            "algorithmic_bytes": nbytes,
            "roofline": roofline(nbytes / ms / 1e6, PEAK["hbm_GBps"], "GB/s", "hbm",
-                                traffic_for(name, ["skinny", "tiled", "decode", "stream", "slab"]))}
+                                traffic_for(name, keys))}
     if b.read_ceiling_c4:
         out["frac_of_read_ceiling"] = round(nbytes / ms / 1e6 / b.read_ceiling_c4, 4)
     if cpu:
@@ -737,6 +745,8 @@ def workload_table(b, args, cpu: bool):
         ("c4_int4_m16_bf16", lambda: bench_c4(b, 72, 16, H, cpu)),
         ("c4_int4_m64_fp32", lambda: bench_c4(b, 72, 64, F, cpu)),
         ("c4_int4_m64_bf16", lambda: bench_c4(b, 72, 64, H, cpu)),
+        ("c4_valu_gemv_m1", lambda: bench_c4(b, 72, 1, F, False, valu=True)),
+        ("c4_valu_gemv_m16", lambda: bench_c4(b, 72, 16, F, False, valu=True)),
         ("c1", lambda: bench_c1(b, args.reps, cpu)),
         ("c2", lambda: bench_c2(b, args.reps, cpu)),
         ("c3", lambda: bench_c3(b, 50, cpu)),

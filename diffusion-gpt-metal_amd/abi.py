@@ -166,6 +166,7 @@ PROTOTYPES = {
     "dgm_gemmNT": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmNT_noalloc": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_probe_read": (_I, [_P, _P, _I64, _I64, _I64, _P]),
+    "dgm_probe_gemv_valu": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_debug_wait_limit": (_I, [_I64]),
     "dgm_gemmDX": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmDW": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),

@@ -123,6 +123,11 @@ class GPU:
         per CU; `sink` gets one u32 per workgroup."""
         self._check(self.lib.dgm_probe_read(self.h, _ptr(src), nbytes, mode, workgroups, _ptr(sink)))
 
+    def probeGemvValu(self, q, scale, x, y, M: int, N: int, K: int, qGroup: int) -> None:
+        """The bench's comparison GEMV (no counterpart in the reference): int4
+        codes, fp32 VALU FMAs with a wave reduction, M = 1 or 16, no bias."""
+        self._check(self.lib.dgm_probe_gemv_valu(self.h, _ptr(q), _ptr(scale), _ptr(x), _ptr(y), M, N, K, qGroup))
+
     def gemmDX(self, bits: int, w, q, scale, dy, dx, M: int, N: int, K: int, qGroup: int) -> None:
         self._check(self.lib.dgm_gemmDX(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(dy),
                                         _ptr(dx), M, N, K, qGroup))

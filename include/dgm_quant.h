@@ -465,6 +465,12 @@ int dgm_tdit_param(const dgm_tdit_header* hdr, int64_t i, dgm_param_info* out);
  * (device memory of at least 4 * workgroups bytes). */
 int dgm_probe_read(dgm_gpu* g, const void* src, int64_t bytes, int64_t mode, int64_t workgroups,
                    uint32_t* sink);
+/* No counterpart in the reference: a wave-reduction VALU GEMV over int4 codes
+ * (Y[M,N] = X[M,K] . dequant(Wq)^T, fp32 FMAs, no bias), the design the
+ * library's MFMA decode kernels are measured against. M is 1 or 16; K and
+ * qGroup are multiples of 32; Wq and X 16-byte aligned. */
+int dgm_probe_gemv_valu(dgm_gpu* g, const uint8_t* Wq, const float* scale, const float* X, float* Y, int64_t M,
+                        int64_t N, int64_t K, int64_t qGroup);
 
 /* ---- test hook -------------------------------------------------------------
  * No counterpart in the reference: bounds every in-workgroup hand-over wait of
