@@ -1005,17 +1005,26 @@ void launch_fwd_lds(const GemmArgs& a, int num_cus, hipStream_t st) {
 // columns of dX; each of its 4 waves owns 16 columns over the whole
 // contraction. The 16 x N block of dY goes to LDS as in the forward (direct
 // loads, swizzled slots). The weight strip W[0:N, k0:k0+64] is read with
-// 16-byte loads (consecutive lanes take consecutive rows n), dequantized once
-// per workgroup (code * scale, the reference's rounding) and written TRANSPOSED
-// to LDS as wt[k][n], rows padded to N + 4 floats, so a lane's 4 consecutive
-// contraction indices are one 16-byte LDS read and the 16 rows an MFMA operand
-// touches fall in distinct banks. Contraction order inside a 64-wide stage is
-// the same permutation for both operands (lane q takes 16q .. 16q+15).
+// 16-byte loads (consecutive lanes take consecutive rows n) and written
+// TRANSPOSED to LDS, [k][n], so that a lane's 4 consecutive contraction
+// indices are one LDS read: dequantized once per workgroup (code * scale, the
+// reference's rounding) as floats, rows padded to N + 4; or, with CODED, as
+// one offset-binary byte per code (code + 8, code + 128; rows padded to N + 12
+// bytes: at most two lanes per bank) with the scales per 16-k quarter of the
+// strip as [quarter][n], each code dequantized when its operand is read,
+// (byte - offset) * scale, the same single rounding. CODED holds 13 KB of
+// codes instead of 49 KB of floats at N = 192: the backward pair, whose dX
+// tiles otherwise leave room for only two workgroups per CU, takes it (c2:
+// 8.2-8.5 us against 8.6-8.8); alone, the dequantization in the MFMA loop
+// costs more than it saves (6.5-6.7 us against 5.9-6.1).
+// Contraction order inside a 64-wide stage is the same permutation for both
+// operands (lane q takes 16q .. 16q+15).
 // Body of one dX tile; `blk` is the workgroup's index within its own grid
-// (dealt round-robin to the 8 XCDs), sm4 its LDS (dx_lds_bytes(N)).
-template <int BITS>
+// (dealt round-robin to the 8 XCDs), sm4 its LDS (dx_lds_bytes(CODED, N)).
+template <int BITS, bool CODED = false>
 __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int tiles_j, int per_xcd, int blk,
                                             float4* sm4) {
+    static_assert(!CODED || BITS != 32, "codes only");
     const int t = (blk & 7) * per_xcd + (blk >> 3);
     if (t >= tiles_i * tiles_j) return;
     const int ti = t / tiles_j, tj = t - ti * tiles_j;
@@ -1025,8 +1034,11 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     const int r16 = lane & 15, q4 = lane >> 4;
     const int spr = N >> 2;
     float4* ys = sm4;                                          // [16][spr], swizzled
-    float* wt = reinterpret_cast<float*>(sm4 + 16 * spr);     // [64][N + 4]
+    float* wt = reinterpret_cast<float*>(sm4 + 16 * spr);     // fp32: [64][N + 4]
     const int wld = N + 4;
+    uint8_t* wc = reinterpret_cast<uint8_t*>(sm4 + 16 * spr);  // codes: [64][N + 12] bytes
+    const int wldb = N + 12;
+    float* sc = reinterpret_cast<float*>(wc + 64 * wldb);      // codes: scales [4 quarters][N]
 
     // -- weight strip: 16-byte units. 32 consecutive lanes take 32 consecutive
     // rows n of one part of the strip, the next 32 lanes the next part, so a
@@ -1072,19 +1084,28 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
         if (idx >= units) break;
         const int grp = idx >> 5;
         const int n = (grp / UPR) * 32 + (idx & 31), part = grp % UPR;
-        float* dst = wt + (part * CPU) * wld + n;
         const uint32_t w4[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
         if constexpr (BITS == 32) {
+            float* dst = wt + (part * CPU) * wld + n;
 #pragma unroll
             for (int e = 0; e < 4; ++e) dst[e * wld] = __uint_as_float(w4[e]);
-        } else if constexpr (BITS == 8) {
+        } else if constexpr (!CODED) {
+            float* dst = wt + (part * CPU) * wld + n;
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                dst[e * wld] = float(int(__builtin_amdgcn_sbfe(int(w4[e >> 2]), 8 * (e & 3), 8))) * ws[u];
+            for (int e = 0; e < CPU; ++e)
+                dst[e * wld] = float(int(BITS == 8 ? __builtin_amdgcn_sbfe(int(w4[e >> 2]), 8 * (e & 3), 8)
+                                                   : __builtin_amdgcn_sbfe(int(w4[e >> 3]), 4 * (e & 7), 4))) *
+                               ws[u];
         } else {
+            // Offset binary: a two's-complement nibble (byte) XOR its top bit.
+            uint8_t* dst = wc + (part * CPU) * wldb + n;
 #pragma unroll
-            for (int e = 0; e < 32; ++e)
-                dst[e * wld] = float(int(__builtin_amdgcn_sbfe(int(w4[e >> 3]), 4 * (e & 7), 4))) * ws[u];
+            for (int e = 0; e < CPU; ++e) {
+                const uint32_t b = BITS == 8 ? (w4[e >> 2] >> (8 * (e & 3))) & 0xFFu : (w4[e >> 3] >> (4 * (e & 7))) & 0xFu;
+                dst[e * wldb] = uint8_t(b ^ (BITS == 8 ? 0x80u : 0x8u));
+            }
+#pragma unroll
+            for (int qq = 0; qq < CPU / 16; ++qq) sc[(part * (CPU / 16) + qq) * N + n] = ws[u];
         }
     }
     __syncthreads();
@@ -1092,12 +1113,26 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const float4* yrow = ys + r16 * spr;
     const float* wrow = wt + (wave * 16 + r16) * wld + 16 * q4;
+    const uint8_t* crow = wc + (wave * 16 + r16) * wldb + 16 * q4;   // this lane's k row
+    const float* srow = sc + wave * N + 16 * q4;                      // its quarter's scales
+    constexpr float OFF = BITS == 8 ? 128.0f : 8.0f;
     const int nst = N >> 6;
     for (int st = 0; st < nst; ++st) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const float4 yv = yrow[(st * 16 + 4 * q4 + c) ^ r16];
-            const float4 wv4 = *reinterpret_cast<const float4*>(wrow + st * 64 + 4 * c);
+            float4 wv4;
+            if constexpr (!CODED) {
+                wv4 = *reinterpret_cast<const float4*>(wrow + st * 64 + 4 * c);
+            } else {
+                const uint32_t cb = *reinterpret_cast<const uint32_t*>(crow + st * 64 + 4 * c);
+                const float4 s4 = *reinterpret_cast<const float4*>(srow + st * 64 + 4 * c);
+                // (code + OFF) - OFF is exact; one rounding in the product.
+                wv4.x = (float(cb & 0xFFu) - OFF) * s4.x;
+                wv4.y = (float((cb >> 8) & 0xFFu) - OFF) * s4.y;
+                wv4.z = (float((cb >> 16) & 0xFFu) - OFF) * s4.z;
+                wv4.w = (float(cb >> 24) - OFF) * s4.w;
+            }
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.x, wv4.x, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.y, wv4.y, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.z, wv4.z, acc, 0, 0, 0);
@@ -1140,7 +1175,10 @@ __global__ __launch_bounds__(kThreads) void gemm_dx_lds_kernel(GemmArgs a, int t
     dx_lds_tile<BITS>(a, tiles_i, tiles_j, per_xcd, int(blockIdx.x), sm4);
 }
 
-size_t dx_lds_bytes(int N) { return size_t(16) * N * 4 + size_t(64) * (N + 4) * 4; }
+size_t dx_lds_bytes(bool coded, int N) {
+    const size_t strip = coded ? size_t(64) * (N + 12) + size_t(4) * N * 4 : size_t(64) * (N + 4) * 4;
+    return size_t(16) * N * 4 + strip;
+}
 
 // N % 64 == 0 and N <= 448 (dY block and the transposed strip stay in LDS),
 // K a multiple of the 16-byte unit, a group that holds a whole unit, aligned rows.
@@ -1154,7 +1192,7 @@ bool dx_lds_ok(const GemmArgs& a, int bits, const void* dY, const void* W) {
 
 template <int BITS>
 int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
-    const size_t lds = dx_lds_bytes(a.N);
+    const size_t lds = dx_lds_bytes(false, a.N);
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_dx_lds_kernel<BITS>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -1258,7 +1296,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bwd_pair_kernel(GemmArgs ax, in
     extern __shared__ __align__(16) float4 sm4[];
     const int nx = 8 * per_x;
     if (int(blockIdx.x) < nx) {
-        dx_lds_tile<BITS>(ax, ti, tj, per_x, int(blockIdx.x), sm4);
+        dx_lds_tile<BITS, BITS != 32>(ax, ti, tj, per_x, int(blockIdx.x), sm4);
     } else {
         dw_pair_tile(aw, tn, tk, per_w, int(blockIdx.x) - nx, reinterpret_cast<float (*)[2][16][16]>(sm4));
     }
@@ -1706,7 +1744,7 @@ int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, c
         *fused = true;
         return DGM_OK;
     }
-    const size_t lds = dx_lds_bytes(ax.N);   // >= the 8 KB the dW tiles use (N >= 64)
+    const size_t lds = dx_lds_bytes(bits != 32, ax.N);   // >= the 8 KB the dW tiles use (N >= 64)
     const void* kern = bits == 32 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<32>)
                        : bits == 8 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<8>)
                                    : reinterpret_cast<const void*>(gemm_bwd_pair_kernel<4>);
