@@ -76,6 +76,26 @@ def test_slab_parity(gpu, dgm, orc, bits, G, K, N, M):
     assert worst <= 1e-2, worst
 
 
+@pytest.mark.parametrize("bits,G,K,N,M", [(4, 128, 8192, 3584, 1), (4, 128, 8192, 3584, 3), (4, 512, 4096, 3585, 7),
+                                          (8, 256, 4096, 4000, 12), (8, 64, 512, 14337, 16)])
+def test_slab_more_shapes(gpu, dgm, orc, bits, G, K, N, M):
+    """M = 1 and 3 at K = 8192 (more chunks than the streaming kernel takes),
+    N one row past a multiple of 448, groups spanning a whole slice (G = 512)
+    or half of one (int8 G = 256), two slices at N = 14337."""
+    rng = np.random.default_rng(M * 7 + K + N + bits)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal(N * K) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    q, s = _quantize(gpu, w, N, K, G, bits)
+    ref = x.astype(np.float64) @ _dequant(orc, q, s, N, K, G, bits).astype(np.float64).T + bias.astype(np.float64)
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_FP32)
+    worst = max(rel_err(y[m], ref[m]) for m in range(M))
+    assert worst <= 1e-5, worst
+    y = _forward(gpu, dgm, bits, q, s, x, bias, M, N, K, G, dgm.DGM_MATH_BF16)
+    worst = max(rel_err(y[m], ref[m]) for m in range(M))
+    assert worst <= 1e-2, worst
+
+
 def test_slab_extreme_rows_and_non_finite(gpu, dgm, orc):
     bits, G, K, N, M = 4, 128, 4096, 3600, 8
     rng = np.random.default_rng(11)
