@@ -7,7 +7,8 @@ static device scratch, called through the C ABI.
   nothing (fp32 tiles), two calls in a row, the second with a smaller input,
   return exactly dgm_gemmNT's bytes.
 * On a fresh context the call can be captured in a HIP graph (nothing to
-  allocate) on the staging paths (M = 64 decode pieces, bf16 prefill), and
+  allocate) on the staging paths (M = 64 decode pieces, the K-sliced
+  partial sums, bf16 prefill), and
   every replay, with eager work between replays, matches the eager result;
   under the same capture the regular entry point refuses.
 * A call that needs more scratch than the library holds fails with
@@ -77,9 +78,11 @@ def test_matches_gemmNT_twice(gpu, dgm, math, bits, first, second):
 
 
 # Shapes whose forward stages data: the decode kernels' prepared activation
-# pieces (16 < M <= 64) and the bf16 prefill path's bf16 copy of X.
+# pieces (16 < M <= 64), the K-sliced kernel's partial sums (two launches)
+# and the bf16 prefill path's bf16 copy of X.
 CAPTURED = [
     ("fp32", 4, (64, 512, 2048, 128)),
+    ("fp32", 4, (16, 3600, 4096, 128)),
     ("bf16", 4, (512, 512, 1024, 128)),
 ]
 
