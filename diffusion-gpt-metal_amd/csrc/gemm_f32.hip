@@ -1207,69 +1207,86 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
     return DGM_OK;
 }
 
-// ---- dW with paired columns (M % 64 == 0, N % 2 == 0) ---------------------------
-// dW[n, k] (=|+=) sum_m dY[m, n] * X[m, k]. A workgroup owns 32 rows (n) x 16
+// ---- dW with 2 or 4 columns per lane (M % 64 == 0, N % NP == 0) ------------------
+// dW[n, k] (=|+=) sum_m dY[m, n] * X[m, k]. A workgroup owns 16 NP rows (n) x 16
 // columns (k) of dW; its 4 waves split M and load their operands straight into
-// registers, every load of the wave's range issued before the first MFMA. A
-// lane reads dY[m, n0 + 2i .. n0 + 2i + 1] as one 8-byte load, so 16 lanes cover
-// a whole 128-byte line of a dY row; the even and odd columns feed two MFMA
-// tiles (dW rows n0 + 2r and n0 + 2r + 1). At step s a lane group q uses row
-// m = m0 + q + 4 s. Wave partials are reduced through LDS in a fixed order.
-constexpr int DWP_CH = 8;   // 16-row chunks per wave and round
+// registers, CH 16-row chunks of loads issued before the first MFMA of a round.
+// A lane reads dY[m, n0 + NP i .. n0 + NP i + NP - 1] as one 8-byte (NP = 2) or
+// 16-byte (NP = 4) load, so 16 lanes cover one or two whole 128-byte lines of
+// a dY row; column e of the lane's NP feeds MFMA tile e (dW rows n0 + NP r + e).
+// At step s a lane group q uses row m = m0 + q + 4 s. Wave partials are
+// reduced through LDS in a fixed order. Every dW element is the same chain of
+// MFMAs over the same rows for any NP and CH, so the results are bitwise equal.
+// The backward pairs run NP = 2, CH = 8 (32 x 16 tiles, 125 VGPRs: beside the
+// dX tiles the wider tile measured slower); dW alone runs NP = 4, CH = 4 when
+// N % 4 == 0 (64 x 16 tiles, 110 VGPRs: 5.4 us at c2 / c1 against 6.7 us).
+constexpr int DWP_CH = 8;   // 16-row chunks per wave and round of the paired tiles
 
-// Body of one dW tile; `blk` as in dx_lds_tile, part: 8 KB of LDS.
+// Body of one dW tile; `blk` as in dx_lds_tile, part: NP x 4 KB of LDS. Lanes
+// whose columns pass N load the last NP columns (N % NP == 0, so those lanes'
+// own rows are all >= N) and are never stored.
+template <int NP = 2, int CH = DWP_CH>
 __device__ __forceinline__ void dw_pair_tile(const GemmArgs& a, int tiles_n, int tiles_k, int per_xcd, int blk,
-                                             float (*part)[2][16][16]) {
+                                             float (*part)[NP][16][16]) {
+    static_assert(NP == 2 || NP == 4, "2 or 4 columns per lane");
     const int t = (blk & 7) * per_xcd + (blk >> 3);
     if (t >= tiles_n * tiles_k) return;
     const int tk = t / tiles_n, tn = t - tk * tiles_n;
-    const int n0 = tn * 32, k0 = tk * 16;
+    const int n0 = tn * 16 * NP, k0 = tk * 16;
     const int M = a.M, N = a.N, K = a.K;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
-    const int nc = min(n0 + 2 * r16, N - 2);   // pairs past N: clamped, never stored
+    const int nc = min(n0 + NP * r16, N - NP);
     const int kc = min(k0 + r16, K - 1);
     const float* X = static_cast<const float*>(a.B);
     const int per = M >> 2;
     const int mb = wave * per;
 
-    f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
-    for (int r0 = mb; r0 < mb + per; r0 += 16 * DWP_CH) {
-        float2 av[DWP_CH][4];
-        float bv[DWP_CH][4];
+    f32x4 acc[NP];
 #pragma unroll
-        for (int c = 0; c < DWP_CH; ++c) {
+    for (int e = 0; e < NP; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r0 = mb; r0 < mb + per; r0 += 16 * CH) {
+        float av[CH][4][NP];
+        float bv[CH][4];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
             const int m0 = min(r0 + 16 * c, mb + per - 16);   // past the range: re-read, not computed
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2) {
                 const int m = m0 + q4 + 4 * s2;
-                av[c][s2] = *reinterpret_cast<const float2*>(a.A + size_t(m) * N + nc);
+                const float* src = a.A + size_t(m) * N + nc;
+                if constexpr (NP == 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(src);
+                    av[c][s2][0] = v.x; av[c][s2][1] = v.y; av[c][s2][2] = v.z; av[c][s2][3] = v.w;
+                } else {
+                    const float2 v = *reinterpret_cast<const float2*>(src);
+                    av[c][s2][0] = v.x; av[c][s2][1] = v.y;
+                }
                 bv[c][s2] = X[size_t(m) * K + kc];
             }
         }
         __builtin_amdgcn_sched_barrier(0);   // every load of the round before the first MFMA
 #pragma unroll
-        for (int c = 0; c < DWP_CH; ++c) {
+        for (int c = 0; c < CH; ++c) {
             if (r0 + 16 * c >= mb + per) continue;
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][s2].x, bv[c][s2], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][s2].y, bv[c][s2], acc1, 0, 0, 0);
-            }
+            for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+                for (int e = 0; e < NP; ++e)
+                    acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][s2][e], bv[c][s2], acc[e], 0, 0, 0);
         }
     }
-    // acc_e[r]: dW row n0 + 2 (4 q4 + r) + e, column k0 + r16.
+    // acc[e][r]: dW row n0 + NP (4 q4 + r) + e, column k0 + r16.
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        part[wave][0][4 * q4 + r][r16] = acc0[r];
-        part[wave][1][4 * q4 + r][r16] = acc1[r];
-    }
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < NP; ++e) part[wave][e][4 * q4 + r][r16] = acc[e][r];
     __syncthreads();
-    for (int e = threadIdx.x; e < 32 * 16; e += kThreads) {
-        const int il = e >> 4, j = e & 15;   // il: local dW row 0..31
+    for (int e = threadIdx.x; e < 16 * NP * 16; e += kThreads) {
+        const int il = e >> 4, j = e & 15;   // il: local dW row 0 .. 16 NP - 1
         const int i = n0 + il, k = k0 + j;
         if (i >= N || k >= K) continue;
-        const int rr = il >> 1, par = il & 1;
+        const int rr = il / NP, par = il - rr * NP;
         float v = part[0][par][rr][j];
         v += part[1][par][rr][j];
         v += part[2][par][rr][j];
@@ -1280,9 +1297,10 @@ __device__ __forceinline__ void dw_pair_tile(const GemmArgs& a, int tiles_n, int
     }
 }
 
+template <int NP, int CH>
 __global__ __launch_bounds__(kThreads) void gemm_dw_pair_kernel(GemmArgs a, int tiles_n, int tiles_k, int per_xcd) {
-    __shared__ float part[4][2][16][16];
-    dw_pair_tile(a, tiles_n, tiles_k, per_xcd, int(blockIdx.x), part);
+    __shared__ float part[4][NP][16][16];
+    dw_pair_tile<NP, CH>(a, tiles_n, tiles_k, per_xcd, int(blockIdx.x), part);
 }
 
 // ---- the STE backward pair in one launch ------------------------------------------
@@ -1326,10 +1344,15 @@ bool dw_pair_ok(const GemmArgs& a, const void* dY) {
 }
 
 void launch_dw_pair(const GemmArgs& a, hipStream_t st) {
-    const int tn = int(dgm::ceil_div(a.N, 32)), tk = int(dgm::ceil_div(a.K, 16));
+    const bool four = a.N % 4 == 0 && dgm::aligned(a.A, 16);
+    const int tn = int(dgm::ceil_div(a.N, four ? 64 : 32)), tk = int(dgm::ceil_div(a.K, 16));
     const int64_t nt = int64_t(tn) * tk;
     const int per = int((nt + 7) / 8);
-    hipLaunchKernelGGL(gemm_dw_pair_kernel, dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn, tk, per);
+    if (four)
+        hipLaunchKernelGGL((gemm_dw_pair_kernel<4, 4>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn, tk, per);
+    else
+        hipLaunchKernelGGL((gemm_dw_pair_kernel<2, DWP_CH>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn, tk,
+                           per);
 }
 
 template <int MODE, int BITS, int TM, int TN>

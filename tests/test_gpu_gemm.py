@@ -190,10 +190,11 @@ def test_multiple_of_16_contractions(gpu, orc, M, N, K, G, bits):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 20, 36), (128, 36, 100), (448, 52, 44), (192, 12, 8), (512, 192, 768),
-                                   (64, 4, 4), (320, 100, 260)])
+                                   (64, 4, 4), (320, 100, 260), (128, 30, 48), (256, 66, 20)])
 def test_dw_shapes(gpu, orc, M, N, K):
     """dW / dW += over contractions that are multiples of 64 with ragged output
-    tiles (rows and columns past N or K clamped, never stored)."""
+    tiles (rows and columns past N or K clamped, never stored): four dY columns
+    per lane when N % 4 == 0, two otherwise (N = 30, 66)."""
     import torch
     rng = np.random.default_rng(M + N + K)
     x = rng.standard_normal(M * K).astype(np.float32)
