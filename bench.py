@@ -410,8 +410,8 @@ def bench_c2(b: Bench, reps: int, cpu: bool) -> dict:
            "us_per_step": round(ms_step * 1e3, 3), "TFLOPs": round(3 * gemm / ms_step / 1e9, 3),
            "per_kernel_us": {k: round(v * 1e3, 3) for k, v in per.items()},
            "roofline": roofline(2 * gemm / per["gemm_bwd_i4"] / 1e9, PEAK["fp32_TFLOPs"], "TFLOP/s", "mfma",
-                                traffic_for("c2", ["gemm_bwd_pair_kernel<4>"])),
-           "roofline_kernel": "gemm_bwd_i4 (gemm_bwd_pair_kernel<4>)",
+                                traffic_for("c2", ["gemm_bwd_pair_kernel<4, 2>"])),
+           "roofline_kernel": "gemm_bwd_i4 (gemm_bwd_pair_kernel<4, 2>)",
            "algorithmic_bytes": nbytes,
            "note": "latency-bound shape; fp32 MFMA (157.3 TFLOP/s) is the nearer roof"}
     if cpu:

@@ -1017,26 +1017,32 @@ void launch_fwd_lds(const GemmArgs& a, int num_cus, hipStream_t st) {
 // tiles otherwise leave room for only two workgroups per CU, takes it (c2:
 // 8.2-8.5 us against 8.6-8.8); alone, the dequantization in the MFMA loop
 // costs more than it saves (6.5-6.7 us against 5.9-6.1).
+// RT = 2 gives the workgroup 32 rows (two accumulator tiles per wave on the
+// same weight operands): half the strip loads and conversions per row of dX.
+// The pair takes it when the tiles still fill the CUs (c2: 7.7-7.9 us
+// against 8.4-8.5 us; fewer tiles or a 64-wide contraction lose).
 // Contraction order inside a 64-wide stage is the same permutation for both
-// operands (lane q takes 16q .. 16q+15).
+// operands (lane q takes 16q .. 16q+15), and every dX element is the same
+// chain for either RT.
 // Body of one dX tile; `blk` is the workgroup's index within its own grid
-// (dealt round-robin to the 8 XCDs), sm4 its LDS (dx_lds_bytes(CODED, N)).
-template <int BITS, bool CODED = false>
+// (dealt round-robin to the 8 XCDs), sm4 its LDS (dx_lds_bytes(CODED, N, RT)).
+template <int BITS, bool CODED = false, int RT = 1>
 __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int tiles_j, int per_xcd, int blk,
                                             float4* sm4) {
     static_assert(!CODED || BITS != 32, "codes only");
+    static_assert(RT == 1 || RT == 2, "16 or 32 rows");
     const int t = (blk & 7) * per_xcd + (blk >> 3);
     if (t >= tiles_i * tiles_j) return;
     const int ti = t / tiles_j, tj = t - ti * tiles_j;
-    const int i0 = ti * 16, k0 = tj * 64;
+    const int i0 = ti * 16 * RT, k0 = tj * 64;
     const int N = a.N, K = a.K;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
     const int spr = N >> 2;
-    float4* ys = sm4;                                          // [16][spr], swizzled
-    float* wt = reinterpret_cast<float*>(sm4 + 16 * spr);     // fp32: [64][N + 4]
+    float4* ys = sm4;                                          // [16 RT][spr], swizzled
+    float* wt = reinterpret_cast<float*>(sm4 + 16 * RT * spr);  // fp32: [64][N + 4]
     const int wld = N + 4;
-    uint8_t* wc = reinterpret_cast<uint8_t*>(sm4 + 16 * spr);  // codes: [64][N + 12] bytes
+    uint8_t* wc = reinterpret_cast<uint8_t*>(sm4 + 16 * RT * spr);  // codes: [64][N + 12] bytes
     const int wldb = N + 12;
     float* sc = reinterpret_cast<float*>(wc + 64 * wldb);      // codes: scales [4 quarters][N]
 
@@ -1068,7 +1074,7 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
         }
     }
     // -- dY block via direct-to-LDS loads (slot pos of row r holds global slot pos ^ (r & 15)).
-    const int ninst = (16 * spr) >> 6;
+    const int ninst = (16 * RT * spr) >> 6;
     uint8_t* yb = reinterpret_cast<uint8_t*>(ys);
     for (int ii = wave; ii < ninst; ii += 4) {
         const int L = ii * 64 + lane;
@@ -1110,7 +1116,9 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     }
     __syncthreads();
 
-    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const float4* yrow = ys + r16 * spr;
     const float* wrow = wt + (wave * 16 + r16) * wld + 16 * q4;
     const uint8_t* crow = wc + (wave * 16 + r16) * wldb + 16 * q4;   // this lane's k row
@@ -1120,7 +1128,6 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
     for (int st = 0; st < nst; ++st) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const float4 yv = yrow[(st * 16 + 4 * q4 + c) ^ r16];
             float4 wv4;
             if constexpr (!CODED) {
                 wv4 = *reinterpret_cast<const float4*>(wrow + st * 64 + 4 * c);
@@ -1133,38 +1140,48 @@ __device__ __forceinline__ void dx_lds_tile(const GemmArgs& a, int tiles_i, int 
                 wv4.z = (float((cb >> 16) & 0xFFu) - OFF) * s4.z;
                 wv4.w = (float(cb >> 24) - OFF) * s4.w;
             }
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.x, wv4.x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.y, wv4.y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.z, wv4.z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.w, wv4.w, acc, 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const float4 yv = yrow[rt * 16 * spr + ((st * 16 + 4 * q4 + c) ^ r16)];
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.x, wv4.x, acc[rt], 0, 0, 0);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.y, wv4.y, acc[rt], 0, 0, 0);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.z, wv4.z, acc[rt], 0, 0, 0);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(yv.w, wv4.w, acc[rt], 0, 0, 0);
+            }
         }
     }
     const int k = k0 + wave * 16 + r16;
     if (k < K) {
         if (a.sg_gate) {
-            // All four rows' gate and up values are loaded before the first
-            // store, so no store waits on a later row's loads.
-            float gv[4], uv[4];
+            // All rows' gate and up values are loaded before the first store,
+            // so no store waits on a later row's loads.
+            float gv[RT][4], uv[RT][4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const size_t e = size_t(min(i0 + 4 * q4 + r, a.rows - 1)) * K + k;
-                gv[r] = a.sg_gate[e];
-                uv[r] = a.sg_up[e];
-            }
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = i0 + 4 * q4 + r;
-                if (i < a.rows) {
-                    float* o = a.out + size_t(i) * 2 * K + k;
-                    dgm::swiglu_bwd_value(gv[r], uv[r], acc[r], o[0], o[K]);
+                for (int r = 0; r < 4; ++r) {
+                    const size_t e = size_t(min(i0 + 16 * rt + 4 * q4 + r, a.rows - 1)) * K + k;
+                    gv[rt][r] = a.sg_gate[e];
+                    uv[rt][r] = a.sg_up[e];
                 }
-            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = i0 + 16 * rt + 4 * q4 + r;
+                    if (i < a.rows) {
+                        float* o = a.out + size_t(i) * 2 * K + k;
+                        dgm::swiglu_bwd_value(gv[rt][r], uv[rt][r], acc[rt][r], o[0], o[K]);
+                    }
+                }
         } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = i0 + 4 * q4 + r;
-                if (i < a.rows) a.out[size_t(i) * K + k] = acc[r];
-            }
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = i0 + 16 * rt + 4 * q4 + r;
+                    if (i < a.rows) a.out[size_t(i) * K + k] = acc[rt][r];
+                }
         }
     }
 }
@@ -1175,9 +1192,9 @@ __global__ __launch_bounds__(kThreads) void gemm_dx_lds_kernel(GemmArgs a, int t
     dx_lds_tile<BITS>(a, tiles_i, tiles_j, per_xcd, int(blockIdx.x), sm4);
 }
 
-size_t dx_lds_bytes(bool coded, int N) {
+size_t dx_lds_bytes(bool coded, int N, int rt = 1) {
     const size_t strip = coded ? size_t(64) * (N + 12) + size_t(4) * N * 4 : size_t(64) * (N + 4) * 4;
-    return size_t(16) * N * 4 + strip;
+    return size_t(16) * rt * N * 4 + strip;
 }
 
 // N % 64 == 0 and N <= 448 (dY block and the transposed strip stay in LDS),
@@ -1306,15 +1323,15 @@ __global__ __launch_bounds__(kThreads) void gemm_dw_pair_kernel(GemmArgs a, int 
 // ---- the STE backward pair in one launch ------------------------------------------
 // Workgroups [0, 8*per_x) compute dX tiles (dx_lds_tile), the rest dW tiles
 // (dw_pair_tile): the two GEMMs share no output and only read dY, so they run
-// side by side instead of back to back. Each tile is computed exactly as by
-// its own kernel.
-template <int BITS>
+// side by side instead of back to back. Each tile's elements are computed as
+// by its own kernel (dX tiles of 16 RT rows).
+template <int BITS, int RT>
 __global__ __launch_bounds__(kThreads) void gemm_bwd_pair_kernel(GemmArgs ax, int ti, int tj, int per_x, GemmArgs aw,
                                                                  int tn, int tk, int per_w) {
     extern __shared__ __align__(16) float4 sm4[];
     const int nx = 8 * per_x;
     if (int(blockIdx.x) < nx) {
-        dx_lds_tile<BITS, BITS != 32>(ax, ti, tj, per_x, int(blockIdx.x), sm4);
+        dx_lds_tile<BITS, BITS != 32, RT>(ax, ti, tj, per_x, int(blockIdx.x), sm4);
     } else {
         dw_pair_tile(aw, tn, tk, per_w, int(blockIdx.x) - nx, reinterpret_cast<float (*)[2][16][16]>(sm4));
     }
@@ -1767,30 +1784,38 @@ int gemm_f32_bwd_pair(dgm_gpu* g, int bits, const void* W, const float* scale, c
         *fused = true;
         return DGM_OK;
     }
-    const size_t lds = dx_lds_bytes(bits != 32, ax.N);   // >= the 8 KB the dW tiles use (N >= 64)
-    const void* kern = bits == 32 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<32>)
-                       : bits == 8 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<8>)
-                                   : reinterpret_cast<const void*>(gemm_bwd_pair_kernel<4>);
+    // 32-row dX tiles (coded strips) when N >= 128 and they still give at
+    // least half as many workgroups as CUs; else 16 rows.
+    const int rt = (bits != 32 && ax.N >= 128 &&
+                    int64_t(dgm::ceil_div(ax.rows, 32)) * dgm::ceil_div(ax.K, 64) * 2 >= g->num_cus)
+                       ? 2
+                       : 1;
+    const size_t lds = dx_lds_bytes(bits != 32, ax.N, rt);   // >= the 8 KB the dW tiles use (N >= 64)
+    const void* kern =
+        bits == 32 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<32, 1>)
+        : bits == 8 ? (rt == 2 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<8, 2>)
+                               : reinterpret_cast<const void*>(gemm_bwd_pair_kernel<8, 1>))
+                    : (rt == 2 ? reinterpret_cast<const void*>(gemm_bwd_pair_kernel<4, 2>)
+                               : reinterpret_cast<const void*>(gemm_bwd_pair_kernel<4, 1>));
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess)
             return dgm::fail(g, DGM_ERR_HIP, "gemm_bwd: cannot reserve %zu bytes of LDS: %s", lds,
                              hipGetErrorString(e));
     }
-    const int ti = int(dgm::ceil_div(ax.rows, 16)), tj = int(dgm::ceil_div(ax.K, 64));
+    const int ti = int(dgm::ceil_div(ax.rows, 16 * rt)), tj = int(dgm::ceil_div(ax.K, 64));
     const int per_x = int((int64_t(ti) * tj + 7) / 8);
     const int tn = int(dgm::ceil_div(aw.N, 32)), tk = int(dgm::ceil_div(aw.K, 16));
     const int per_w = int((int64_t(tn) * tk + 7) / 8);
     const dim3 grid(unsigned(per_x + per_w) * 8u);
-    if (bits == 32)
-        hipLaunchKernelGGL(gemm_bwd_pair_kernel<32>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk,
-                           per_w);
-    else if (bits == 8)
-        hipLaunchKernelGGL(gemm_bwd_pair_kernel<8>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk,
-                           per_w);
-    else
-        hipLaunchKernelGGL(gemm_bwd_pair_kernel<4>, grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk,
-                           per_w);
+#define DGM_PAIR_LAUNCH(B, R) \
+    hipLaunchKernelGGL((gemm_bwd_pair_kernel<B, R>), grid, dim3(kThreads), lds, g->stream, ax, ti, tj, per_x, aw, tn, tk, per_w)
+    if (bits == 32) DGM_PAIR_LAUNCH(32, 1);
+    else if (bits == 8 && rt == 2) DGM_PAIR_LAUNCH(8, 2);
+    else if (bits == 8) DGM_PAIR_LAUNCH(8, 1);
+    else if (rt == 2) DGM_PAIR_LAUNCH(4, 2);
+    else DGM_PAIR_LAUNCH(4, 1);
+#undef DGM_PAIR_LAUNCH
     *fused = true;
     return DGM_OK;
 }

@@ -182,6 +182,15 @@ def test_block_backward_separate_grads(gpu, dgm, orc):
     _check_block(blk, dgm, from_dev(x), from_dev(g), xo, gx, gw, gn)
 
 
+def test_block_backward_swiglu_wide_dx_tiles(gpu, dgm, orc):
+    """int8 G=16 (no bf16-dX weight backward): wdown's backward runs the
+    STE pair with the SwiGLU backward in its dX epilogue on 32-row dX tiles
+    (C = 192, F = 1024, 512 rows)."""
+    cfg = dgm.DiTConfig(B=8, T=64, C=192, F=1024, H=4, D=48, loops=1, group=16, bits=8)
+    blk, xg, gg, xo, gx, gw, gn, _ = _run_block(gpu, dgm, orc, cfg, 41)
+    _check_block(blk, dgm, xg, gg, xo, gx, gw, gn)
+
+
 def test_wide_block_backward(gpu, dgm, orc):
     """C = 320 > 256: the RMSNorm backwards run one launch each (no chains)."""
     cfg = dgm.DiTConfig(B=2, T=16, C=320, F=128, H=4, D=80, loops=2, group=16, bits=8)

@@ -286,12 +286,15 @@ def test_gemm_error_paths(gpu, dgm):
 
 # ---- gemmBwd: the gemmDW(+Acc) / gemmDX pair in one launch ---------------------
 
-# One launch with LDS dX tiles (N % 64 == 0, N <= 448, M % 64 == 0), one launch
-# with deep dX tiles (longer N, small dX: (512, 768, 192), (512, 48, 192)), or
-# the two calls ((512, 768, 768): dX large enough for its own launch; M % 64 or
-# N % 16 off).
+# One launch with LDS dX tiles (N % 64 == 0, N <= 448, M % 64 == 0; 32-row
+# tiles for codes when N >= 128 and they fill half the CUs: (512, 192, 768),
+# (1024, 192, 768), (512, 256, 800) with a ragged last column tile,
+# (512, 128, 1024)), one launch with deep dX tiles (longer N, small dX:
+# (512, 768, 192), (512, 48, 192)), or the two calls ((512, 768, 768): dX
+# large enough for its own launch; M % 64 or N % 16 off).
 BWD_SHAPES = [(512, 192, 768, 32), (512, 768, 192, 32), (512, 48, 192, 32), (512, 192, 192, 32),
-              (64, 64, 128, 16), (128, 448, 64, 32),
+              (64, 64, 128, 16), (128, 448, 64, 32), (1024, 192, 768, 32), (512, 256, 800, 32),
+              (512, 128, 1024, 32),
               (512, 768, 768, 32), (100, 192, 768, 32), (64, 62, 128, 16)]
 
 
