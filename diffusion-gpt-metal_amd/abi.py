@@ -165,6 +165,9 @@ PROTOTYPES = {
     "dgm_quantize": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmNT": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_gemmNT_noalloc": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
+    "dgm_gemmNT_workspace_bound": (_I64, [_I64, _I64, _I64]),
+    "dgm_gpu_reserve": (_I, [_P, _I64]),
+    "dgm_gpu_workspace_bytes": (_I64, [_P]),
     "dgm_probe_read": (_I, [_P, _P, _I64, _I64, _I64, _P]),
     "dgm_probe_gemv_valu": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64]),
     "dgm_debug_wait_limit": (_I, [_I64]),

@@ -6,6 +6,8 @@
 // mode, else the fp32 MFMA tiles; dX and dW always on the fp32 tiles.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace dgm {
 int gemm_check_sizes(dgm_gpu* g, const char* name, const dgm_GemmP* p, int bits);
 int gemm_f32_fwd(dgm_gpu* g, int bits, const void* W, const float* scale, const float* X,
@@ -136,6 +138,29 @@ int dgm_gemmNT_noalloc(dgm_gpu* g, int64_t bits, const float* w, const void* q, 
     g->use_scratch = false;
     return rc;
 }
+
+int64_t dgm_gemmNT_workspace_bound(int64_t M, int64_t N, int64_t K) {
+    if (M < 0 || N < 0 || K < 0) return -1;
+    // Activation pieces of the decode-shaped kernels (M <= 64 and the int8
+    // skinny kernel's virtual rows): at most 4 row tiles x 2 pieces x 1 KB per
+    // 32 k, plus the exponents / offset terms (4 bytes per row tile, 16 rows,
+    // per 64 k) and alignment slack.
+    int64_t b = 260 * K + 512;
+    // bf16 copy of X (reduced-precision prefill, M > 64).
+    if (M > 64) b = std::max(b, 2 * M * K);
+    // Partial sums of the K-sliced kernel (M <= 16): slices x M x N floats with
+    // at most K / 256 slices, refused beyond the static scratch's size.
+    if (M <= 16) b = std::max(b, std::min<int64_t>(int64_t(dgm::kScratchBytes), M * N * (K / 256) * 4));
+    return b;
+}
+
+int dgm_gpu_reserve(dgm_gpu* g, int64_t bytes) {
+    if (!g || bytes < 0) return DGM_ERR_ARG;
+    if (size_t(bytes) <= g->ws_bytes) return DGM_OK;
+    return dgm::workspace(g, size_t(bytes)) ? DGM_OK : dgm::ws_error(g);
+}
+
+int64_t dgm_gpu_workspace_bytes(const dgm_gpu* g) { return g ? int64_t(g->ws_bytes) : -1; }
 
 int dgm_gemmDX(dgm_gpu* g, int64_t bits, const float* w, const void* q, const float* scale,
                const float* dy, float* dx, int64_t M, int64_t N, int64_t K, int64_t qGroup) {

@@ -117,6 +117,19 @@ class GPU:
         self._check(self.lib.dgm_gemmNT_noalloc(self.h, bits, _ptr(w), _ptr(q), _ptr(scale), _ptr(x),
                                                  _ptr(bias), _ptr(y), M, N, K, qGroup))
 
+    def gemmNT_workspace_bound(self, M: int, N: int, K: int) -> int:
+        """Bytes of workspace that cover any gemmNT call of this shape (no
+        counterpart in the reference, whose buffers are all made at setup)."""
+        return int(self.lib.dgm_gemmNT_workspace_bound(M, N, K))
+
+    def reserve(self, nbytes: int) -> None:
+        """Grow the context's workspace to at least nbytes now, so that later
+        calls within it allocate nothing."""
+        self._check(self.lib.dgm_gpu_reserve(self.h, nbytes))
+
+    def workspaceBytes(self) -> int:
+        return int(self.lib.dgm_gpu_workspace_bytes(self.h))
+
     def probeRead(self, src, nbytes: int, mode: int, workgroups: int, sink) -> None:
         """The bench's read-rate probe (no counterpart in the reference): mode 0
         16-byte register loads, mode 1 direct-to-LDS loads, `workgroups` 0 = one

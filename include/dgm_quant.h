@@ -161,8 +161,10 @@ int dgm_gemmNT(dgm_gpu* g, int64_t bits, const float* w, const void* q,
  * path) comes from a static device scratch of DGM_NOALLOC_SCRATCH_BYTES per
  * GPU, held from library load until the process ends; nothing is allocated.
  * A call that would need more scratch returns DGM_ERR_UNSUPPORTED before
- * launching anything (the decode path needs about 192 * K bytes at M <= 64;
- * the bf16 prefill path 2 * M * K bytes). Every such call on one GPU shares
+ * launching anything (dgm_gemmNT_workspace_bound gives the most a call can
+ * need: at most 260 * K + 512 bytes at M <= 64, the K-sliced path's partial
+ * sums up to all of the scratch at M <= 16, the bf16 prefill path 2 * M * K
+ * bytes). Every such call on one GPU shares
  * that scratch, which keeps the last call's contents (no kernel relies on it
  * starting at zero): calls that overlap in time on one GPU (other streams,
  * other contexts, other threads) race and must be serialized by the caller. */
@@ -170,6 +172,20 @@ int dgm_gemmNT(dgm_gpu* g, int64_t bits, const float* w, const void* q,
 int dgm_gemmNT_noalloc(dgm_gpu* g, int64_t bits, const float* w, const void* q,
                        const float* scale, const float* x, const float* bias, float* y,
                        int64_t M, int64_t N, int64_t K, int64_t qGroup);
+/* No counterpart in the reference, whose buffers are all allocated at setup
+ * (src/GPU.swift:31-88; its kernels never allocate). dgm_gemmNT's staging
+ * buffers (activation pieces of the decode-shaped kernels, partial sums of the
+ * K-sliced kernel, the bf16 copy of X of the prefill path) come from a
+ * workspace of the context that is otherwise allocated by the first call that
+ * needs it. dgm_gemmNT_workspace_bound returns bytes that cover every path a
+ * dgm_gemmNT call of that shape can take, in either math mode (-1 for
+ * negative sizes); dgm_gpu_reserve grows the workspace to at least `bytes`
+ * now (DGM_ERR_UNSUPPORTED during a graph capture), so that later calls whose
+ * bound it covers allocate nothing; dgm_gpu_workspace_bytes returns its size
+ * (0 before anything was allocated). */
+int64_t dgm_gemmNT_workspace_bound(int64_t M, int64_t N, int64_t K);
+int dgm_gpu_reserve(dgm_gpu* g, int64_t bytes);
+int64_t dgm_gpu_workspace_bytes(const dgm_gpu* g);
 /* GPU.gemmDX (src/GPU.swift:245-260). */
 int dgm_gemmDX(dgm_gpu* g, int64_t bits, const float* w, const void* q,
                const float* scale, const float* dy, float* dx,

@@ -62,3 +62,19 @@ def test_product_does_not_touch_the_oracle():
             if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
                 text = open(os.path.join(root, f), errors="ignore").read()
                 assert not banned.search(text), f
+
+
+def test_workspace_bound_closed_forms(dgm):
+    """dgm_gemmNT_workspace_bound is host arithmetic: the decode pieces'
+    260 K + 512 bytes, the K-sliced partial sums (M <= 16, at most K / 256
+    slices, capped at the static scratch), the bf16 copy of X above 64 rows."""
+    lib = dgm.load_library()
+    f = lib.dgm_gemmNT_workspace_bound
+    assert f(1, 14336, 4096) == 260 * 4096 + 512                  # partials 917,504 < pieces
+    assert f(16, 14336, 4096) == dgm.DGM_NOALLOC_SCRATCH_BYTES     # 14.7 MB of partials, capped
+    assert f(8, 1024, 4096) == max(260 * 4096 + 512, 8 * 1024 * 16 * 4)
+    assert f(64, 14336, 4096) == 260 * 4096 + 512
+    assert f(8192, 14336, 4096) == 2 * 8192 * 4096
+    assert f(65, 10, 100) == 260 * 100 + 512                       # 2 M K = 13,000 is smaller
+    assert f(0, 0, 0) == 512
+    assert f(-1, 4, 4) == -1 and f(4, -1, 4) == -1 and f(4, 4, -1) == -1
