@@ -1235,8 +1235,9 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
 // reduced through LDS in a fixed order. Every dW element is the same chain of
 // MFMAs over the same rows for any NP and CH, so the results are bitwise equal.
 // The backward pairs run NP = 2, CH = 8 (32 x 16 tiles, 125 VGPRs: beside the
-// dX tiles the wider tile measured slower); dW alone runs NP = 4, CH = 4 when
-// N % 4 == 0 (64 x 16 tiles, 110 VGPRs: 5.4 us at c2 / c1 against 6.7 us).
+// dX tiles the wider tile measured slower); dW alone runs NP = 4, CH = 4 (64 x
+// 16 tiles, 110 VGPRs) where launch_dw_pair finds it pays (c2 / c1: 5.4 us
+// against 6.7 us).
 constexpr int DWP_CH = 8;   // 16-row chunks per wave and round of the paired tiles
 
 // Body of one dW tile; `blk` as in dx_lds_tile, part: NP x 4 KB of LDS. Lanes
@@ -1360,8 +1361,14 @@ bool dw_pair_ok(const GemmArgs& a, const void* dY) {
     return a.M > 0 && a.M % 64 == 0 && a.N >= 2 && a.N % 2 == 0 && a.K > 0 && dgm::aligned(dY, 8);
 }
 
-void launch_dw_pair(const GemmArgs& a, hipStream_t st) {
-    const bool four = a.N % 4 == 0 && dgm::aligned(a.A, 16);
+// 64-row tiles (four dY columns per lane) do a 32-row tile's work in ~1.65x
+// its time; they pay when they need fewer rounds of workgroups over the CUs
+// by more than that factor (measured at M = 512..2048, N x K from 192 x 192 to
+// 4096 x 1024: e.g. 192 x 768 5.75 against 6.9 us, 192 x 192 6.3 against 4.8).
+void launch_dw_pair(const GemmArgs& a, int num_cus, hipStream_t st) {
+    const int64_t nc = num_cus > 0 ? num_cus : 1, tk64 = dgm::ceil_div(a.K, 16);
+    const int64_t r2 = (dgm::ceil_div(a.N, 32) * tk64 + nc - 1) / nc, r4 = (dgm::ceil_div(a.N, 64) * tk64 + nc - 1) / nc;
+    const bool four = a.N % 4 == 0 && dgm::aligned(a.A, 16) && 33 * r4 < 20 * r2;
     const int tn = int(dgm::ceil_div(a.N, four ? 64 : 32)), tk = int(dgm::ceil_div(a.K, 16));
     const int64_t nt = int64_t(tn) * tk;
     const int per = int((nt + 7) / 8);
@@ -1730,7 +1737,7 @@ int gemm_f32_dw(dgm_gpu* g, const float* dY, const float* X, float* dW, const dg
     a.G = 1; a.groups = 0;
     a.accumulate = accumulate;
     if (dw_pair_ok(a, dY)) {
-        launch_dw_pair(a, g->stream);
+        launch_dw_pair(a, g->num_cus, g->stream);
         return DGM_OK;
     }
     if (deep_ok<MODE_DW>(a, 32, false)) launch_deep<MODE_DW, 32>(a, g->num_cus, g->stream);

@@ -190,11 +190,15 @@ def test_multiple_of_16_contractions(gpu, orc, M, N, K, G, bits):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 20, 36), (128, 36, 100), (448, 52, 44), (192, 12, 8), (512, 192, 768),
-                                   (64, 4, 4), (320, 100, 260), (128, 30, 48), (256, 66, 20)])
+                                   (64, 4, 4), (320, 100, 260), (128, 30, 48), (256, 66, 20), (128, 100, 1280),
+                                   (64, 68, 2048)])
 def test_dw_shapes(gpu, orc, M, N, K):
     """dW / dW += over contractions that are multiples of 64 with ragged output
-    tiles (rows and columns past N or K clamped, never stored): four dY columns
-    per lane when N % 4 == 0, two otherwise (N = 30, 66)."""
+    tiles (rows and columns past N or K clamped, never stored): 64-row tiles
+    (four dY columns per lane) where they need fewer rounds of workgroups on a
+    256-CU part ((512, 192, 768), and ragged in N: (128, 100, 1280),
+    (64, 68, 2048)), 32-row tiles otherwise (N = 30 and 66: two columns per
+    lane always)."""
     import torch
     rng = np.random.default_rng(M + N + K)
     x = rng.standard_normal(M * K).astype(np.float32)
