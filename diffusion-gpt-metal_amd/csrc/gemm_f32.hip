@@ -1234,11 +1234,14 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
 // At step s a lane group q uses row m = m0 + q + 4 s. Wave partials are
 // reduced through LDS in a fixed order. Every dW element is the same chain of
 // MFMAs over the same rows for any NP and CH, so the results are bitwise equal.
-// The backward pairs run NP = 2, CH = 8 (32 x 16 tiles, 125 VGPRs: beside the
-// dX tiles the wider tile measured slower); dW alone runs NP = 4, CH = 4 (64 x
-// 16 tiles, 110 VGPRs) where launch_dw_pair finds it pays (c2 / c1: 5.4 us
-// against 6.7 us).
-constexpr int DWP_CH = 8;   // 16-row chunks per wave and round of the paired tiles
+// dW alone runs NP = 2, CH = 8 (32 x 16 tiles, 125 VGPRs), or NP = 4, CH = 4
+// (64 x 16 tiles, 110 VGPRs) where launch_dw_pair finds it pays (c2 / c1: 5.4
+// us against 6.7 us). Beside dX tiles (the backward pairs) the 32 x 16 tile
+// takes two chunks per round (kPairCH): fewer registers, more workgroups per
+// CU (c2 pair 7.5-7.6 us against 7.8-7.9 with eight; the DiT training step
+// 324 us against 331; one chunk and four measured slower, and wider tiles too).
+constexpr int DWP_CH = 8;    // 16-row chunks per wave and round, dW alone
+constexpr int kPairCH = 2;   // the same beside dX tiles
 
 // Body of one dW tile; `blk` as in dx_lds_tile, part: NP x 4 KB of LDS. Lanes
 // whose columns pass N load the last NP columns (N % NP == 0, so those lanes'
@@ -1334,7 +1337,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bwd_pair_kernel(GemmArgs ax, in
     if (int(blockIdx.x) < nx) {
         dx_lds_tile<BITS, BITS != 32, RT>(ax, ti, tj, per_x, int(blockIdx.x), sm4);
     } else {
-        dw_pair_tile(aw, tn, tk, per_w, int(blockIdx.x) - nx, reinterpret_cast<float (*)[2][16][16]>(sm4));
+        dw_pair_tile<2, kPairCH>(aw, tn, tk, per_w, int(blockIdx.x) - nx, reinterpret_cast<float (*)[2][16][16]>(sm4));
     }
 }
 
@@ -1560,7 +1563,7 @@ __global__ __launch_bounds__(kThreads) void gemm_bwd_fold_pair_kernel(DxFoldArgs
     __shared__ float part[4][2][16][16];
     const int nx = 8 * per_x;
     if (int(blockIdx.x) < nx) dx_fold_tile(ax, tm, tk, per_x, int(blockIdx.x), part);
-    else dw_pair_tile(aw, tn, tkw, per_w, int(blockIdx.x) - nx, part);
+    else dw_pair_tile<2, kPairCH>(aw, tn, tkw, per_w, int(blockIdx.x) - nx, part);
 }
 
 // codesT[k][n] = code[n][k] (int8, also for int4 codes) and scalesT[g][n] =
