@@ -1234,14 +1234,15 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
 // At step s a lane group q uses row m = m0 + q + 4 s. Wave partials are
 // reduced through LDS in a fixed order. Every dW element is the same chain of
 // MFMAs over the same rows for any NP and CH, so the results are bitwise equal.
-// dW alone runs NP = 2, CH = 8 (32 x 16 tiles, 125 VGPRs), or NP = 4, CH = 4
-// (64 x 16 tiles, 110 VGPRs) where launch_dw_pair finds it pays (c2 / c1: 5.4
-// us against 6.7 us). Beside dX tiles (the backward pairs) the 32 x 16 tile
-// takes two chunks per round (kPairCH): fewer registers, more workgroups per
-// CU (c2 pair 7.5-7.6 us against 7.8-7.9 with eight; the DiT training step
-// 324 us against 331; one chunk and four measured slower, and wider tiles too).
-constexpr int DWP_CH = 8;    // 16-row chunks per wave and round, dW alone
-constexpr int kPairCH = 2;   // the same beside dX tiles
+// The 32 x 16 tile (NP = 2) takes two chunks per round (kPairCH): fewer
+// registers, more workgroups per CU (c2 pair 7.5-7.6 us against 7.8-7.9 with
+// eight; the DiT training step 324 us against 331; dW alone 2-7% faster at
+// the 32-row shapes; one chunk and four measured no better). The 64 x 16
+// tile (NP = 4, CH = 4, 110 VGPRs) runs dW alone where launch_dw_pair finds
+// it pays (c2 / c1: 5.4 us against 6.7 us). The deep-dX pair keeps eight
+// chunks (two measured 3% slower at the c1 shape).
+constexpr int DWP_CH = 8;    // 16-row chunks per wave and round beside the deep dX tiles
+constexpr int kPairCH = 2;   // the same for the 32 x 16 tiles elsewhere
 
 // Body of one dW tile; `blk` as in dx_lds_tile, part: NP x 4 KB of LDS. Lanes
 // whose columns pass N load the last NP columns (N % NP == 0, so those lanes'
@@ -1378,8 +1379,8 @@ void launch_dw_pair(const GemmArgs& a, int num_cus, hipStream_t st) {
     if (four)
         hipLaunchKernelGGL((gemm_dw_pair_kernel<4, 4>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn, tk, per);
     else
-        hipLaunchKernelGGL((gemm_dw_pair_kernel<2, DWP_CH>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn, tk,
-                           per);
+        hipLaunchKernelGGL((gemm_dw_pair_kernel<2, kPairCH>), dim3(unsigned(per) * 8u), dim3(kThreads), 0, st, a, tn,
+                           tk, per);
 }
 
 template <int MODE, int BITS, int TM, int TN>
