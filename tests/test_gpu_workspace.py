@@ -115,12 +115,13 @@ def test_growth_during_capture_is_refused(dgm, orc, torch_cuda):
         gpu.close()
 
 
-# (math, bits, (M, N, K, G)): stream (M = 1), K-sliced (fp32 M = 16), one-launch
+# (math, bits, (M, N, K, G)): stream (M = 1), K-sliced (fp32 M = 16, int4 and int8), one-launch
 # decode (reduced M = 16), decode pieces (M = 64 both modes, M = 33), int8
 # skinny (M = 24 int8 fp32), bf16 prefill (M = 256 reduced), fp32 tiles (M = 256).
 CASES = [
     ("fp32", 4, (1, 14336, 4096, 128)),
     ("fp32", 4, (16, 14336, 4096, 128)),
+    ("fp32", 8, (16, 8192, 4096, 128)),      # int8 K-sliced: 16 slices, partial sums exactly 8 MiB
     ("bf16", 4, (16, 14336, 4096, 128)),
     ("fp32", 4, (64, 14336, 4096, 128)),
     ("bf16", 4, (64, 14336, 4096, 128)),
