@@ -136,7 +136,7 @@ struct RmsChainArgs {
     const float* pin[2];
     float* dwp[2];
     int npend, npin;
-    int rows, cols, ndx, ndw;
+    int rows, cols, ndx, ndw, ndd;   // ndd: stage 0's weight-gradient workgroups (8 columns each)
 };
 
 __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainArgs a) {
@@ -213,32 +213,50 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainAr
         }
         return;
     }
-    // direct weight gradient of stage 0 (as rms_bwd), then the pending partial sums.
+    // Stage 0's weight gradient: 8 columns per workgroup; lane (column c0 +
+    // lane % 8, row phase lane / 8) of wave w sums rows 8 w + phase + 128 u in
+    // order, all its loads in flight at once (one round trip, like the dx
+    // workgroups: with 64 columns per workgroup and 32 rows per lane in two
+    // rounds these workgroups finished last, ~8 us per training step), then
+    // the 128 partial sums of a column are added in a fixed order (wave, then
+    // phase).
     const int rest = blk - a.ndx;
-    const bool direct = rest < a.ndw;
-    const int pi = direct ? 0 : (rest - a.ndw) / a.ndw;
-    const int c = (direct ? rest : (rest - a.ndw) % a.ndw) * 64 + lane;
-    float acc = 0.0f;
-    if (c < cols) {
-        if (direct) {
+    if (rest < a.ndd) {
+        const int c = rest * 8 + (lane % 8), ph = lane / 8;
+        float acc = 0.0f;
+        if (c < cols) {
             const float* x = a.st[0].x;
             const float* r1 = a.st[0].r;
-            int r = wave;
-            for (; r + 15 * kDwWaves < rows; r += 16 * kDwWaves) {   // 16 rows' loads in flight
-                float v[16];
+            for (int r0 = 8 * wave + ph; r0 < rows; r0 += 128 * 8) {   // 8 rows' loads in flight
+                float v[8];
 #pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    const int rr = r + u * kDwWaves;
-                    v[u] = a.dy[size_t(rr) * cols + c] * x[size_t(rr) * cols + c] * r1[rr];
+                for (int u = 0; u < 8; ++u) {
+                    const int rr = r0 + 128 * u;
+                    v[u] = rr < rows ? a.dy[size_t(rr) * cols + c] * x[size_t(rr) * cols + c] * r1[rr] : 0.0f;
                 }
 #pragma unroll
-                for (int u = 0; u < 16; ++u) acc += v[u];
+                for (int u = 0; u < 8; ++u) acc += v[u];
             }
-            for (; r < rows; r += kDwWaves) acc += a.dy[size_t(r) * cols + c] * x[size_t(r) * cols + c] * r1[r];
-        } else {
-            const float* pin = a.pin[pi];
-            for (int b2 = wave; b2 < a.npin; b2 += kDwWaves) acc += pin[size_t(b2) * cols + c];
         }
+        part[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0 && ph == 0 && c < cols) {
+            float tot = 0.0f;
+            for (int w2 = 0; w2 < kDwWaves; ++w2)
+#pragma unroll
+                for (int p2 = 0; p2 < 8; ++p2) tot += part[w2][8 * p2 + lane];
+            a.dw0[c] += tot;
+        }
+        return;
+    }
+    // The pending partial sums: 64 columns per workgroup.
+    const int pr = rest - a.ndd;
+    const int pi = pr / a.ndw;
+    const int c = (pr % a.ndw) * 64 + lane;
+    float acc = 0.0f;
+    if (c < cols) {
+        const float* pin = a.pin[pi];
+        for (int b2 = wave; b2 < a.npin; b2 += kDwWaves) acc += pin[size_t(b2) * cols + c];
     }
     part[wave][lane] = acc;
     __syncthreads();
@@ -246,7 +264,7 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainAr
         float tot = 0.0f;
 #pragma unroll
         for (int w2 = 0; w2 < kDwWaves; ++w2) tot += part[w2][lane];
-        (direct ? a.dw0 : a.dwp[pi])[c] += tot;
+        a.dwp[pi][c] += tot;
     }
 }
 
@@ -782,7 +800,8 @@ int launch_rms_chain(dgm_gpu* g, RmsChainArgs a) {
     if (a.rows == 0 || a.cols == 0) return DGM_OK;
     a.ndx = (a.rows + kDwWaves - 1) / kDwWaves;
     a.ndw = (a.cols + 63) / 64;
-    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndw * (1 + a.npend))), dim3(64 * kDwWaves), 0,
+    a.ndd = (a.cols + 7) / 8;
+    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndd + a.ndw * a.npend)), dim3(64 * kDwWaves), 0,
                        g->stream, a);
     return dgm::check_launch(g, "rms_bwd");
 }
