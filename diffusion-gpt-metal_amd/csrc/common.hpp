@@ -9,6 +9,7 @@
 #include <cstring>
 
 #include "../../include/dgm_quant.h"
+#include "dw_tile.hpp"
 
 // Context behind the opaque dgm_gpu handle (mirrors class GPU, src/GPU.swift:91-198).
 struct dgm_gpu {
@@ -126,9 +127,13 @@ int dit_forward_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w
 // kNotFused, launching nothing, unless dit_attn_bwd_loop_ok holds for the
 // activation and workspace buffers (16-byte aligned pieces).
 bool dit_attn_bwd_loop_ok(const dgm_dit_cfg* c, const float* acts, const float* ws);
+// dw (may be null): the 32 x 16 tiles of one linear's dW, run by extra
+// workgroups of the same launch beside the attention backward (they read
+// none of its outputs).
 int dit_attn_bwd_loop(dgm_gpu* g, const dgm_dit_cfg* c, const float* q, const float* k, const float* v,
                       const float* probs, const float* o, const float* dout, const float* cosv, const float* sinv,
-                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first, bool fresh);
+                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first, bool fresh,
+                      const dgm_dw::DwTileArgs* dw = nullptr);
 // True when `next`'s weights (fp32 for bits 32, else codes and scales)
 // start where `first`'s `rows` x K end, so the two act as one [2 rows, K]
 // linear.
@@ -167,7 +172,8 @@ int gemm_bwd_swiglu(dgm_gpu* g, int bits, const float* w, const void* q, const f
 // linears transposed, codesT [K][N] and scalesT [K/G][N], one launch;
 // gemm_bwd_fold then runs dX from them (the group scale folded into dY,
 // which is split into three bf16 pieces) beside the fp32 dW tiles
-// (dW += or = dY^T X), with the SwiGLU backward on dX when sg_gate is set.
+// (dW += or = dY^T X; dW null: the dX tiles alone), with the SwiGLU
+// backward on dX when sg_gate is set.
 // gemm_bwd_fold returns kNotFused, launching nothing, unless bwd_fold_ok
 // holds and the buffers are aligned (dY and scalesT 16 bytes, codesT 8).
 int wt_prep(dgm_gpu* g, int bits, int nlin, const void* const* W, const float* const* S, const int* N, const int* K,

@@ -720,6 +720,9 @@ struct LoopAttnBwdArgs {
     int B, vmix;
     int fresh;               // dfirst holds nothing yet (the first loop the backward runs)
     float ca, mixc, scale;
+    int own;                 // workgroups of the attention backward; those past it run dW tiles
+    dgm_dw::DwTileArgs dw;   // another linear's dW (32 x 16 tiles, one per workgroup)
+    int dw_tiles, dw_tiles_n;
 };
 
 template <int KS, int TT, int DT>
@@ -744,6 +747,15 @@ template <int KS, int TT, int DT>
 __global__ __launch_bounds__(1024) void loop_attn_bwd_kernel(LoopAttnBwdArgs a) {
 #pragma clang fp contract(off)
     using S = AttnBwdShape<KS, TT, DT>;
+    if (int(blockIdx.x) >= a.own) {
+        // One dW tile per workgroup over its sixteen waves (32 KB of the LDS).
+        static_assert(dgm_dw::kHostedWaves == 16, "a 1024-thread workgroup per tile");
+        extern __shared__ __align__(16) float lds_w[];
+        dgm_dw::dw_tile<2, dgm_dw::kPairCH, dgm_dw::kHostedWaves>(
+            a.dw, true, int(blockIdx.x) - a.own, a.dw_tiles_n, int(threadIdx.x >> 6), int(threadIdx.x),
+            reinterpret_cast<float (*)[2][16][16]>(lds_w));
+        return;
+    }
     constexpr int C = S::C, D = S::D, H = S::H, T = S::T, HT = S::HT, C4 = S::C4, D4 = S::D4;
     constexpr int QLD = S::QLD, KLD = S::KLD, VLD = S::VLD, SLD = S::SLD, XLD = S::XLD, mid = D / 2;
     extern __shared__ __align__(16) float lds_f[];
@@ -1049,17 +1061,21 @@ bool shape_built(const dgm_dit_cfg* c) {
 
 
 template <int KS, int TT, int DT>
-int run_attn_bwd(dgm_gpu* g, const LoopAttnBwdArgs& a) {
+int run_attn_bwd(dgm_gpu* g, LoopAttnBwdArgs a) {
     using S = AttnBwdShape<KS, TT, DT>;
     auto k = loop_attn_bwd_kernel<KS, TT, DT>;
-    if (S::BYTES > 64 * 1024) {
+    // The dW workgroups use 32 KB of the same dynamic LDS.
+    constexpr int kDwLds = dgm_dw::kHostedWaves * 2 * 16 * 16 * 4;
+    const int bytes = a.dw_tiles > 0 && S::BYTES < kDwLds ? kDwLds : S::BYTES;
+    if (bytes > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, S::BYTES);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (e != hipSuccess)
-            return dgm::fail(g, DGM_ERR_HIP, "dit_backward: cannot reserve %d bytes of LDS: %s", S::BYTES,
+            return dgm::fail(g, DGM_ERR_HIP, "dit_backward: cannot reserve %d bytes of LDS: %s", bytes,
                              hipGetErrorString(e));
     }
-    hipLaunchKernelGGL(k, dim3(unsigned(8 * ((a.B + 7) / 8) * 2 * TT)), dim3(1024), size_t(S::BYTES), g->stream, a);
+    a.own = 8 * ((a.B + 7) / 8) * 2 * TT;
+    hipLaunchKernelGGL(k, dim3(unsigned(a.own + a.dw_tiles)), dim3(1024), size_t(bytes), g->stream, a);
     return dgm::check_launch(g, "dit_backward loop_attn_bwd");
 }
 
@@ -1108,9 +1124,15 @@ bool dit_attn_bwd_loop_ok(const dgm_dit_cfg* c, const float* acts, const float* 
 
 int dit_attn_bwd_loop(dgm_gpu* g, const dgm_dit_cfg* c, const float* q, const float* k, const float* v,
                       const float* probs, const float* o, const float* dout, const float* cosv, const float* sinv,
-                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first, bool fresh) {
+                      float* dq, int ldq, float* dk, float* dv, int ldkv, float* dfirst, bool first, bool fresh,
+                      const dgm_dw::DwTileArgs* dw) {
     if (!dit_attn_bwd_loop_ok(c, q, dout)) return kNotFused;
     LoopAttnBwdArgs a{};
+    if (dw) {
+        a.dw = *dw;
+        a.dw_tiles = dgm_dw::dw_tiles(*dw);
+        a.dw_tiles_n = dgm_dw::dw_tiles_n(*dw);
+    }
     a.q = q; a.k = k; a.v = v; a.probs = probs; a.o = o; a.dout = dout; a.cosv = cosv; a.sinv = sinv;
     a.dq = dq; a.ldq = ldq; a.dk = dk; a.dv = dv; a.ldkv = ldkv; a.dfirst = dfirst;
     a.B = c->B; a.vmix = first ? 0 : 1; a.fresh = fresh ? 1 : 0; a.ca = 1.0f - c->mix; a.mixc = c->mix;

@@ -137,10 +137,16 @@ struct RmsChainArgs {
     float* dwp[2];
     int npend, npin;
     int rows, cols, ndx, ndw, ndd;   // ndd: stage 0's weight-gradient workgroups (8 columns each)
+    dgm_dw::DwTileArgs dw;           // a linear's dW run beside the chain (it reads none of its outputs)
+    int dw_tiles, dw_tiles_n;        // its 32 x 16 tiles, one per workgroup after the others
 };
 
 __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainArgs a) {
-    __shared__ float part[kDwWaves][kChainCols];
+    static_assert(kDwWaves == dgm_dw::kHostedWaves, "one dW tile per workgroup");
+    // part[kDwWaves][kChainCols] for the chain, 32 KB for a dW tile.
+    constexpr int kDwFloats = dgm_dw::kHostedWaves * 2 * 16 * 16;
+    __shared__ __align__(16) float lds[kDwWaves * kChainCols > kDwFloats ? kDwWaves * kChainCols : kDwFloats];
+    float (*part)[kChainCols] = reinterpret_cast<float (*)[kChainCols]>(lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cols = a.cols, rows = a.rows;
     constexpr int NPL = kChainCols / 64;
@@ -249,8 +255,14 @@ __global__ __launch_bounds__(64 * kDwWaves) void rms_bwd_chain_kernel(RmsChainAr
         }
         return;
     }
-    // The pending partial sums: 64 columns per workgroup.
     const int pr = rest - a.ndd;
+    if (pr >= a.ndw * a.npend) {
+        dgm_dw::dw_tile<2, dgm_dw::kPairCH, dgm_dw::kHostedWaves>(a.dw, true, pr - a.ndw * a.npend, a.dw_tiles_n,
+                                                                  wave, int(threadIdx.x),
+                                                                  reinterpret_cast<float (*)[2][16][16]>(lds));
+        return;
+    }
+    // The pending partial sums: 64 columns per workgroup.
     const int pi = pr / a.ndw;
     const int c = (pr % a.ndw) * 64 + lane;
     float acc = 0.0f;
@@ -795,14 +807,14 @@ int launch_rms_bwd(dgm_gpu* g, const float* x, const float* rstd, const float* w
     return dgm::check_launch(g, "rms_bwd");
 }
 
-// a.ndx / a.ndw are filled in here.
+// a.ndx / a.ndw / a.ndd are filled in here; a.dw_tiles (0: none) and a.dw_tiles_n by the caller.
 int launch_rms_chain(dgm_gpu* g, RmsChainArgs a) {
     if (a.rows == 0 || a.cols == 0) return DGM_OK;
     a.ndx = (a.rows + kDwWaves - 1) / kDwWaves;
     a.ndw = (a.cols + 63) / 64;
     a.ndd = (a.cols + 7) / 8;
-    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndd + a.ndw * a.npend)), dim3(64 * kDwWaves), 0,
-                       g->stream, a);
+    hipLaunchKernelGGL(rms_bwd_chain_kernel, dim3(unsigned(a.ndx + a.ndd + a.ndw * a.npend + a.dw_tiles)),
+                       dim3(64 * kDwWaves), 0, g->stream, a);
     return dgm::check_launch(g, "rms_bwd");
 }
 
@@ -1288,8 +1300,13 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         return st;
     };
     auto run_chain = [&](const float* dy, float* dw0, int nst, const RmsStage* st, int npend, const float* pin0,
-                         float* dwp0, const float* pin1, float* dwp1) {
+                         float* dwp0, const float* pin1, float* dwp1, const dgm_dw::DwTileArgs* dw = nullptr) {
         RmsChainArgs ra{};
+        if (dw) {
+            ra.dw = *dw;
+            ra.dw_tiles = dgm_dw::dw_tiles(*dw);
+            ra.dw_tiles_n = dgm_dw::dw_tiles_n(*dw);
+        }
         ra.dy = dy; ra.dw0 = dw0; ra.nst = nst;
         for (int i = 0; i < nst; ++i) ra.st[i] = st[i];
         ra.npend = npend; ra.pin[0] = pin0; ra.dwp[0] = dwp0; ra.pin[1] = pin1; ra.dwp[1] = dwp1;
@@ -1350,7 +1367,21 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));
             DGM_TRY(rms_bwd(A(l, A_ATTN), A(l, A_R1B), w->n1b, t1, t2, gr->n1b, nullptr));
         }
-        DGM_TRY(bwdf(1, w->wo, dattn, A(l, A_AV), S[B_DAV], gr->wo, C, C));
+        // With the bf16-dX pair, the one-launch attention backward and the
+        // chained RMSNorm backwards, the dW tiles of wo run in the attention
+        // backward's launch and those of [wq; wk; wv] in the chain launch
+        // after them, beside work that reads none of what they write and
+        // writes none of what they read: their own launches are dX alone.
+        const dgm_dw::DwTileArgs dwo{dattn, A(l, A_AV), gr->wo, int(M), int(C), int(C), 1};
+        const dgm_dw::DwTileArgs dwq{qkvrow, A(l, A_LN1), gr->wq, int(M), int(QKV), int(C), 1};
+        bool host_wo = fold && attn1 && chain, host_wq = host_wo;
+        if (host_wo) {
+            const int r = dgm::gemm_bwd_fold(g, fct[1], fst[1], dattn, A(l, A_AV), S[B_DAV], nullptr, int(M), int(C),
+                                             int(C), G, true, nullptr, nullptr);
+            if (r == dgm::kNotFused) host_wo = false;
+            else DGM_TRY(r);
+        }
+        if (!host_wo) DGM_TRY(bwdf(1, w->wo, dattn, A(l, A_AV), S[B_DAV], gr->wo, C, C));
         // The attention backward with sum_heads of dk and dv, rope_bwd of dq
         // and dk and the value residual: one launch for the built shapes,
         // else attnBwd and the per-row gradient kernel.
@@ -1360,7 +1391,7 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         if (attn1) {
             const int ra = dgm::dit_attn_bwd_loop(g, c, A(l, A_Q), A(l, A_K), A(l, A_V), A(l, A_PROBS), A(l, A_AV),
                                                   S[B_DAV], cosv, sinv, oq, ldq, ok, ov, ldkv, S[B_DFIRST], l == 0,
-                                                  l == L - 1);
+                                                  l == L - 1, host_wo ? &dwo : nullptr);
             if (ra == dgm::kNotFused)
                 return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_backward: attention backward shape changed");
             DGM_TRY(ra);
@@ -1370,7 +1401,15 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(launch_qkv_grad(g, S[B_DQ], S[B_DK], S[B_DV], cosv, sinv, oq, ldq, ok, ldkv, ov, ldkv,
                                     S[B_DFIRST], B, T, H, D, l == 0, mix));
         }
-        if (qkv1) {
+        if (host_wq) {
+            const int r = dgm::gemm_bwd_fold(g, fct[0], fst[0], qkvrow, A(l, A_LN1), t2, nullptr, int(M), int(QKV),
+                                             int(C), G, true, nullptr, nullptr);
+            if (r == dgm::kNotFused) host_wq = false;
+            else DGM_TRY(r);
+        }
+        if (host_wq) {
+            // dX done; its dW runs in the chain launch below.
+        } else if (qkv1) {
             DGM_TRY(bwdf(0, w->wq, qkvrow, A(l, A_LN1), t2, gr->wq, QKV, C));
         } else {
             DGM_TRY(bwd(w->wq, S[B_QPRE], A(l, A_LN1), t2, gr->wq, C, C));
@@ -1387,11 +1426,11 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
                 const RmsStage st[3] = {stage(A(l, A_X), A(l, A_R1), w->n1, gx, t1, nullptr),
                                         stage(A(l - 1, A_PRE), A(l - 1, A_RF), w->nf, t1, nullptr, S[B_RPC]),
                                         stage(A(l - 1, A_MLP), A(l - 1, A_R2B), w->n2b, dln, nullptr, S[B_RPA])};
-                DGM_TRY(run_chain(t2, gr->n1, 3, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr));
+                DGM_TRY(run_chain(t2, gr->n1, 3, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr, host_wq ? &dwq : nullptr));
                 dmlp = dln;
             } else {
                 const RmsStage st[1] = {stage(A(l, A_X), A(l, A_R1), w->n1, gx, t1, nullptr)};
-                DGM_TRY(run_chain(t2, gr->n1, 1, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr));
+                DGM_TRY(run_chain(t2, gr->n1, 1, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr, host_wq ? &dwq : nullptr));
             }
         } else {
             DGM_TRY(rms_bwd(A(l, A_X), A(l, A_R1), w->n1, t2, gx, gr->n1, t1));   // gx = t1 + dx

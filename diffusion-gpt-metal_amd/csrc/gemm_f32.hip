@@ -18,6 +18,7 @@
 // These shapes (the DiT linears) are latency-bound, so the design keeps many
 // independent loads in flight per wave and many small workgroups.
 #include "common.hpp"
+#include "dw_tile.hpp"
 
 namespace {
 
@@ -1225,98 +1226,27 @@ int launch_dx_lds(dgm_gpu* g, const GemmArgs& a) {
 }
 
 // ---- dW with 2 or 4 columns per lane (M % 64 == 0, N % NP == 0) ------------------
-// dW[n, k] (=|+=) sum_m dY[m, n] * X[m, k]. A workgroup owns 16 NP rows (n) x 16
-// columns (k) of dW; its 4 waves split M and load their operands straight into
-// registers, CH 16-row chunks of loads issued before the first MFMA of a round.
-// A lane reads dY[m, n0 + NP i .. n0 + NP i + NP - 1] as one 8-byte (NP = 2) or
-// 16-byte (NP = 4) load, so 16 lanes cover one or two whole 128-byte lines of
-// a dY row; column e of the lane's NP feeds MFMA tile e (dW rows n0 + NP r + e).
-// At step s a lane group q uses row m = m0 + q + 4 s. Wave partials are
-// reduced through LDS in a fixed order. Every dW element is the same chain of
-// MFMAs over the same rows for any NP and CH, so the results are bitwise equal.
-// The 32 x 16 tile (NP = 2) takes two chunks per round (kPairCH): fewer
-// registers, more workgroups per CU (c2 pair 7.5-7.6 us against 7.8-7.9 with
-// eight; the DiT training step 324 us against 331; dW alone 2-7% faster at
-// the 32-row shapes; one chunk and four measured no better). The 64 x 16
-// tile (NP = 4, CH = 4, 110 VGPRs) runs dW alone where launch_dw_pair finds
-// it pays (c2 / c1: 5.4 us against 6.7 us). The deep-dX pair keeps eight
-// chunks (two measured 3% slower at the c1 shape).
-constexpr int DWP_CH = 8;    // 16-row chunks per wave and round beside the deep dX tiles
-constexpr int kPairCH = 2;   // the same for the 32 x 16 tiles elsewhere
+// The tile is dgm_dw::dw_tile (dw_tile.hpp): 16 NP rows (n) x 16 columns (k),
+// four waves splitting M, CH 16-row chunks of loads per round. The 32 x 16
+// tile (NP = 2) takes two chunks per round (kPairCH): fewer registers, more
+// workgroups per CU (c2 pair 7.5-7.6 us against 7.8-7.9 with eight; the DiT
+// training step 324 us against 331; dW alone 2-7% faster at the 32-row
+// shapes; one chunk and four measured no better). The 64 x 16 tile (NP = 4,
+// CH = 4, 110 VGPRs) runs dW alone where launch_dw_pair finds it pays (c2 /
+// c1: 5.4 us against 6.7 us). The deep-dX pair keeps eight chunks (two
+// measured 3% slower at the c1 shape).
+constexpr int DWP_CH = 8;                    // 16-row chunks per wave and round beside the deep dX tiles
+constexpr int kPairCH = dgm_dw::kPairCH;     // the same for the 32 x 16 tiles elsewhere
 
-// Body of one dW tile; `blk` as in dx_lds_tile, part: NP x 4 KB of LDS. Lanes
-// whose columns pass N load the last NP columns (N % NP == 0, so those lanes'
-// own rows are all >= N) and are never stored.
+// Body of one dW tile of a 256-thread workgroup; `blk` as in dx_lds_tile,
+// part: NP x 4 KB of LDS.
 template <int NP = 2, int CH = DWP_CH>
 __device__ __forceinline__ void dw_pair_tile(const GemmArgs& a, int tiles_n, int tiles_k, int per_xcd, int blk,
                                              float (*part)[NP][16][16]) {
-    static_assert(NP == 2 || NP == 4, "2 or 4 columns per lane");
     const int t = (blk & 7) * per_xcd + (blk >> 3);
-    if (t >= tiles_n * tiles_k) return;
-    const int tk = t / tiles_n, tn = t - tk * tiles_n;
-    const int n0 = tn * 16 * NP, k0 = tk * 16;
-    const int M = a.M, N = a.N, K = a.K;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r16 = lane & 15, q4 = lane >> 4;
-    const int nc = min(n0 + NP * r16, N - NP);
-    const int kc = min(k0 + r16, K - 1);
-    const float* X = static_cast<const float*>(a.B);
-    const int per = M >> 2;
-    const int mb = wave * per;
-
-    f32x4 acc[NP];
-#pragma unroll
-    for (int e = 0; e < NP; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int r0 = mb; r0 < mb + per; r0 += 16 * CH) {
-        float av[CH][4][NP];
-        float bv[CH][4];
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int m0 = min(r0 + 16 * c, mb + per - 16);   // past the range: re-read, not computed
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const int m = m0 + q4 + 4 * s2;
-                const float* src = a.A + size_t(m) * N + nc;
-                if constexpr (NP == 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(src);
-                    av[c][s2][0] = v.x; av[c][s2][1] = v.y; av[c][s2][2] = v.z; av[c][s2][3] = v.w;
-                } else {
-                    const float2 v = *reinterpret_cast<const float2*>(src);
-                    av[c][s2][0] = v.x; av[c][s2][1] = v.y;
-                }
-                bv[c][s2] = X[size_t(m) * K + kc];
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);   // every load of the round before the first MFMA
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            if (r0 + 16 * c >= mb + per) continue;
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2)
-#pragma unroll
-                for (int e = 0; e < NP; ++e)
-                    acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][s2][e], bv[c][s2], acc[e], 0, 0, 0);
-        }
-    }
-    // acc[e][r]: dW row n0 + NP (4 q4 + r) + e, column k0 + r16.
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int e = 0; e < NP; ++e) part[wave][e][4 * q4 + r][r16] = acc[e][r];
-    __syncthreads();
-    for (int e = threadIdx.x; e < 16 * NP * 16; e += kThreads) {
-        const int il = e >> 4, j = e & 15;   // il: local dW row 0 .. 16 NP - 1
-        const int i = n0 + il, k = k0 + j;
-        if (i >= N || k >= K) continue;
-        const int rr = il / NP, par = il - rr * NP;
-        float v = part[0][par][rr][j];
-        v += part[1][par][rr][j];
-        v += part[2][par][rr][j];
-        v += part[3][par][rr][j];
-        float* o = a.out + size_t(i) * K + k;
-        if (a.accumulate) *o += v;
-        else *o = v;
-    }
+    if (t >= tiles_n * tiles_k) return;   // the whole workgroup: no barrier is skipped by part of it
+    const dgm_dw::DwTileArgs d{a.A, static_cast<const float*>(a.B), a.out, a.M, a.N, a.K, a.accumulate};
+    dgm_dw::dw_tile<NP, CH>(d, true, t, tiles_n, int(threadIdx.x >> 6), int(threadIdx.x), part);
 }
 
 template <int NP, int CH>
@@ -1874,7 +1804,7 @@ int gemm_bwd_fold(dgm_gpu* g, const int8_t* codesT, const float* scalesT, const 
     const int tm = M / 16, tk = K / 32;
     const int per_x = (tm * tk + 7) / 8;
     const int tn = int(ceil_div(N, 32)), tkw = int(ceil_div(K, 16));
-    const int per_w = (tn * tkw + 7) / 8;
+    const int per_w = dW ? (tn * tkw + 7) / 8 : 0;   // no dW: the dX tiles alone
     hipLaunchKernelGGL(gemm_bwd_fold_pair_kernel, dim3(unsigned(per_x + per_w) * 8u), dim3(kThreads), 0, g->stream, ax,
                        tm, tk, per_x, aw, tn, tkw, per_w);
     return check_launch(g, "gemm_bwd_fold");
