@@ -1318,10 +1318,16 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
     const bool attn1 = dgm::dit_attn_bwd_loop_ok(c, acts, ws);
     if (!attn1) DGM_TRY(dgm_zero(g, S[B_DFIRST], nKV));
     const int L = c->loops;
-    float* dmlp = t2;   // dL/dmlp of the loop about to run
+    // With the bf16-dX pair, the chained RMSNorm backwards and the one-launch
+    // attention backward (which leaves the dq scratch unused), dL/dmlp lives
+    // in that scratch until the loop's first chain launch, which runs wdown's
+    // dW tiles beside its own work (it writes none of dL/dmlp, sw or that dW).
+    const bool host_wd = fold && chain && attn1;
+    float* const mlpd = host_wd ? S[B_DQ] : nullptr;
+    float* dmlp = host_wd ? mlpd : t2;   // dL/dmlp of the loop about to run
     if (chain && L > 0) {
         const RmsStage st[2] = {stage(A(L - 1, A_PRE), A(L - 1, A_RF), w->nf, t1, nullptr, nullptr),
-                                stage(A(L - 1, A_MLP), A(L - 1, A_R2B), w->n2b, t2, nullptr, S[B_RPA])};
+                                stage(A(L - 1, A_MLP), A(L - 1, A_R2B), w->n2b, dmlp, nullptr, S[B_RPA])};
         DGM_TRY(run_chain(gx, gr->nf, 2, st, 0, nullptr, nullptr, nullptr, nullptr));
     }
     for (int l = L - 1; l >= 0; --l) {
@@ -1329,15 +1335,19 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             DGM_TRY(rms_bwd(A(l, A_PRE), A(l, A_RF), w->nf, gx, t1, gr->nf, nullptr));
             DGM_TRY(rms_bwd(A(l, A_MLP), A(l, A_R2B), w->n2b, t1, t2, gr->n2b, nullptr));
         }
+        bool hwd = host_wd;
+        const dgm_dw::DwTileArgs dwd{dmlp, A(l, A_SW), gr->wdown, int(M), int(C), int(F), 1};
         if (gu1) {
             // wdown's backward with the SwiGLU backward in its dX epilogue,
             // else the two launches.
-            const int r = fold ? dgm::gemm_bwd_fold(g, fct[3], fst[3], dmlp, A(l, A_SW), S[B_DG], gr->wdown, int(M),
-                                                    int(C), int(F), G, true, A(l, A_GATE), A(l, A_UP))
+            const int r = fold ? dgm::gemm_bwd_fold(g, fct[3], fst[3], dmlp, A(l, A_SW), S[B_DG],
+                                                    hwd ? nullptr : gr->wdown, int(M), int(C), int(F), G, true,
+                                                    A(l, A_GATE), A(l, A_UP))
                                : dgm::gemm_bwd_swiglu(g, bits, w->wdown.w, w->wdown.q, w->wdown.scale, dmlp,
                                                       A(l, A_SW), A(l, A_GATE), A(l, A_UP), S[B_DG], gr->wdown, M, C,
                                                       F, bits == 32 ? 8 : G);
             if (r == dgm::kNotFused) {
+                hwd = false;
                 DGM_TRY(bwd(w->wdown, dmlp, A(l, A_SW), S[B_DSW], gr->wdown, C, F));
                 DGM_TRY(launch_swiglu_bwd(g, A(l, A_GATE), A(l, A_UP), S[B_DSW], S[B_DG], S[B_DG] + F, M * F, F,
                                           2 * F));
@@ -1359,9 +1369,9 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
             const RmsStage st[2] = {stage(A(l, A_MID), A(l, A_R2), w->n2, t1, t1, nullptr),
                                     stage(A(l, A_ATTN), A(l, A_R1B), w->n1b, dln, nullptr, S[B_RPB])};
             if (l == L - 1)   // nf's gradient was direct in the first chain
-                DGM_TRY(run_chain(t2, gr->n2, 2, st, 1, S[B_RPA], gr->n2b, nullptr, nullptr));
+                DGM_TRY(run_chain(t2, gr->n2, 2, st, 1, S[B_RPA], gr->n2b, nullptr, nullptr, hwd ? &dwd : nullptr));
             else
-                DGM_TRY(run_chain(t2, gr->n2, 2, st, 2, S[B_RPA], gr->n2b, S[B_RPC], gr->nf));
+                DGM_TRY(run_chain(t2, gr->n2, 2, st, 2, S[B_RPA], gr->n2b, S[B_RPC], gr->nf, hwd ? &dwd : nullptr));
             dattn = dln;
         } else {
             DGM_TRY(rms_bwd(A(l, A_MID), A(l, A_R2), w->n2, t2, t1, gr->n2, t1));
@@ -1421,13 +1431,15 @@ int dgm_dit_backward(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w,
         if (chain) {
             // gx = t1 + dx of n1 (and the pending n1b sums); below loop 0 the
             // next loop's nf and n2b backwards follow in the same launch, its
-            // dL/dmlp going to dln (t2 is read by the direct workgroups).
+            // dL/dmlp going to the dq scratch when wdown's dW is hosted, else
+            // to dln (t2 is read by the direct workgroups).
             if (l > 0) {
                 const RmsStage st[3] = {stage(A(l, A_X), A(l, A_R1), w->n1, gx, t1, nullptr),
                                         stage(A(l - 1, A_PRE), A(l - 1, A_RF), w->nf, t1, nullptr, S[B_RPC]),
-                                        stage(A(l - 1, A_MLP), A(l - 1, A_R2B), w->n2b, dln, nullptr, S[B_RPA])};
+                                        stage(A(l - 1, A_MLP), A(l - 1, A_R2B), w->n2b, host_wd ? mlpd : dln,
+                                              nullptr, S[B_RPA])};
                 DGM_TRY(run_chain(t2, gr->n1, 3, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr, host_wq ? &dwq : nullptr));
-                dmlp = dln;
+                dmlp = host_wd ? mlpd : dln;
             } else {
                 const RmsStage st[1] = {stage(A(l, A_X), A(l, A_R1), w->n1, gx, t1, nullptr)};
                 DGM_TRY(run_chain(t2, gr->n1, 1, st, 1, S[B_RPB], gr->n1b, nullptr, nullptr, host_wq ? &dwq : nullptr));
