@@ -1,6 +1,6 @@
 // Looped DiT block forward in three launches per loop (src/DiT.swift:520-550),
 // for the block shapes it is built for: int8 / int4 linears with group 32,
-// one KV head, C a multiple of 64, F a multiple of 128.
+// one KV head, C a multiple of 64, F a multiple of the mlp slice (96 or 128 columns).
 //
 //  * loop_row_kernel: one workgroup of 16 waves per (16 rows, column group);
 //    wave w owns row w. The row chain that closes the previous loop
@@ -13,10 +13,10 @@
 //    rows): scores, row softmax and P.V on fp32 MFMA (the stages of
 //    attn_mfma_kernel in dit.hip, every query head against the one KV head),
 //    the wo projection, then mid = x + rms(attn)*n1b and ln2 = rms(mid)*n2.
-//  * loop_mlp_kernel: one workgroup of 8 waves per (16 rows, slice of 128
+//  * loop_mlp_kernel: one workgroup of SL / 16 waves per (16 rows, slice of SL
 //    SwiGLU columns): gate and up of those columns, SwiGLU, and the slice's
-//    share of wdown (its sum over the slice's 128 contraction indices) into
-//    slab `slice` of [P][M][C].
+//    share of wdown (its sum over the slice's SL contraction indices) into
+//    slab `slice` of [P][M][C], P = F / SL.
 //  * loop_tail_kernel after the last loop: the closing row chain.
 // A sequence's workgroups run on one XCD (block b + 8 j), where the previous
 // launch left its rows.
@@ -52,7 +52,19 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSlice = 128;          // SwiGLU columns per mlp workgroup (8 waves x 16)
+// SwiGLU columns per mlp workgroup (16 per wave): 128, or 96 when that gives
+// at most one workgroup per CU of the MI355X's 256 where 128 would leave CUs
+// idle. A workgroup's weight codes set the kernel's time (a CU receives them
+// at a bounded rate): at c3, 96 columns bring 55 KB of codes to each of 256
+// CUs instead of 74 KB to each of 192. The choice depends on the shape alone,
+// so the workspace size does too.
+constexpr int kSlice = 128;
+constexpr int64_t kSliceCus = 256;
+int slice_cols(const dgm_dit_cfg* c) {
+    const int64_t tiles = int64_t(c->B) * c->T / 16;
+    if (c->F % 96 == 0 && tiles * (c->F / 96) <= kSliceCus && tiles * (c->F / kSlice) < kSliceCus) return 96;
+    return kSlice;
+}
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
     const f32x2 v = {a, b};
@@ -554,7 +566,7 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
 }
 
 // ---- loop_mlp_kernel ------------------------------------------------------------------
-// One workgroup of 8 waves per (16 rows, slice of kSlice SwiGLU columns).
+// One workgroup of SL / 16 waves per (16 rows, slice of SL SwiGLU columns).
 struct LoopMlpArgs {
     const float* ln2;        // [M, C]
     const void* Wgu;         // [2F, C] codes of wgate, wup back to back
@@ -566,23 +578,25 @@ struct LoopMlpArgs {
     int B, TT, M, F, P;
 };
 
-template <int BITS, int KS>
-__global__ __launch_bounds__(512) void loop_mlp_kernel(LoopMlpArgs a) {
+template <int BITS, int KS, int SL>
+__global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
 #pragma clang fp contract(off)
-    constexpr int C = 32 * KS, J = C / 64, LDA = C + 8, LDW = kSlice + 8, FKS = kSlice / 32;
-    constexpr int DPW = (2 * KS + 7) / 8;   // wdown column tiles per wave
+    constexpr int C = 32 * KS, J = C / 64, LDA = C + 8, LDW = SL + 8, FKS = SL / 32;
+    constexpr int NW = SL / 16;                 // waves
+    constexpr int DPW = (2 * KS + NW - 1) / NW;   // wdown column tiles per wave
+    static_assert(SL % 32 == 0 && NW >= 4, "whole 32-k steps; four waves stage the ln2 rows");
     __shared__ __align__(16) __bf16 Ah[3 * 16 * LDA];
     __shared__ __align__(16) __bf16 Sw[3 * 16 * LDW];
     int b, item;
     if (!seq_block(a.B, a.TT * a.P, b, item)) return;
     const int slice = item % a.P;
     const size_t row0 = (size_t(b) * a.TT + item / a.P) * 16;
-    const int f0 = slice * kSlice;
+    const int f0 = slice * SL;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
 
     // ln2 rows, then the codes: gate / up column tile `wave`, wdown column
-    // tiles wave, wave + 8, ...
+    // tiles wave, wave + NW, ...
     float4 xv[J];
     if (wave < 4) {
 #pragma unroll
@@ -603,7 +617,7 @@ __global__ __launch_bounds__(512) void loop_mlp_kernel(LoopMlpArgs a) {
     float dsc[DPW][FKS];
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
-        const int ct = wave + 8 * i;
+        const int ct = wave + NW * i;
         if (ct < 2 * KS) {
 #pragma unroll
             for (int s = 0; s < FKS; ++s) dw[i][s] = codes_at<BITS>(a.Wd, size_t(ct * 16 + r16), a.F, f0 + 32 * s + 8 * q4);
@@ -640,10 +654,10 @@ __global__ __launch_bounds__(512) void loop_mlp_kernel(LoopMlpArgs a) {
     }
     lds_barrier();
 
-    // The slice's share of wdown: sw[:, f0 : f0 + kSlice] . wdown[:, f0 : f0 + kSlice]^T.
+    // The slice's share of wdown: sw[:, f0 : f0 + SL] . wdown[:, f0 : f0 + SL]^T.
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
-        const int ct = wave + 8 * i;
+        const int ct = wave + NW * i;
         if (ct >= 2 * KS) break;
         f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -956,7 +970,7 @@ __global__ __launch_bounds__(1024) void loop_attn_bwd_kernel(LoopAttnBwdArgs a) 
 }
 
 // ---- host side -------------------------------------------------------------------------
-template <int BITS, int KS, int TT, int DT, int NP>
+template <int BITS, int KS, int TT, int DT, int NP, int SL>
 int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv, const float* sinv,
               float* x, const dgm::DitLoopBufs& buf, const dgm::DitSaves* sv) {
     using S = AttnShape<KS, TT, DT>;
@@ -1026,7 +1040,8 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         ma.part = buf.part;
         if (sv) { ma.sgate = sv[l].gate; ma.sup = sv[l].up; ma.ssw = sv[l].sw; }
         ma.B = B; ma.TT = TT; ma.M = M; ma.F = c->F; ma.P = NP;
-        hipLaunchKernelGGL((loop_mlp_kernel<BITS, KS>), dim3(unsigned(gb * TT * NP)), dim3(512), 0, g->stream, ma);
+        hipLaunchKernelGGL((loop_mlp_kernel<BITS, KS, SL>), dim3(unsigned(gb * TT * NP)), dim3(4 * SL), 0, g->stream,
+                           ma);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_mlp");
     }
     if (L > 0) {
@@ -1044,19 +1059,26 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
     return DGM_OK;
 }
 
-// The built shapes: (C / 32, T / 16, D / 16, F / kSlice).
+// The built shapes: (C / 32, T / 16, D / 16, F / SL, SL).
 template <int BITS>
 int dispatch(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const float* cosv, const float* sinv,
              float* x, const dgm::DitLoopBufs& buf, const dgm::DitSaves* sv) {
-    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16, np = c->F / kSlice;
-    if (ks == 6 && tt == 4 && dt == 3 && np == 6) return run_loops<BITS, 6, 4, 3, 6>(g, c, w, cosv, sinv, x, buf, sv);
-    if (ks == 2 && tt == 1 && dt == 1 && np == 1) return run_loops<BITS, 2, 1, 1, 1>(g, c, w, cosv, sinv, x, buf, sv);
+    const int sl = slice_cols(c);
+    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16, np = c->F / sl;
+    if (ks == 6 && tt == 4 && dt == 3 && np == 8 && sl == 96)
+        return run_loops<BITS, 6, 4, 3, 8, 96>(g, c, w, cosv, sinv, x, buf, sv);
+    if (ks == 6 && tt == 4 && dt == 3 && np == 6 && sl == 128)
+        return run_loops<BITS, 6, 4, 3, 6, 128>(g, c, w, cosv, sinv, x, buf, sv);
+    if (ks == 2 && tt == 1 && dt == 1 && np == 1 && sl == 128)
+        return run_loops<BITS, 2, 1, 1, 1, 128>(g, c, w, cosv, sinv, x, buf, sv);
     return dgm::fail(g, DGM_ERR_UNSUPPORTED, "dit_forward: no loop kernels built for this shape");
 }
 
 bool shape_built(const dgm_dit_cfg* c) {
-    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16, np = c->F / kSlice;
-    return (ks == 6 && tt == 4 && dt == 3 && np == 6) || (ks == 2 && tt == 1 && dt == 1 && np == 1);
+    const int sl = slice_cols(c);
+    const int ks = c->C / 32, tt = c->T / 16, dt = c->D / 16, np = c->F / sl;
+    return (ks == 6 && tt == 4 && dt == 3 && ((np == 8 && sl == 96) || (np == 6 && sl == 128))) ||
+           (ks == 2 && tt == 1 && dt == 1 && np == 1 && sl == 128);
 }
 
 
@@ -1086,13 +1108,13 @@ namespace dgm {
 bool dit_loop_shape_ok(const dgm_dit_cfg* c) {
     if (!c || (c->bits != 8 && c->bits != 4) || c->group != 32 || c->loops < 0 || c->B <= 0) return false;
     if (c->C % 64 != 0 || c->D % 16 != 0 || c->H * c->D != c->C || c->T % 16 != 0) return false;
-    if (c->F % kSlice != 0 || c->F <= 0) return false;
+    if (c->F <= 0 || c->F % slice_cols(c) != 0) return false;
     return shape_built(c);
 }
 
 int64_t dit_loop_part_floats(const dgm_dit_cfg* c) {
     if (!dit_loop_shape_ok(c)) return 0;
-    return int64_t(c->F / kSlice) * c->B * c->T * c->C;
+    return int64_t(c->F / slice_cols(c)) * c->B * c->T * c->C;
 }
 
 bool dit_loop_ok(const dgm_dit_cfg* c, const dgm_dit_weights* w) {
