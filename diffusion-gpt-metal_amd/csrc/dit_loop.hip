@@ -28,8 +28,9 @@
 // is left, at most 8 bits). Every product is exact; each 32-k group's sum is
 // accumulated in fp32 (lo, mid, then hi pieces) and multiplied by the group's
 // scale. RoPE, softmax, SwiGLU and the row chains use the standalone kernels'
-// formulas (the chains' rstd with the hardware inverse square root), so
-// results agree with the oracle to fp32 rounding of the sums.
+// formulas (the chains' rstd with the hardware inverse square root, the
+// softmax's exponential as the hardware 2^x of x log2 e, within a few ulp of
+// expf), so results agree with the oracle to fp32 rounding of the sums.
 #include <algorithm>
 #include <cmath>
 
@@ -484,7 +485,8 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     lds_barrier();
 
     // -- row softmax, 16 lanes per (head, query row): attn_softmax's max, sum
-    // of exp and normalize (each exp computed once).
+    // of exp and normalize (each exp computed once, on the hardware 2^x: the
+    // library expf made this phase VALU-bound with 16 waves on 4 SIMDs).
     for (int rr = 4 * wave + q4; rr < H * 16; rr += 64) {
         float* rp = ps + rr * VLD;
         float ev[TT];
@@ -498,7 +500,7 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
         float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < TT; ++i) {
-            ev[i] = expf(ev[i] - mx);
+            ev[i] = __builtin_amdgcn_exp2f((ev[i] - mx) * 1.44269504088896341f);   // e^x = 2^(x log2 e)
             sum += ev[i];
         }
         sum = row16_sum(sum);
