@@ -29,8 +29,9 @@
 // accumulated in fp32 (lo, mid, then hi pieces) and multiplied by the group's
 // scale. RoPE, softmax, SwiGLU and the row chains use the standalone kernels'
 // formulas (the chains' rstd with the hardware inverse square root, the
-// softmax's exponential as the hardware 2^x of x log2 e, within a few ulp of
-// expf), so results agree with the oracle to fp32 rounding of the sums.
+// softmax's and SwiGLU's exponentials as the hardware 2^x of x log2 e, within
+// a few ulp of expf), so results agree with the oracle to fp32 rounding of
+// the sums.
 #include <algorithm>
 #include <cmath>
 
@@ -567,6 +568,14 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     }
 }
 
+// swiglu_fwd's logistic (metal/kernels.metal:911-930), sign-split as
+// silu_sigmoid, with the exponential as the hardware 2^x of x log2 e.
+__device__ __forceinline__ float silu_sigmoid_hw(float z) {
+#pragma clang fp contract(off)
+    const float e = __builtin_amdgcn_exp2f(-fabsf(z) * 1.44269504088896341f);   // e^-|z|
+    return z >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+}
+
 // ---- loop_mlp_kernel ------------------------------------------------------------------
 // One workgroup of SL / 16 waves per (16 rows, slice of SL SwiGLU columns).
 struct LoopMlpArgs {
@@ -644,7 +653,7 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
     for (int e = 0; e < 4; ++e) {
         const int r = 4 * q4 + e;
         const float z = ag[e];
-        const float act = z * silu_sigmoid(z);
+        const float act = z * silu_sigmoid_hw(z);
         const float sw = act * au[e];
         if (a.sgate) {
             const size_t o = (row0 + r) * a.F + f0 + wave * 16 + r16;
