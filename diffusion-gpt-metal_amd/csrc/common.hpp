@@ -159,6 +159,19 @@ __device__ inline void swiglu_bwd_value(float z, float u, float g, float& dgate,
     dup = silu * g;
 }
 
+// The same with the logistic's exponential as the hardware 2^x of x log2 e
+// (e^-|z| for both signs, no branch; within a few ulp of expf), as the DiT
+// loop kernels' forward SwiGLU computes it.
+__device__ inline void swiglu_bwd_value_hw(float z, float u, float g, float& dgate, float& dup) {
+#pragma clang fp contract(off)
+    const float e = __builtin_amdgcn_exp2f(-fabsf(z) * 1.44269504088896341f);
+    const float s = z >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+    const float silu = z * s;
+    const float siluP = s * (1.0f + z * (1.0f - s));
+    dgate = siluP * u * g;
+    dup = silu * g;
+}
+
 // gemmBwd (dW += dY^T X, dX = dY W) of a linear whose input was
 // SwiGLU(gate, up) [M, K], with the SwiGLU backward applied to dX in the same
 // launch: dgu gets [M, 2K] rows [dgate | dup]. Returns kNotFused, having

@@ -1481,7 +1481,7 @@ __device__ __forceinline__ void dx_fold_tile(const DxFoldArgs& a, int tiles_m, i
         if (a.sg_gate) {
             const size_t ei = size_t(i) * K + k;
             float* o = a.out + size_t(i) * 2 * K + k;
-            dgm::swiglu_bwd_value(a.sg_gate[ei], a.sg_up[ei], v, o[0], o[K]);
+            dgm::swiglu_bwd_value_hw(a.sg_gate[ei], a.sg_up[ei], v, o[0], o[K]);
         } else {
             a.out[size_t(i) * K + k] = v;
         }
