@@ -9,12 +9,15 @@
 //    ln1 = rms(x)*n1, and the group's columns of the [wq; wk; wv] projection
 //    (HG query heads, or k | v), with RoPE on q and k and the value residual
 //    on v.
-//  * loop_attn_kernel: one workgroup of 16 waves per (sequence b, 16 query
+//  * loop_attn_kernel: two workgroups of 16 waves per (sequence b, 16 query
 //    rows): scores, row softmax and P.V on fp32 MFMA (the stages of
 //    attn_mfma_kernel in dit.hip, every query head against the one KV head),
-//    the wo projection, then mid = x + rms(attn)*n1b and ln2 = rms(mid)*n2.
+//    each workgroup then half of the wo projection's output columns (half of
+//    the wo codes per CU).
 //  * loop_mlp_kernel: one workgroup of SL / 16 waves per (16 rows, slice of SL
-//    SwiGLU columns): gate and up of those columns, SwiGLU, and the slice's
+//    SwiGLU columns): the row chain mid = x + rms(attn)*n1b and ln2 =
+//    rms(mid)*n2 of its 16 rows (stored by the slice-0 workgroup), gate and up
+//    of those columns, SwiGLU, and the slice's
 //    share of wdown (its sum over the slice's SL contraction indices) into
 //    slab `slice` of [P][M][C], P = F / SL.
 //  * loop_tail_kernel after the last loop: the closing row chain.
@@ -381,25 +384,21 @@ struct LoopAttnArgs {
     const float* q;          // [M, C] after RoPE
     const float *k, *v;      // rows of kv_ld floats, the KV head at column 0
     int kv_ld;
-    const float* x;          // this loop's x [M, C] (the residual)
-    const float *n1b, *n2;
     const void* Wo;          // [C, C]
     const float* So;
-    float *mid, *ln2;        // outputs [M, C]
+    float* attn;             // output [M, C]: av . wo^T
     float* probs;            // optional [B, H, T, T]
-    float *sav, *sattn, *sr1b, *sr2;   // optional training saves
+    float* sav;              // optional training save of av
     int B;
-    float eps, scale;
+    float scale;
 };
 
 template <int KS, int TT, int DT>
 struct AttnShape {
     static constexpr int C = 32 * KS, D = 16 * DT, H = C / D, T = 16 * TT;
     static constexpr int LDA = C + 8, QLD = C + 4, KLD = D + 4, VLD = T + 4;
-    static constexpr int QS = 0, XS = QS + 16 * QLD * 4, KO = XS + 16 * QLD * 4, VT = KO + T * KLD * 4;
-    static constexpr int PS = VT + D * VLD * 4, AV = PS + H * 16 * VLD * 4, AT = AV + 3 * 16 * LDA * 2;
-    static constexpr int NRM = AT + 16 * QLD * 4, BYTES = NRM + 2 * C * 4;
-    static constexpr int WPW = (2 * KS + 15) / 16;   // wo column tiles per wave
+    static constexpr int QS = 0, KO = QS + 16 * QLD * 4, VT = KO + T * KLD * 4;
+    static constexpr int PS = VT + D * VLD * 4, AV = PS + H * 16 * VLD * 4, BYTES = AV + 3 * 16 * LDA * 2;
     static_assert(KS % 2 == 0 && C % D == 0 && TT >= 1 && C / 4 <= 64, "loop_attn shape");
     static_assert(BYTES <= 160 * 1024, "loop_attn LDS");
 };
@@ -412,40 +411,35 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     constexpr int LDA = S::LDA, QLD = S::QLD, KLD = S::KLD, VLD = S::VLD;
     extern __shared__ __align__(16) unsigned char lds[];
     float* qs = reinterpret_cast<float*>(lds + S::QS);
-    float* xs = reinterpret_cast<float*>(lds + S::XS);
     float* ks = reinterpret_cast<float*>(lds + S::KO);
     float* vt = reinterpret_cast<float*>(lds + S::VT);
     float* ps = reinterpret_cast<float*>(lds + S::PS);
     __bf16* Av = reinterpret_cast<__bf16*>(lds + S::AV);
-    float* at = reinterpret_cast<float*>(lds + S::AT);
-    float* nrm = reinterpret_cast<float*>(lds + S::NRM);   // n1b | n2
-    int b, qt;
-    if (!seq_block(a.B, TT, b, qt)) return;
+    int b, item;
+    if (!seq_block(a.B, 2 * TT, b, item)) return;
+    const int qt = item >> 1, half = item & 1;   // half: wo's output column tiles [KS half, KS half + KS)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t seq0 = size_t(b) * T, own0 = seq0 + size_t(qt) * 16;
 
-    // -- wo codes of this wave's column tiles, then q, x (16 rows), k, v (T
-    // rows) and the norms, all issued before any is used.
-    uint2 wo[S::WPW][KS];
-    float wos[S::WPW][KS];
+    // -- wo codes of this wave's column tile (waves 0 .. KS-1), then q (16
+    // rows), k, v (T rows), all issued before any is used.
+    static_assert(KS <= 16, "one wo column tile per wave");
+    const int ct = half * KS + wave;   // this wave's wo column tile when wave < KS
+    uint2 wo[KS];
+    float wos[KS];
+    if (wave < KS) {
 #pragma unroll
-    for (int i = 0; i < S::WPW; ++i) {
-        const int ct = wave + 16 * i;
-        if (ct < 2 * KS) {
-#pragma unroll
-            for (int s = 0; s < KS; ++s) wo[i][s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, 32 * s + 8 * q4);
-            load_scales<KS>(a.So + size_t(ct * 16 + r16) * KS, wos[i]);
-        }
+        for (int s = 0; s < KS; ++s) wo[s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, 32 * s + 8 * q4);
+        load_scales<KS>(a.So + size_t(ct * 16 + r16) * KS, wos);
     }
-    constexpr int QC = 16 * C / 4, KC = T * D / 4, NC = 2 * C / 4;   // float4 chunks
+    constexpr int QC = 16 * C / 4, KC = T * D / 4;   // float4 chunks
     constexpr int RQ = (QC + 1023) / 1024, RK = (KC + 1023) / 1024;
-    float4 qv[RQ], xv[RQ], kv[RK], vv[RK], nv;
+    float4 qv[RQ], kv[RK], vv[RK];
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
         const int e = min(tid + 1024 * i, QC - 1), r = e / (C / 4), c4 = e - r * (C / 4);
         qv[i] = ld4(a.q + (own0 + r) * C + 4 * c4);
-        xv[i] = ld4(a.x + (own0 + r) * C + 4 * c4);
     }
 #pragma unroll
     for (int i = 0; i < RK; ++i) {
@@ -453,14 +447,10 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
         kv[i] = ld4(a.k + (seq0 + t) * a.kv_ld + 4 * c4);
         vv[i] = ld4(a.v + (seq0 + t) * a.kv_ld + 4 * c4);
     }
-    if (tid < NC) nv = ld4((tid < C / 4 ? a.n1b : a.n2) + 4 * (tid % (C / 4)));
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
         const int e = tid + 1024 * i, r = e / (C / 4), c4 = e - r * (C / 4);
-        if (e < QC) {
-            st4(qs + r * QLD + 4 * c4, qv[i]);
-            st4(xs + r * QLD + 4 * c4, xv[i]);
-        }
+        if (e < QC) st4(qs + r * QLD + 4 * c4, qv[i]);
     }
 #pragma unroll
     for (int i = 0; i < RK; ++i) {
@@ -473,7 +463,6 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
             vt[(4 * c4 + 3) * VLD + t] = vv[i].w;
         }
     }
-    if (tid < NC) st4(nrm + 4 * tid, nv);
     lds_barrier();
 
     // -- scores = (q . k) * scale per (head, 16 keys).
@@ -506,7 +495,8 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
         }
         sum = row16_sum(sum);
         const float inv = 1.0f / sum;
-        float* po = a.probs ? a.probs + ((size_t(b) * H + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T : nullptr;
+        float* po = a.probs && half == 0 ? a.probs + ((size_t(b) * H + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T
+                                         : nullptr;
 #pragma unroll
         for (int i = 0; i < TT; ++i) {
             const float pv = ev[i] * inv;
@@ -524,47 +514,20 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = 4 * q4 + e;
-            if (a.sav) a.sav[(own0 + r) * C + col] = acc[e];
+            if (a.sav && half == 0) a.sav[(own0 + r) * C + col] = acc[e];
             put1(Av, 16 * LDA, r * LDA + col, acc[e]);
         }
     }
     lds_barrier();
 
-    // -- attn = av . wo^T.
-#pragma unroll
-    for (int i = 0; i < S::WPW; ++i) {
-        const int ct = wave + 16 * i;
-        if (ct >= 2 * KS) break;
+    // -- attn = av . wo^T, this workgroup's half of the columns.
+    if (wave < KS) {
         f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < KS; ++s)
-            acc = scale_add(acc, step3(Av + r16 * LDA + 32 * s + 8 * q4, 16 * LDA, codes_bf16<BITS>(wo[i][s])),
-                            wos[i][s]);
+            acc = scale_add(acc, step3(Av + r16 * LDA + 32 * s + 8 * q4, 16 * LDA, codes_bf16<BITS>(wo[s])), wos[s]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 4 * q4 + e;
-            at[r * QLD + ct * 16 + r16] = acc[e];
-            if (a.sattn) a.sattn[(own0 + r) * C + ct * 16 + r16] = acc[e];
-        }
-    }
-    lds_barrier();
-
-    // -- mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2 (wave w: row w; lane l:
-    // columns 4l .. 4l+3).
-    {
-        const int r = wave;
-        const bool act = lane < C / 4;
-        const int c0 = 4 * (act ? lane : C / 4 - 1);
-        const size_t o = (own0 + r) * C + c0;
-        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float4 y = ld4(at + r * QLD + c0);
-        float rs = rstd_row<C>(act ? y : z4, a.eps);
-        if (lane == 0 && a.sr1b) a.sr1b[own0 + r] = rs;
-        y = add4(ld4(xs + r * QLD + c0), norm4(y, rs, ld4(nrm + c0)));
-        if (act) st4(a.mid + o, y);
-        rs = rstd_row<C>(act ? y : z4, a.eps);
-        if (lane == 0 && a.sr2) a.sr2[own0 + r] = rs;
-        if (act) st4(a.ln2 + o, norm4(y, rs, ld4(nrm + C + c0)));
+        for (int e = 0; e < 4; ++e) a.attn[(own0 + 4 * q4 + e) * C + ct * 16 + r16] = acc[e];
     }
 }
 
@@ -579,7 +542,12 @@ __device__ __forceinline__ float silu_sigmoid_hw(float z) {
 // ---- loop_mlp_kernel ------------------------------------------------------------------
 // One workgroup of SL / 16 waves per (16 rows, slice of SL SwiGLU columns).
 struct LoopMlpArgs {
-    const float* ln2;        // [M, C]
+    const float* attn;       // [M, C]: this loop's av . wo^T
+    const float* x;          // this loop's x [M, C] (the attention half's residual)
+    const float *n1b, *n2;
+    float* mid;              // output [M, C], stored by the slice-0 workgroups
+    float *sln2, *sr1b, *sr2;   // optional training saves (slice-0 workgroups)
+    float eps;
     const void* Wgu;         // [2F, C] codes of wgate, wup back to back
     const float* Sgu;
     const void* Wd;          // [C, F]
@@ -595,7 +563,7 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
     constexpr int C = 32 * KS, J = C / 64, LDA = C + 8, LDW = SL + 8, FKS = SL / 32;
     constexpr int NW = SL / 16;                 // waves
     constexpr int DPW = (2 * KS + NW - 1) / NW;   // wdown column tiles per wave
-    static_assert(SL % 32 == 0 && NW >= 4, "whole 32-k steps; four waves stage the ln2 rows");
+    static_assert(SL % 32 == 0 && NW >= 4, "whole 32-k steps; four waves run the row chains");
     __shared__ __align__(16) __bf16 Ah[3 * 16 * LDA];
     __shared__ __align__(16) __bf16 Sw[3 * 16 * LDW];
     int b, item;
@@ -606,12 +574,20 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
 
-    // ln2 rows, then the codes: gate / up column tile `wave`, wdown column
-    // tiles wave, wave + NW, ...
-    float4 xv[J];
+    // attn and x rows and the norms (waves 0..3: row 4 wave + q4, lane r16
+    // of the row: columns 4 (r16 + 16 j)), then the codes: gate / up column
+    // tile `wave`, wdown column tiles wave, wave + NW, ...
+    float4 xv[J], xa[J], w1[J], w2[J];
+    const size_t crow = row0 + 4 * wave + q4;
     if (wave < 4) {
 #pragma unroll
-        for (int j = 0; j < J; ++j) xv[j] = ld4(a.ln2 + (row0 + 4 * wave + q4) * C + 4 * (r16 + 16 * j));
+        for (int j = 0; j < J; ++j) {
+            const int c = 4 * (r16 + 16 * j);
+            xv[j] = ld4(a.attn + crow * C + c);
+            xa[j] = ld4(a.x + crow * C + c);
+            w1[j] = ld4(a.n1b + c);
+            w2[j] = ld4(a.n2 + c);
+        }
     }
     const size_t n = size_t(f0 + wave * 16 + r16);
     uint2 gw[KS], uw[KS];
@@ -635,7 +611,34 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
             load_scales<FKS>(a.Sd + size_t(ct * 16 + r16) * fgroups + f0 / 32, dsc[i]);
         }
     }
+    // mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2 (the loop kernels' rstd:
+    // 1 / sqrt(mean(v^2) + eps) with the hardware inverse square root).
     if (wave < 4) {
+        auto rstd = [&](const float4 (&v)[J]) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                ss += v[j].x * v[j].x;
+                ss += v[j].y * v[j].y;
+                ss += v[j].z * v[j].z;
+                ss += v[j].w * v[j].w;
+            }
+            return __builtin_amdgcn_rsqf(row16_sum(ss) * (1.0f / float(C)) + a.eps);
+        };
+        const bool saver = slice == 0;
+        const float rs1 = rstd(xv);
+#pragma unroll
+        for (int j = 0; j < J; ++j) xv[j] = add4(xa[j], norm4(xv[j], rs1, w1[j]));   // mid
+        const float rs2 = rstd(xv);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = 4 * (r16 + 16 * j);
+            if (saver) st4(a.mid + crow * C + c, xv[j]);
+            xv[j] = norm4(xv[j], rs2, w2[j]);                                          // ln2
+            if (saver && a.sln2) st4(a.sln2 + crow * C + c, xv[j]);
+        }
+        if (saver && r16 == 0 && a.sr1b) a.sr1b[crow] = rs1;
+        if (saver && r16 == 0 && a.sr2) a.sr2[crow] = rs2;
 #pragma unroll
         for (int j = 0; j < J; ++j) put4(Ah, 16 * LDA, (4 * wave + q4) * LDA + 4 * (r16 + 16 * j), xv[j]);
     }
@@ -1003,7 +1006,6 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
     // 0 .. D-1, which is all the backward of these shapes reads) or the
     // inference buffers (k, v as [M, D]).
     auto mid_of = [&](int l) { return sv ? sv[l].mid : buf.mid[l & 1]; };
-    auto ln2_of = [&](int l) { return sv ? sv[l].ln2 : buf.ln2; };
     for (int l = 0; l < L; ++l) {
         float* q = sv ? sv[l].q : buf.q;
         float* k = sv ? sv[l].k : buf.k;
@@ -1032,20 +1034,24 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
                            g->stream, ra);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_row");
 
+        // attn: the training save, or (inference) the ln2 buffer, which the
+        // loop shapes do not otherwise use: ln2 lives in the mlp kernel's LDS.
+        float* attn = sv ? sv[l].attn : buf.ln2;
         LoopAttnArgs aa{};
         aa.q = q; aa.k = k; aa.v = v; aa.kv_ld = kv_ld;
-        aa.x = xl;
-        aa.n1b = w->n1b; aa.n2 = w->n2;
         aa.Wo = w->wo.q; aa.So = w->wo.scale;
-        aa.mid = mid_of(l); aa.ln2 = ln2_of(l);
+        aa.attn = attn;
         aa.probs = sv ? sv[l].probs : (l == L - 1 ? buf.probs_last : nullptr);
-        if (sv) { aa.sav = sv[l].av; aa.sattn = sv[l].attn; aa.sr1b = sv[l].r1b; aa.sr2 = sv[l].r2; }
-        aa.B = B; aa.eps = c->eps; aa.scale = 1.0f / sqrtf(float(D));
-        hipLaunchKernelGGL(attn_k, dim3(unsigned(gb * TT)), dim3(1024), size_t(S::BYTES), g->stream, aa);
+        if (sv) aa.sav = sv[l].av;
+        aa.B = B; aa.scale = 1.0f / sqrtf(float(D));
+        hipLaunchKernelGGL(attn_k, dim3(unsigned(gb * TT * 2)), dim3(1024), size_t(S::BYTES), g->stream, aa);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_attn");
 
         LoopMlpArgs ma{};
-        ma.ln2 = ln2_of(l);
+        ma.attn = attn; ma.x = xl; ma.n1b = w->n1b; ma.n2 = w->n2;
+        ma.mid = mid_of(l);
+        if (sv) { ma.sln2 = sv[l].ln2; ma.sr1b = sv[l].r1b; ma.sr2 = sv[l].r2; }
+        ma.eps = c->eps;
         ma.Wgu = w->wgate.q; ma.Sgu = w->wgate.scale;
         ma.Wd = w->wdown.q; ma.Sd = w->wdown.scale;
         ma.part = buf.part;
