@@ -9,11 +9,11 @@
 //    ln1 = rms(x)*n1, and the group's columns of the [wq; wk; wv] projection
 //    (HG query heads, or k | v), with RoPE on q and k and the value residual
 //    on v.
-//  * loop_attn_kernel: two workgroups of 16 waves per (sequence b, 16 query
-//    rows): scores, row softmax and P.V on fp32 MFMA (the stages of
+//  * loop_attn_kernel: four (or two) workgroups of 16 waves per (sequence b,
+//    16 query rows): scores, row softmax and P.V on fp32 MFMA (the stages of
 //    attn_mfma_kernel in dit.hip, every query head against the one KV head),
-//    each workgroup then half of the wo projection's output columns (half of
-//    the wo codes per CU).
+//    each workgroup then a quarter (a half) of the wo projection's output
+//    columns, so each CU receives that share of wo's codes.
 //  * loop_mlp_kernel: one workgroup of SL / 16 waves per (16 rows, slice of SL
 //    SwiGLU columns): the row chain mid = x + rms(attn)*n1b and ln2 =
 //    rms(mid)*n2 of its 16 rows (stored by the slice-0 workgroup), gate and up
@@ -399,6 +399,10 @@ struct AttnShape {
     static constexpr int LDA = C + 8, QLD = C + 4, KLD = D + 4, VLD = T + 4;
     static constexpr int QS = 0, KO = QS + 16 * QLD * 4, VT = KO + T * KLD * 4;
     static constexpr int PS = VT + D * VLD * 4, AV = PS + H * 16 * VLD * 4, BYTES = AV + 3 * 16 * LDA * 2;
+    // Workgroups per (sequence, 16 query rows), each with 2 KS / NWO of wo's
+    // output column tiles (each computes the whole attention).
+    static constexpr int NWO = (2 * KS) % 4 == 0 ? 4 : 2;
+    static_assert(2 * KS / NWO <= 16, "one wo column tile per wave");
     static_assert(KS % 2 == 0 && C % D == 0 && TT >= 1 && C / 4 <= 64, "loop_attn shape");
     static_assert(BYTES <= 160 * 1024, "loop_attn LDS");
 };
@@ -415,20 +419,20 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     float* vt = reinterpret_cast<float*>(lds + S::VT);
     float* ps = reinterpret_cast<float*>(lds + S::PS);
     __bf16* Av = reinterpret_cast<__bf16*>(lds + S::AV);
+    constexpr int NWO = S::NWO, WT = 2 * KS / NWO;   // workgroups per query tile, wo column tiles each
     int b, item;
-    if (!seq_block(a.B, 2 * TT, b, item)) return;
-    const int qt = item >> 1, half = item & 1;   // half: wo's output column tiles [KS half, KS half + KS)
+    if (!seq_block(a.B, NWO * TT, b, item)) return;
+    const int qt = item / NWO, part = item % NWO;   // part: wo's output column tiles [WT part, WT part + WT)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t seq0 = size_t(b) * T, own0 = seq0 + size_t(qt) * 16;
 
     // -- wo codes of this wave's column tile (waves 0 .. KS-1), then q (16
     // rows), k, v (T rows), all issued before any is used.
-    static_assert(KS <= 16, "one wo column tile per wave");
-    const int ct = half * KS + wave;   // this wave's wo column tile when wave < KS
+    const int ct = part * WT + wave;   // this wave's wo column tile when wave < WT
     uint2 wo[KS];
     float wos[KS];
-    if (wave < KS) {
+    if (wave < WT) {
 #pragma unroll
         for (int s = 0; s < KS; ++s) wo[s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, 32 * s + 8 * q4);
         load_scales<KS>(a.So + size_t(ct * 16 + r16) * KS, wos);
@@ -495,7 +499,7 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
         }
         sum = row16_sum(sum);
         const float inv = 1.0f / sum;
-        float* po = a.probs && half == 0 ? a.probs + ((size_t(b) * H + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T
+        float* po = a.probs && part == 0 ? a.probs + ((size_t(b) * H + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T
                                          : nullptr;
 #pragma unroll
         for (int i = 0; i < TT; ++i) {
@@ -514,14 +518,14 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = 4 * q4 + e;
-            if (a.sav && half == 0) a.sav[(own0 + r) * C + col] = acc[e];
+            if (a.sav && part == 0) a.sav[(own0 + r) * C + col] = acc[e];
             put1(Av, 16 * LDA, r * LDA + col, acc[e]);
         }
     }
     lds_barrier();
 
-    // -- attn = av . wo^T, this workgroup's half of the columns.
-    if (wave < KS) {
+    // -- attn = av . wo^T, this workgroup's share of the columns.
+    if (wave < WT) {
         f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < KS; ++s)
@@ -1044,7 +1048,7 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         aa.probs = sv ? sv[l].probs : (l == L - 1 ? buf.probs_last : nullptr);
         if (sv) aa.sav = sv[l].av;
         aa.B = B; aa.scale = 1.0f / sqrtf(float(D));
-        hipLaunchKernelGGL(attn_k, dim3(unsigned(gb * TT * 2)), dim3(1024), size_t(S::BYTES), g->stream, aa);
+        hipLaunchKernelGGL(attn_k, dim3(unsigned(gb * TT * S::NWO)), dim3(1024), size_t(S::BYTES), g->stream, aa);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_attn");
 
         LoopMlpArgs ma{};
