@@ -427,7 +427,7 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t seq0 = size_t(b) * T, own0 = seq0 + size_t(qt) * 16;
 
-    // -- wo codes of this wave's column tile (waves 0 .. KS-1), then q (16
+    // -- wo codes of this wave's column tile (waves 0 .. WT-1), then q (16
     // rows), k, v (T rows), all issued before any is used.
     const int ct = part * WT + wave;   // this wave's wo column tile when wave < WT
     uint2 wo[KS];
