@@ -2,8 +2,10 @@
 // for the block shapes it is built for: int8 / int4 linears with group 32,
 // one KV head, C a multiple of 64, F a multiple of the mlp slice (96 or 128 columns).
 //
-//  * loop_row_kernel: one workgroup of 16 waves per (16 rows, column group);
-//    wave w owns row w. The row chain that closes the previous loop
+//  * loop_row_kernel: one workgroup of 16 waves per (8 rows, column group);
+//    waves 8 .. 15 own a row each, waves 0 .. ntile-1 the group's projection
+//    tiles (16 x 16, the MFMA's other 8 rows computed and dropped). The row
+//    chain that closes the previous loop
 //    (mlp = the previous loop's wdown slabs added in slab order;
 //    pre = mid + rms(mlp)*n2b; x = rms(pre)*nf; loop 0: x = the input), then
 //    ln1 = rms(x)*n1, and the group's columns of the [wq; wk; wv] projection
@@ -65,6 +67,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // so the workspace size does too.
 constexpr int kSlice = 128;
 constexpr int64_t kSliceCus = 256;
+constexpr int kRowTile = 8;           // rows per loop_row_kernel workgroup
 int slice_cols(const dgm_dit_cfg* c) {
     const int64_t tiles = int64_t(c->B) * c->T / 16;
     if (c->F % 96 == 0 && tiles * (c->F / 96) <= kSliceCus && tiles * (c->F / kSlice) < kSliceCus) return 96;
@@ -255,22 +258,39 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
     static_assert(C4 <= 64, "one float4 of the row per lane");
     __shared__ __align__(16) __bf16 Ap[3 * 16 * LDA];
     __shared__ __align__(16) float os[16 * OLD];
+    // kRowTile rows per workgroup: the rows' slab sums are most of what a
+    // workgroup reads, so 8-row tiles (the MFMA's other 8 rows computed and
+    // dropped) halve what each CU receives with twice the workgroups.
+    constexpr int RT = kRowTile;
+    static_assert(2 * DT <= 16 - RT, "the chain waves load no codes");
     int b, item;
-    if (!seq_block(a.B, (a.T / 16) * a.NG, b, item)) return;
+    if (!seq_block(a.B, (a.T / RT) * a.NG, b, item)) return;
     const int g = item % a.NG;
-    const size_t row0 = size_t(b) * a.T + size_t(item / a.NG) * 16;
+    const size_t row0 = size_t(b) * a.T + size_t(item / a.NG) * RT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
     const bool kvg = g == a.NG - 1;
     const int ntile = kvg ? 2 * DT : a.HG * DT;
     const int nbase = kvg ? C : g * a.HG * D;   // first weight row (output column) of the group
 
-    // -- loads: this wave's row (lane l: columns 4l .. 4l+3), then its
-    // projection tile's codes and scales.
-    const size_t row = row0 + wave;
+    // -- loads: waves 0 .. ntile-1 their projection tile's codes and scales;
+    // waves 16-RT .. 15 a row each (lane l: columns 4l .. 4l+3), so no wave
+    // waits for codes before its row chain (vmcnt counts in issue order).
+    const int rw = wave - (16 - RT);   // this wave's row when >= 0
+    const bool chainw = rw >= 0;
+    const size_t row = row0 + (chainw ? rw : 0);
     const bool act = lane < C4;
     const int c0 = 4 * (act ? lane : C4 - 1);
     const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint2 wr[KS];
+    float wsc[KS];
+    if (wave < ntile) {
+        const size_t n = size_t(nbase + wave * 16 + r16);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) wr[s] = codes_at<BITS>(a.Wqkv, n, C, 32 * s + 8 * q4);
+        load_scales<KS>(a.Sqkv + n * KS, wsc);
+    }
+    if (chainw) {
     float4 y, mp, w2, w3;
     if (a.first) {
         y = ld4(a.x + row * C + c0);
@@ -286,14 +306,6 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
         for (int p = 1; p < NP; ++p) y = add4(y, pp[p]);   // slab order
     }
     const float4 w1 = ld4(a.n1 + c0);
-    uint2 wr[KS];
-    float wsc[KS];
-    if (wave < ntile) {
-        const size_t n = size_t(nbase + wave * 16 + r16);
-#pragma unroll
-        for (int s = 0; s < KS; ++s) wr[s] = codes_at<BITS>(a.Wqkv, n, C, 32 * s + 8 * q4);
-        load_scales<KS>(a.Sqkv + n * KS, wsc);
-    }
 
     // -- the row chain (group 0 stores the row outputs), ln1 pieces into LDS.
     const bool saver = g == 0;
@@ -313,7 +325,8 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
     if (saver && a.sr1 && lane == 0) a.sr1[row] = rs;
     const float4 ln = norm4(y, rs, w1);
     if (saver && act && a.sln1) st4(a.sln1 + row * C + c0, ln);
-    if (act) put4(Ap, 16 * LDA, wave * LDA + c0, ln);
+    if (act) put4(Ap, 16 * LDA, rw * LDA + c0, ln);
+    }
     lds_barrier();
 
     // -- the group's projection tiles (wave w: tile w).
@@ -341,7 +354,7 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
         yb = p2 + r2;
     };
     if (!kvg) {
-        const int np = 16 * a.HG * half;
+        const int np = RT * a.HG * half;
         for (int e = threadIdx.x; e < np; e += 1024) {
             const int r = e / (a.HG * half), rem = e - r * (a.HG * half), hh = rem / half, d = rem - hh * half;
             float ya, yb;
@@ -351,7 +364,7 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
             o[d + half] = yb;
         }
     } else {
-        for (int e = threadIdx.x; e < 16 * half; e += 1024) {
+        for (int e = threadIdx.x; e < RT * half; e += 1024) {
             const int r = e / half, d = e - r * half;
             float ya, yb;
             rope(os + r * OLD, r, d, ya, yb);
@@ -361,7 +374,7 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
                 o[h * D + d + half] = yb;
             }
         }
-        for (int e = threadIdx.x; e < 16 * D; e += 1024) {
+        for (int e = threadIdx.x; e < RT * D; e += 1024) {
             const int r = e / D, d = e - r * D;
             float vv = os[r * OLD + D + d];
             float* f = a.vfirst + (row0 + r) * D + d;
@@ -1034,7 +1047,7 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         }
         ra.B = B; ra.T = T; ra.NG = NG; ra.HG = HG;
         ra.eps = c->eps; ra.ca = 1.0f - c->mix; ra.cb = c->mix;
-        hipLaunchKernelGGL((loop_row_kernel<BITS, KS, DT, NP>), dim3(unsigned(gb * TT * NG)), dim3(1024), 0,
+        hipLaunchKernelGGL((loop_row_kernel<BITS, KS, DT, NP>), dim3(unsigned(gb * (T / kRowTile) * NG)), dim3(1024), 0,
                            g->stream, ra);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_row");
 
