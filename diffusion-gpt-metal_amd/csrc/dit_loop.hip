@@ -11,11 +11,13 @@
 //    ln1 = rms(x)*n1, and the group's columns of the [wq; wk; wv] projection
 //    (HG query heads, or k | v), with RoPE on q and k and the value residual
 //    on v.
-//  * loop_attn_kernel: four (or two) workgroups of 16 waves per (sequence b,
-//    16 query rows): scores, row softmax and P.V on fp32 MFMA (the stages of
-//    attn_mfma_kernel in dit.hip, every query head against the one KV head),
-//    each workgroup then a quarter (a half) of the wo projection's output
-//    columns, so each CU receives that share of wo's codes.
+//  * loop_attn_kernel: one workgroup of 16 waves per (sequence b, 16 query
+//    rows, head pair, quarter of wo's output columns): scores, row softmax and
+//    P.V of the pair's two heads on fp32 MFMA (the stages of attn_mfma_kernel
+//    in dit.hip, each query head against the one KV head), then the pair's
+//    share of av . wo^T (its 2D contraction columns) for the quarter's output
+//    columns into the pair's slab; the mlp kernel adds the pairs' slabs in
+//    order.
 //  * loop_mlp_kernel: one workgroup of SL / 16 waves per (16 rows, slice of SL
 //    SwiGLU columns): the row chain mid = x + rms(attn)*n1b and ln2 =
 //    rms(mid)*n2 of its 16 rows (stored by the slice-0 workgroup), gate and up
@@ -399,7 +401,8 @@ struct LoopAttnArgs {
     int kv_ld;
     const void* Wo;          // [C, C]
     const float* So;
-    float* attn;             // output [M, C]: av . wo^T
+    float* attn;             // output [H/2][M][C]: av . wo^T over each head pair's columns
+    int64_t slab;            // M C: floats between the head pairs' partial outputs
     float* probs;            // optional [B, H, T, T]
     float* sav;              // optional training save of av
     int B;
@@ -412,10 +415,11 @@ struct AttnShape {
     static constexpr int LDA = C + 8, QLD = C + 4, KLD = D + 4, VLD = T + 4;
     static constexpr int QS = 0, KO = QS + 16 * QLD * 4, VT = KO + T * KLD * 4;
     static constexpr int PS = VT + D * VLD * 4, AV = PS + H * 16 * VLD * 4, BYTES = AV + 3 * 16 * LDA * 2;
-    // Workgroups per (sequence, 16 query rows), each with 2 KS / NWO of wo's
-    // output column tiles (each computes the whole attention).
-    static constexpr int NWO = (2 * KS) % 4 == 0 ? 4 : 2;
-    static_assert(2 * KS / NWO <= 16, "one wo column tile per wave");
+    // Workgroups per (sequence, 16 query rows): one per (head pair, quarter of
+    // wo's output columns; a half when C/32 is odd).
+    static constexpr int NHG = H / 2, NWH = KS % 2 == 0 ? 4 : 2, NWO = NWH * NHG, KSW = 2 * D / 32;
+    static constexpr int OT = 2 * KS / NWH;   // wo output column tiles per workgroup
+    static_assert(H % 2 == 0 && (2 * D) % 32 == 0 && KS <= 16, "head pairs of whole 32-k steps");
     static_assert(KS % 2 == 0 && C % D == 0 && TT >= 1 && C / 4 <= 64, "loop_attn shape");
     static_assert(BYTES <= 160 * 1024, "loop_attn LDS");
 };
@@ -432,31 +436,38 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     float* vt = reinterpret_cast<float*>(lds + S::VT);
     float* ps = reinterpret_cast<float*>(lds + S::PS);
     __bf16* Av = reinterpret_cast<__bf16*>(lds + S::AV);
-    constexpr int NWO = S::NWO, WT = 2 * KS / NWO;   // workgroups per query tile, wo column tiles each
+    constexpr int NWO = S::NWO, KSW = S::KSW;
     int b, item;
     if (!seq_block(a.B, NWO * TT, b, item)) return;
-    const int qt = item / NWO, part = item % NWO;   // part: wo's output column tiles [WT part, WT part + WT)
+    // Heads h0, h0 + 1 (their contraction columns k0 .. k0 + 2D of wo), wo's
+    // output column tiles wh OT .. wh OT + OT-1.
+    constexpr int NWH = S::NWH, OT = S::OT;
+    const int qt = item / NWO, hg = (item % NWO) / NWH, wh = item % NWH;
+    const int h0 = 2 * hg, k0 = h0 * D;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t seq0 = size_t(b) * T, own0 = seq0 + size_t(qt) * 16;
 
-    // -- wo codes of this wave's column tile (waves 0 .. WT-1), then q (16
-    // rows), k, v (T rows), all issued before any is used.
-    const int ct = part * WT + wave;   // this wave's wo column tile when wave < WT
-    uint2 wo[KS];
-    float wos[KS];
-    if (wave < WT) {
+    // -- wo codes of this wave's column tile over the pair's columns (waves
+    // 0 .. OT-1), then q (16 rows, the pair's columns), k, v (T rows), all
+    // issued before any is used.
+    const int ct = wh * OT + wave;   // this wave's wo column tile when wave < OT
+    uint2 wo[KSW];
+    float wos[KSW];
+    if (wave < OT) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s) wo[s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, 32 * s + 8 * q4);
-        load_scales<KS>(a.So + size_t(ct * 16 + r16) * KS, wos);
+        for (int s = 0; s < KSW; ++s) {
+            wo[s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, k0 + 32 * s + 8 * q4);
+            wos[s] = a.So[size_t(ct * 16 + r16) * KS + k0 / 32 + s];
+        }
     }
-    constexpr int QC = 16 * C / 4, KC = T * D / 4;   // float4 chunks
+    constexpr int QC = 16 * 2 * D / 4, KC = T * D / 4;   // float4 chunks
     constexpr int RQ = (QC + 1023) / 1024, RK = (KC + 1023) / 1024;
     float4 qv[RQ], kv[RK], vv[RK];
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
-        const int e = min(tid + 1024 * i, QC - 1), r = e / (C / 4), c4 = e - r * (C / 4);
-        qv[i] = ld4(a.q + (own0 + r) * C + 4 * c4);
+        const int e = min(tid + 1024 * i, QC - 1), r = e / (2 * D / 4), c4 = e - r * (2 * D / 4);
+        qv[i] = ld4(a.q + (own0 + r) * C + k0 + 4 * c4);
     }
 #pragma unroll
     for (int i = 0; i < RK; ++i) {
@@ -466,8 +477,8 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < RQ; ++i) {
-        const int e = tid + 1024 * i, r = e / (C / 4), c4 = e - r * (C / 4);
-        if (e < QC) st4(qs + r * QLD + 4 * c4, qv[i]);
+        const int e = tid + 1024 * i, r = e / (2 * D / 4), c4 = e - r * (2 * D / 4);
+        if (e < QC) st4(qs + r * QLD + k0 + 4 * c4, qv[i]);
     }
 #pragma unroll
     for (int i = 0; i < RK; ++i) {
@@ -482,19 +493,20 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     }
     lds_barrier();
 
-    // -- scores = (q . k) * scale per (head, 16 keys).
-    for (int tile = wave; tile < H * TT; tile += 16) {
-        const int h = tile / TT, kt = tile - h * TT;
-        const f32x4 acc = dot_tile(qs + r16 * QLD + h * D + 4 * q4, ks + (kt * 16 + r16) * KLD + 4 * q4, D);
+    // -- scores = (q . k) * scale per (head of the pair, 16 keys).
+    for (int tile = wave; tile < 2 * TT; tile += 16) {
+        const int hl = tile / TT, kt = tile - hl * TT;
+        const f32x4 acc =
+            dot_tile(qs + r16 * QLD + (h0 + hl) * D + 4 * q4, ks + (kt * 16 + r16) * KLD + 4 * q4, D);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ps[(h * 16 + 4 * q4 + e) * VLD + kt * 16 + r16] = acc[e] * a.scale;
+        for (int e = 0; e < 4; ++e) ps[(hl * 16 + 4 * q4 + e) * VLD + kt * 16 + r16] = acc[e] * a.scale;
     }
     lds_barrier();
 
     // -- row softmax, 16 lanes per (head, query row): attn_softmax's max, sum
     // of exp and normalize (each exp computed once, on the hardware 2^x: the
     // library expf made this phase VALU-bound with 16 waves on 4 SIMDs).
-    for (int rr = 4 * wave + q4; rr < H * 16; rr += 64) {
+    for (int rr = 4 * wave + q4; rr < 2 * 16; rr += 64) {
         float* rp = ps + rr * VLD;
         float ev[TT];
         float mx = -INFINITY;
@@ -512,8 +524,9 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
         }
         sum = row16_sum(sum);
         const float inv = 1.0f / sum;
-        float* po = a.probs && part == 0 ? a.probs + ((size_t(b) * H + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T
-                                         : nullptr;
+        float* po = a.probs && wh == 0
+                        ? a.probs + ((size_t(b) * H + h0 + (rr >> 4)) * T + qt * 16 + (rr & 15)) * T
+                        : nullptr;
 #pragma unroll
         for (int i = 0; i < TT; ++i) {
             const float pv = ev[i] * inv;
@@ -523,28 +536,31 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     }
     lds_barrier();
 
-    // -- av = P.V per (head, 16 columns), kept as bf16 pieces for wo.
-    for (int tile = wave; tile < H * DT; tile += 16) {
-        const int h = tile / DT, dt = tile - h * DT;
-        const f32x4 acc = dot_tile(ps + (h * 16 + r16) * VLD + 4 * q4, vt + (dt * 16 + r16) * VLD + 4 * q4, T);
-        const int col = h * D + dt * 16 + r16;
+    // -- av = P.V per (head of the pair, 16 columns), kept as bf16 pieces
+    // (the pair's 2D columns) for wo.
+    for (int tile = wave; tile < 2 * DT; tile += 16) {
+        const int hl = tile / DT, dt = tile - hl * DT;
+        const f32x4 acc = dot_tile(ps + (hl * 16 + r16) * VLD + 4 * q4, vt + (dt * 16 + r16) * VLD + 4 * q4, T);
+        const int col = hl * D + dt * 16 + r16;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = 4 * q4 + e;
-            if (a.sav && part == 0) a.sav[(own0 + r) * C + col] = acc[e];
+            if (a.sav && wh == 0) a.sav[(own0 + r) * C + k0 + col] = acc[e];
             put1(Av, 16 * LDA, r * LDA + col, acc[e]);
         }
     }
     lds_barrier();
 
-    // -- attn = av . wo^T, this workgroup's share of the columns.
-    if (wave < WT) {
+    // -- the pair's share of attn = av . wo^T (its 2D contraction columns)
+    // for this workgroup's output columns, into head-pair slab hg.
+    if (wave < OT) {
         f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KSW; ++s)
             acc = scale_add(acc, step3(Av + r16 * LDA + 32 * s + 8 * q4, 16 * LDA, codes_bf16<BITS>(wo[s])), wos[s]);
+        float* o = a.attn + hg * a.slab;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a.attn[(own0 + 4 * q4 + e) * C + ct * 16 + r16] = acc[e];
+        for (int e = 0; e < 4; ++e) o[(own0 + 4 * q4 + e) * C + ct * 16 + r16] = acc[e];
     }
 }
 
@@ -559,7 +575,10 @@ __device__ __forceinline__ float silu_sigmoid_hw(float z) {
 // ---- loop_mlp_kernel ------------------------------------------------------------------
 // One workgroup of SL / 16 waves per (16 rows, slice of SL SwiGLU columns).
 struct LoopMlpArgs {
-    const float* attn;       // [M, C]: this loop's av . wo^T
+    const float* attn;       // [NHG][M][C]: this loop's av . wo^T per head pair (summed in order here)
+    int64_t slab;            // M C
+    int nhg;
+    float* sattn;            // optional training save of the sum (slice-0 workgroups)
     const float* x;          // this loop's x [M, C] (the attention half's residual)
     const float *n1b, *n2;
     float* mid;              // output [M, C], stored by the slice-0 workgroups
@@ -601,6 +620,7 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
         for (int j = 0; j < J; ++j) {
             const int c = 4 * (r16 + 16 * j);
             xv[j] = ld4(a.attn + crow * C + c);
+            for (int h = 1; h < a.nhg; ++h) xv[j] = add4(xv[j], ld4(a.attn + h * a.slab + crow * C + c));   // pair order
             xa[j] = ld4(a.x + crow * C + c);
             w1[j] = ld4(a.n1b + c);
             w2[j] = ld4(a.n2 + c);
@@ -643,6 +663,10 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
             return __builtin_amdgcn_rsqf(row16_sum(ss) * (1.0f / float(C)) + a.eps);
         };
         const bool saver = slice == 0;
+        if (saver && a.sattn) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) st4(a.sattn + crow * C + 4 * (r16 + 16 * j), xv[j]);
+        }
         const float rs1 = rstd(xv);
 #pragma unroll
         for (int j = 0; j < J; ++j) xv[j] = add4(xa[j], norm4(xv[j], rs1, w1[j]));   // mid
@@ -1051,13 +1075,12 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
                            g->stream, ra);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_row");
 
-        // attn: the training save, or (inference) the ln2 buffer, which the
-        // loop shapes do not otherwise use: ln2 lives in the mlp kernel's LDS.
-        float* attn = sv ? sv[l].attn : buf.ln2;
+        // The head pairs' partial attn slabs follow the wdown slabs.
+        float* attn = buf.part + int64_t(NP) * M * C;
         LoopAttnArgs aa{};
         aa.q = q; aa.k = k; aa.v = v; aa.kv_ld = kv_ld;
         aa.Wo = w->wo.q; aa.So = w->wo.scale;
-        aa.attn = attn;
+        aa.attn = attn; aa.slab = int64_t(M) * C;
         aa.probs = sv ? sv[l].probs : (l == L - 1 ? buf.probs_last : nullptr);
         if (sv) aa.sav = sv[l].av;
         aa.B = B; aa.scale = 1.0f / sqrtf(float(D));
@@ -1065,7 +1088,8 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         DGM_LAUNCH_CHECK(g, "dit_forward loop_attn");
 
         LoopMlpArgs ma{};
-        ma.attn = attn; ma.x = xl; ma.n1b = w->n1b; ma.n2 = w->n2;
+        ma.attn = attn; ma.slab = int64_t(M) * C; ma.nhg = S::NHG; ma.x = xl; ma.n1b = w->n1b; ma.n2 = w->n2;
+        if (sv) ma.sattn = sv[l].attn;
         ma.mid = mid_of(l);
         if (sv) { ma.sln2 = sv[l].ln2; ma.sr1b = sv[l].r1b; ma.sr2 = sv[l].r2; }
         ma.eps = c->eps;
@@ -1146,9 +1170,10 @@ bool dit_loop_shape_ok(const dgm_dit_cfg* c) {
     return shape_built(c);
 }
 
+// The wdown slabs (F / SL) and the attention's head-pair slabs (H / 2).
 int64_t dit_loop_part_floats(const dgm_dit_cfg* c) {
     if (!dit_loop_shape_ok(c)) return 0;
-    return int64_t(c->F / slice_cols(c)) * c->B * c->T * c->C;
+    return int64_t(c->F / slice_cols(c) + c->H / 2) * c->B * c->T * c->C;
 }
 
 bool dit_loop_ok(const dgm_dit_cfg* c, const dgm_dit_weights* w) {
