@@ -574,10 +574,12 @@ __device__ __forceinline__ float silu_sigmoid_hw(float z) {
 
 // ---- loop_mlp_kernel ------------------------------------------------------------------
 // One workgroup of SL / 16 waves per (16 rows, slice of SL SwiGLU columns).
+// NHG (head pairs, the attention slabs to add) is a compile-time count, so
+// that every slab load of a row is issued before the first add waits (a
+// run-time count compiled to a loop that waited for each load in turn).
 struct LoopMlpArgs {
     const float* attn;       // [NHG][M][C]: this loop's av . wo^T per head pair (summed in order here)
     int64_t slab;            // M C
-    int nhg;
     float* sattn;            // optional training save of the sum (slice-0 workgroups)
     const float* x;          // this loop's x [M, C] (the attention half's residual)
     const float *n1b, *n2;
@@ -593,7 +595,7 @@ struct LoopMlpArgs {
     int B, TT, M, F, P;
 };
 
-template <int BITS, int KS, int SL>
+template <int BITS, int KS, int SL, int NHG>
 __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
 #pragma clang fp contract(off)
     constexpr int C = 32 * KS, J = C / 64, LDA = C + 8, LDW = SL + 8, FKS = SL / 32;
@@ -620,7 +622,8 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
         for (int j = 0; j < J; ++j) {
             const int c = 4 * (r16 + 16 * j);
             xv[j] = ld4(a.attn + crow * C + c);
-            for (int h = 1; h < a.nhg; ++h) xv[j] = add4(xv[j], ld4(a.attn + h * a.slab + crow * C + c));   // pair order
+#pragma unroll
+            for (int h = 1; h < NHG; ++h) xv[j] = add4(xv[j], ld4(a.attn + h * a.slab + crow * C + c));   // pair order
             xa[j] = ld4(a.x + crow * C + c);
             w1[j] = ld4(a.n1b + c);
             w2[j] = ld4(a.n2 + c);
@@ -1088,7 +1091,7 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         DGM_LAUNCH_CHECK(g, "dit_forward loop_attn");
 
         LoopMlpArgs ma{};
-        ma.attn = attn; ma.slab = int64_t(M) * C; ma.nhg = S::NHG; ma.x = xl; ma.n1b = w->n1b; ma.n2 = w->n2;
+        ma.attn = attn; ma.slab = int64_t(M) * C; ma.x = xl; ma.n1b = w->n1b; ma.n2 = w->n2;
         if (sv) ma.sattn = sv[l].attn;
         ma.mid = mid_of(l);
         if (sv) { ma.sln2 = sv[l].ln2; ma.sr1b = sv[l].r1b; ma.sr2 = sv[l].r2; }
@@ -1098,7 +1101,7 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         ma.part = buf.part;
         if (sv) { ma.sgate = sv[l].gate; ma.sup = sv[l].up; ma.ssw = sv[l].sw; }
         ma.B = B; ma.TT = TT; ma.M = M; ma.F = c->F; ma.P = NP;
-        hipLaunchKernelGGL((loop_mlp_kernel<BITS, KS, SL>), dim3(unsigned(gb * TT * NP)), dim3(4 * SL), 0, g->stream,
+        hipLaunchKernelGGL((loop_mlp_kernel<BITS, KS, SL, S::NHG>), dim3(unsigned(gb * TT * NP)), dim3(4 * SL), 0, g->stream,
                            ma);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_mlp");
     }
