@@ -42,13 +42,15 @@ extern "C" {
 
 /* ---- math modes (dgm_set_math) ------------------------------------------ */
 /* FP32 (default): every result is within max relative error 1e-5 of the
- * float64 product. Quantized forwards of a few rows (M <= 4) run on int8
- * MFMA over an exact split of the activations into four int8 pieces against
- * a power of two per row and k-range (2^-27 of its maximum); up to M = 64 on
- * f16 MFMA over two f16 pieces per activation against a power of two per
- * (row, 128-k block) (2^-22 of each element); the rest accumulate fp32
- * products of fp32 operands.
- * BF16: the few-row kernels take two int8 pieces; up to M = 64, int4 codes
+ * float64 product. Quantized forwards of a few rows (M <= 4, and up to
+ * M = 16 for weights large enough to split K over the CUs) run on int8 MFMA
+ * over an exact split of the activations into four int8 pieces against a
+ * power of two per row and k-range (2^-27 of its maximum); other forwards up
+ * to M = 64 on f16 MFMA over two f16 pieces per activation against a power
+ * of two per (row, 128-k block) (2^-22 of each element); the rest accumulate
+ * fp32 products of fp32 operands.
+ * BF16: the int8-piece kernels take two pieces (up to M = 8 when K is
+ * split); otherwise up to M = 64, int4 codes
  * meet bf16(x) and int8 codes one f16 piece; larger M (with K % 128 == 0 and
  * qGroup % 32 == 0) runs on bf16 MFMA with activations rounded to bf16 and
  * weights dequantized to bf16 in LDS, fp32 accumulate. Max relative error

@@ -1,8 +1,9 @@
 """GPU parity of the decode-shaped (M <= 64) quantized forward: gemm_nt_i4 /
 gemm_nt_i8 (metal/kernels.metal:152-209) through dgm_gemmNT, whichever kernel
 the library routes the shape to: the streaming int8-MFMA kernel (a few rows
-whose activation pieces fit LDS, gemm_stream.hip), the int8-MFMA skinny
-kernel (other shapes of up to 3 rows, and shapes outside the decode kernels'
+whose activation pieces fit LDS, gemm_stream.hip), the K-sliced int8-MFMA
+kernel (up to 16 rows of weights large enough to split K over the CUs,
+gemm_slab.hip), the int8-MFMA skinny kernel (other shapes of up to 3 rows, and shapes outside the decode kernels'
 domain, gemm_skinny.hip), or the f16 / bf16 decode kernels (4 <= M <= 64,
 gemm_decode.hip).
 
