@@ -250,10 +250,11 @@ struct LoopRowArgs {
     float *sln1, *sr1, *pmlp, *ppre, *pr2b, *prf;
     int B, T, NG, HG;
     float eps, ca, cb;
-    int first;
 };
 
-template <int BITS, int KS, int DT, int NP>
+// FIRST: the first loop (x from the input, v stored as the value residual);
+// a compile-time flag, so that no branch splits the row loads into rounds.
+template <int BITS, int KS, int DT, int NP, bool FIRST>
 __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
 #pragma clang fp contract(off)
     constexpr int C = 32 * KS, D = 16 * DT, C4 = C / 4, LDA = C + 8, OLD = 2 * D + 4;
@@ -293,8 +294,9 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
         load_scales<KS>(a.Sqkv + n * KS, wsc);
     }
     if (chainw) {
+    const float4 w1 = ld4(a.n1 + c0);
     float4 y, mp, w2, w3;
-    if (a.first) {
+    if constexpr (FIRST) {
         y = ld4(a.x + row * C + c0);
     } else {
         float4 pp[NP];
@@ -307,12 +309,11 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
 #pragma unroll
         for (int p = 1; p < NP; ++p) y = add4(y, pp[p]);   // slab order
     }
-    const float4 w1 = ld4(a.n1 + c0);
 
     // -- the row chain (group 0 stores the row outputs), ln1 pieces into LDS.
     const bool saver = g == 0;
     float rs;
-    if (!a.first) {
+    if constexpr (!FIRST) {
         rs = rstd_row<C>(act ? y : z4, a.eps);   // rms(mlp)
         if (saver && act && a.pmlp) st4(a.pmlp + row * C + c0, y);
         if (saver && a.pr2b && lane == 0) a.pr2b[row] = rs;
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(1024) void loop_row_kernel(LoopRowArgs a) {
             const int r = e / D, d = e - r * D;
             float vv = os[r * OLD + D + d];
             float* f = a.vfirst + (row0 + r) * D + d;
-            if (a.first) {
+            if constexpr (FIRST) {
                 *f = vv;
             } else {
                 const float pa = a.ca * vv;
@@ -1058,7 +1059,6 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         float* xl = sv ? sv[l].x : x;   // this loop's x, the residual of its attention half
 
         LoopRowArgs ra{};
-        ra.first = l == 0;
         ra.x = x;
         ra.part = buf.part;
         ra.mid_prev = l > 0 ? mid_of(l - 1) : nullptr;
@@ -1074,8 +1074,9 @@ int run_loops(dgm_gpu* g, const dgm_dit_cfg* c, const dgm_dit_weights* w, const 
         }
         ra.B = B; ra.T = T; ra.NG = NG; ra.HG = HG;
         ra.eps = c->eps; ra.ca = 1.0f - c->mix; ra.cb = c->mix;
-        hipLaunchKernelGGL((loop_row_kernel<BITS, KS, DT, NP>), dim3(unsigned(gb * (T / kRowTile) * NG)), dim3(1024), 0,
-                           g->stream, ra);
+        const dim3 rgrid(unsigned(gb * (T / kRowTile) * NG));
+        if (l == 0) hipLaunchKernelGGL((loop_row_kernel<BITS, KS, DT, NP, true>), rgrid, dim3(1024), 0, g->stream, ra);
+        else hipLaunchKernelGGL((loop_row_kernel<BITS, KS, DT, NP, false>), rgrid, dim3(1024), 0, g->stream, ra);
         DGM_LAUNCH_CHECK(g, "dit_forward loop_row");
 
         // The head pairs' partial attn slabs follow the wdown slabs.
