@@ -449,19 +449,11 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t seq0 = size_t(b) * T, own0 = seq0 + size_t(qt) * 16;
 
-    // -- wo codes of this wave's column tile over the pair's columns (waves
-    // 0 .. OT-1), then q (16 rows, the pair's columns), k, v (T rows), all
-    // issued before any is used.
-    const int ct = wh * OT + wave;   // this wave's wo column tile when wave < OT
-    uint2 wo[KSW];
-    float wos[KSW];
-    if (wave < OT) {
-#pragma unroll
-        for (int s = 0; s < KSW; ++s) {
-            wo[s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, k0 + 32 * s + 8 * q4);
-            wos[s] = a.So[size_t(ct * 16 + r16) * KS + k0 / 32 + s];
-        }
-    }
+    // -- q (16 rows, the pair's columns), k, v (T rows), staged in LDS; the
+    // wo codes of this wave's column tile over the pair's columns (waves
+    // 0 .. OT-1) are issued after the staging, so that it does not wait for
+    // them (a wave waits for its loads in issue order): they are needed only
+    // by the last phase.
     constexpr int QC = 16 * 2 * D / 4, KC = T * D / 4;   // float4 chunks
     constexpr int RQ = (QC + 1023) / 1024, RK = (KC + 1023) / 1024;
     float4 qv[RQ], kv[RK], vv[RK];
@@ -490,6 +482,16 @@ __global__ __launch_bounds__(1024) void loop_attn_kernel(LoopAttnArgs a) {
             vt[(4 * c4 + 1) * VLD + t] = vv[i].y;
             vt[(4 * c4 + 2) * VLD + t] = vv[i].z;
             vt[(4 * c4 + 3) * VLD + t] = vv[i].w;
+        }
+    }
+    const int ct = wh * OT + wave;   // this wave's wo column tile when wave < OT
+    uint2 wo[KSW];
+    float wos[KSW];
+    if (wave < OT) {
+#pragma unroll
+        for (int s = 0; s < KSW; ++s) {
+            wo[s] = codes_at<BITS>(a.Wo, size_t(ct * 16 + r16), C, k0 + 32 * s + 8 * q4);
+            wos[s] = a.So[size_t(ct * 16 + r16) * KS + k0 / 32 + s];
         }
     }
     lds_barrier();
