@@ -618,15 +618,16 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
     // attn and x rows and the norms (waves 0..3: row 4 wave + q4, lane r16
     // of the row: columns 4 (r16 + 16 j)), then the codes: gate / up column
     // tile `wave`, wdown column tiles wave, wave + NW, ...
-    float4 xv[J], xa[J], w1[J], w2[J];
+    // The slabs are added only after the codes' loads are issued: adding
+    // them first would hold those loads until the first slabs had landed.
+    float4 xv[J], xs[NHG][J], xa[J], w1[J], w2[J];
     const size_t crow = row0 + 4 * wave + q4;
     if (wave < 4) {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int c = 4 * (r16 + 16 * j);
-            xv[j] = ld4(a.attn + crow * C + c);
 #pragma unroll
-            for (int h = 1; h < NHG; ++h) xv[j] = add4(xv[j], ld4(a.attn + h * a.slab + crow * C + c));   // pair order
+            for (int h = 0; h < NHG; ++h) xs[h][j] = ld4(a.attn + h * a.slab + crow * C + c);
             xa[j] = ld4(a.x + crow * C + c);
             w1[j] = ld4(a.n1b + c);
             w2[j] = ld4(a.n2 + c);
@@ -657,6 +658,12 @@ __global__ __launch_bounds__(4 * SL) void loop_mlp_kernel(LoopMlpArgs a) {
     // mid = x + rms(attn) * n1b; ln2 = rms(mid) * n2 (the loop kernels' rstd:
     // 1 / sqrt(mean(v^2) + eps) with the hardware inverse square root).
     if (wave < 4) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            xv[j] = xs[0][j];
+#pragma unroll
+            for (int h = 1; h < NHG; ++h) xv[j] = add4(xv[j], xs[h][j]);   // pair order
+        }
         auto rstd = [&](const float4 (&v)[J]) {
             float ss = 0.0f;
 #pragma unroll
